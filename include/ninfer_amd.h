@@ -1,0 +1,231 @@
+/*
+ * ninfer_amd — C ABI of the MI355X (gfx950) MTP speculative-decoding verify step.
+ *
+ * Every entry point validates its arguments on the host before any launch, returns an
+ * nmi_status, and launches only hand-written gfx950 kernels on the caller's stream. Nothing
+ * allocates device memory, synchronizes, or reads device memory back: state scalars (length,
+ * token, commit counts) and sampling parameters are device-resident, so every call can be
+ * captured in a HIP graph and replayed. Transient storage is a caller-owned region sized by the
+ * matching *_workspace_bytes query (the reference's WorkspaceArena contract).
+ *
+ * Tensors use the reference's non-owning view (src/core/tensor.h:11-28): a data pointer, a dtype,
+ * ne[4] element counts (ne[0] fastest) and nb[4] byte strides. The C++ drop-in layer in
+ * include/ninfer_amd/ops.hpp turns statuses back into the reference's exceptions
+ * (std::invalid_argument / std::overflow_error).
+ *
+ * Reference: Neroued/ninfer, include/ninfer/ops/{gqa_attention,argmax,sampling,
+ * speculative_round,kv_cache_append_prefix}.h. Entries marked EXTENSION have no reference symbol.
+ */
+#ifndef NINFER_AMD_H
+#define NINFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same object as hipStream_t (0 = the null stream). */
+typedef struct ihipStream_t* nmi_stream_t;
+
+typedef enum nmi_status {
+    NMI_OK = 0,
+    NMI_INVALID_ARGUMENT = 1, /* reference: std::invalid_argument */
+    NMI_OVERFLOW = 2,         /* reference: std::overflow_error */
+    NMI_HIP_ERROR = 3,        /* launch failure (reference: CUDA_CHECK abort, src/core/device.cu:38-43) */
+    NMI_UNSUPPORTED = 4       /* valid request outside the built kernel set */
+} nmi_status;
+
+/* src/core/dtype.h */
+typedef enum nmi_dtype {
+    NMI_BF16 = 0,
+    NMI_FP16 = 1,
+    NMI_FP32 = 2,
+    NMI_I8 = 3,
+    NMI_I32 = 4,
+    NMI_I64 = 5
+} nmi_dtype;
+
+/* src/core/tensor.h:11-15 */
+typedef struct nmi_tensor {
+    void* data;
+    int32_t dtype; /* nmi_dtype */
+    int32_t ne[4];
+    int64_t nb[4];
+} nmi_tensor;
+
+/* src/core/kv_cache.h:13-24. INT8-G64: k/v are I8 [D, P, Hkv] (or [D, P, Hkv, B] for a batch of
+ * sequences), k_scale/v_scale FP16 [D/64, P, Hkv(, B)], P = padded_context = align_up(max, 128). */
+typedef struct nmi_kv_layer_view {
+    nmi_tensor k;
+    nmi_tensor v;
+    nmi_tensor k_scale;
+    nmi_tensor v_scale;
+    uint32_t max_context;
+    uint32_t padded_context;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t dtype; /* NMI_I8 (INT8-G64) or NMI_BF16 */
+    int32_t quant_group;
+} nmi_kv_layer_view;
+
+/* include/ninfer/ops/gqa_attention.h:13-16 */
+typedef struct nmi_gqa_envelope {
+    uint32_t min_visible_keys;
+    uint32_t max_visible_keys;
+} nmi_gqa_envelope;
+
+/* include/ninfer/ops/sampling.h:24-33 — binary-identical device-resident layout (40 bytes). */
+typedef struct nmi_sampling_config {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float min_p;
+    float presence_penalty;
+    float frequency_penalty;
+    unsigned long long seed;
+    int32_t* token_counts;
+} nmi_sampling_config;
+
+/* include/ninfer/ops/kv_cache_append_prefix.h:18-21 */
+typedef struct nmi_commit_envelope {
+    uint32_t min_count;
+    uint32_t max_count;
+} nmi_commit_envelope;
+
+/* EXTENSION: device-resident parameters of the general (Mode F) acceptance. */
+typedef struct nmi_general_config {
+    float temperature;
+    float top_p;
+} nmi_general_config;
+
+/* Thread-local text of the last non-OK status. */
+const char* nmi_last_error(void);
+/* Library build identification (architecture list and kernel set). */
+const char* nmi_build_info(void);
+
+/* ---------------------------------------------------------------- verify attention (part a, c) */
+
+/* Replaces gqa_attention_workspace_bytes (include/ninfer/ops/gqa_attention.h:50). The split-K
+ * partial count depends on the geometry and on the envelope's max_visible_keys, so both are
+ * inputs here. batch = number of sequences (q.ne[3]). */
+size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                         int32_t tokens, int32_t batch,
+                                         uint32_t max_visible_keys);
+
+/* A1, replaces gqa_attention (include/ninfer/ops/gqa_attention.h:71-73): quantize-append the T
+ * new K/V columns at rows positions[t] and compute causal GQA over rows [0, positions[t]].
+ * q/out BF16 [D, Hq, T(, B)]; k/v BF16 [D, Hkv, T(, B)]; positions I32 [T(, B)] sequential;
+ * out may also be FP32 (EXTENSION). */
+int nmi_gqa_attention(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                      const nmi_tensor* positions, float scale, const nmi_kv_layer_view* cache,
+                      nmi_gqa_envelope envelope, void* workspace, size_t workspace_bytes,
+                      nmi_tensor* out, nmi_stream_t stream);
+
+/* A2, replaces gqa_kv_append (include/ninfer/ops/gqa_attention.h:80-81). */
+int nmi_gqa_kv_append(const nmi_tensor* k, const nmi_tensor* v, const nmi_tensor* positions,
+                      const nmi_kv_layer_view* cache, nmi_stream_t stream);
+
+/* A3, replaces gqa_attention_cached (include/ninfer/ops/gqa_attention.h:89-91). */
+int nmi_gqa_attention_cached(const nmi_tensor* q, const nmi_tensor* positions, float scale,
+                             const nmi_kv_layer_view* cache, nmi_gqa_envelope envelope,
+                             void* workspace, size_t workspace_bytes, nmi_tensor* out,
+                             nmi_stream_t stream);
+
+/* EXTENSION (tree verification): A1/A3 with an ancestor mask. parents I32 [T(, B)], parents[0] =
+ * -1, parents[u] < u. Node u occupies row positions[u]; query t sees history rows
+ * [0, positions[0]) and the new rows of its ancestors-or-self. write_cache = 0 gives A3
+ * (k and v may then be NULL). */
+int nmi_gqa_attention_tree(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                           const nmi_tensor* positions, const nmi_tensor* parents, float scale,
+                           const nmi_kv_layer_view* cache, nmi_gqa_envelope envelope,
+                           int32_t write_cache, void* workspace, size_t workspace_bytes,
+                           nmi_tensor* out, nmi_stream_t stream);
+
+/* ---------------------------------------------------------------- acceptance (part b) */
+
+/* Replaces argmax (include/ninfer/ops/argmax.h:21): out[t] = min argmax_{v < valid_rows}
+ * float(logits[v, t]). logits BF16 [physical_rows, C(, B)], out I32 [C(, B)]. */
+int nmi_argmax(const nmi_tensor* logits, nmi_tensor* out, int32_t valid_rows,
+               nmi_stream_t stream);
+
+/* Replaces sampling_workspace_bytes (include/ninfer/ops/sampling.h:37). batch = sequences. */
+size_t nmi_sampling_workspace_bytes(int32_t token_domain, int32_t columns, int32_t batch);
+
+/* Replaces speculative_prepare_verify_inputs (include/ninfer/ops/speculative_round.h:29-31). */
+int nmi_speculative_prepare_verify_inputs(const nmi_tensor* token, const nmi_tensor* drafts,
+                                          const nmi_tensor* length, nmi_tensor* verify_ids,
+                                          nmi_tensor* positions, nmi_stream_t stream);
+
+/* Replaces speculative_accept_greedy_drafts (include/ninfer/ops/speculative_round.h:68-73):
+ * greedy (config->temperature <= 0) or reference stochastic acceptance with the top-20 candidate
+ * cap ("Mode R"). `config` is a DEVICE pointer. EXTENSION: a trailing batch dimension
+ * (drafts I32 [K, B], logits BF16 [rows, K+1, B], scalars I32 [B], stats I64 [4+K, B]). */
+int nmi_speculative_accept_greedy_drafts(const nmi_tensor* target_tokens, const nmi_tensor* logits,
+                                         const nmi_tensor* drafts, nmi_tensor* length,
+                                         nmi_tensor* token, nmi_tensor* sampled_out,
+                                         nmi_tensor* num_sampled, nmi_tensor* accepted,
+                                         nmi_tensor* stats, int32_t token_domain,
+                                         const nmi_sampling_config* config, void* workspace,
+                                         size_t workspace_bytes, nmi_stream_t stream);
+
+/* EXTENSION ("Mode F"): general speculative acceptance with full-vocabulary temperature and
+ * top-p for both the target columns (logits BF16 [rows, K+1(, B)]) and the draft columns
+ * (draft_logits BF16 [rows, K(, B)]). Accept draft i iff u_accept[i] * q_i(d_i) < p_i(d_i);
+ * on the first rejection sample max(0, p_i - q_i) normalized with u_residual; if all K are
+ * accepted sample column K with u_accept[K]. uniforms: u_accept FP32 [K+1(, B)],
+ * u_residual FP32 [1(, B)]. Probabilities are 64-bit fixed point (bit-exact, order-free).
+ * `config` is a DEVICE pointer. */
+size_t nmi_general_accept_workspace_bytes(int32_t token_domain, int32_t K, int32_t batch);
+int nmi_speculative_accept_general(const nmi_tensor* logits, const nmi_tensor* draft_logits,
+                                   const nmi_tensor* drafts, const nmi_tensor* u_accept,
+                                   const nmi_tensor* u_residual, nmi_tensor* length,
+                                   nmi_tensor* token, nmi_tensor* sampled_out,
+                                   nmi_tensor* num_sampled, nmi_tensor* accepted,
+                                   nmi_tensor* stats, int32_t token_domain,
+                                   const nmi_general_config* config, void* workspace,
+                                   size_t workspace_bytes, nmi_stream_t stream);
+
+/* Replaces speculative_select_accepted_hidden (include/ninfer/ops/speculative_round.h:86-87). */
+int nmi_speculative_select_accepted_hidden(const nmi_tensor* hidden, const nmi_tensor* accepted,
+                                           nmi_tensor* out, nmi_stream_t stream);
+
+/* ---------------------------------------------------------------- commit / rollback (part c) */
+
+/* Replaces kv_cache_append_prefix (include/ninfer/ops/kv_cache_append_prefix.h:34-37) and
+ * extends it to INT8-G64 caches: columns i < *commit_count are quantized (INT8) or copied (BF16)
+ * into row positions[i]; no byte of a rejected column is written. */
+int nmi_kv_cache_append_prefix(const nmi_tensor* k, const nmi_tensor* v,
+                               const nmi_tensor* positions, const nmi_tensor* commit_count,
+                               nmi_commit_envelope envelope, const nmi_kv_layer_view* cache,
+                               nmi_stream_t stream);
+
+/* EXTENSION: explicit rollback — zero codes and scales of rows positions[i] for
+ * i in [*keep_count, T). */
+int nmi_kv_cache_rollback(const nmi_tensor* positions, const nmi_tensor* keep_count,
+                          const nmi_kv_layer_view* cache, nmi_stream_t stream);
+
+/* EXTENSION (tree verification): move rows base + path[j] to base + j for j < *path_len, where
+ * base = *base_position (device I32 scalar), path I32 [T] strictly increasing with path[j] >= j.
+ * Codes and scales are copied bit-exactly. */
+int nmi_kv_cache_compact_path(const nmi_tensor* base_position, const nmi_tensor* path,
+                              const nmi_tensor* path_len, const nmi_kv_layer_view* cache,
+                              nmi_stream_t stream);
+
+/* EXTENSION (tree verification): greedy longest accepted root-to-leaf chain and commit.
+ * parents I32 [N], node_tokens I32 [N] (node 0 = the current token), target_tokens I32 [N]
+ * (argmax per node). Writes path I32 [N] (first *path_len entries valid), sampled_out I32 [N]
+ * (path tokens then the correction/bonus token, zero padded), num_sampled, accepted, advances
+ * length by accepted+1, sets token, and updates stats like the chain case. */
+int nmi_tree_accept_greedy(const nmi_tensor* parents, const nmi_tensor* node_tokens,
+                           const nmi_tensor* target_tokens, nmi_tensor* path, nmi_tensor* path_len,
+                           nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,
+                           nmi_tensor* num_sampled, nmi_tensor* accepted, nmi_tensor* stats,
+                           nmi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NINFER_AMD_H */

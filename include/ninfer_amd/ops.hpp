@@ -1,0 +1,291 @@
+// C++20 drop-in layer over the ninfer_amd C ABI: the reference's ninfer::ops signatures
+// (include/ninfer/ops/{gqa_attention,argmax,sampling,speculative_round,kv_cache_append_prefix}.h)
+// with hipStream_t in place of cudaStream_t. Statuses become the reference's exceptions:
+// std::invalid_argument, std::overflow_error, std::runtime_error (launch failure).
+//
+// Header-only; link against ninfer_amd/libninfer_amd.so.
+#pragma once
+
+#include "ninfer_amd.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <initializer_list>
+#include <stdexcept>
+#include <string>
+
+namespace ninfer_amd {
+
+enum class DType : int32_t { BF16 = NMI_BF16, FP16 = NMI_FP16, FP32 = NMI_FP32, I8 = NMI_I8, I32 = NMI_I32, I64 = NMI_I64 };
+
+inline std::size_t dtype_size(DType d) {
+    switch (d) {
+    case DType::BF16:
+    case DType::FP16: return 2;
+    case DType::FP32:
+    case DType::I32: return 4;
+    case DType::I8: return 1;
+    case DType::I64: return 8;
+    }
+    return 0;
+}
+
+// src/core/tensor.h:11-28 — non-owning view, ne[0] fastest, nb in bytes.
+struct Tensor {
+    void* data = nullptr;
+    DType dtype = DType::BF16;
+    int32_t ne[4] = {1, 1, 1, 1};
+    int64_t nb[4] = {0, 0, 0, 0};
+
+    Tensor() noexcept = default;
+    Tensor(void* d, DType t, std::initializer_list<int32_t> shape) : data(d), dtype(t) {
+        int i = 0;
+        for (int32_t s : shape) { ne[i++] = s; }
+        int64_t stride = static_cast<int64_t>(dtype_size(t));
+        for (int k = 0; k < 4; ++k) {
+            nb[k] = stride;
+            stride *= ne[k];
+        }
+    }
+    nmi_tensor c() const {
+        nmi_tensor r{};
+        r.data = data;
+        r.dtype = static_cast<int32_t>(dtype);
+        for (int k = 0; k < 4; ++k) {
+            r.ne[k] = ne[k];
+            r.nb[k] = nb[k];
+        }
+        return r;
+    }
+};
+
+// src/core/kv_cache.h:13-24.
+struct KVCacheLayerView {
+    Tensor k, v, k_scale, v_scale;
+    uint32_t max_context = 0;
+    uint32_t padded_context = 0;
+    int32_t num_kv_heads = 0;
+    int32_t head_dim = 0;
+    DType dtype = DType::BF16;
+    int32_t quant_group = 0;
+
+    nmi_kv_layer_view c() const {
+        nmi_kv_layer_view r{};
+        r.k = k.c();
+        r.v = v.c();
+        r.k_scale = k_scale.c();
+        r.v_scale = v_scale.c();
+        r.max_context = max_context;
+        r.padded_context = padded_context;
+        r.num_kv_heads = num_kv_heads;
+        r.head_dim = head_dim;
+        r.dtype = static_cast<int32_t>(dtype);
+        r.quant_group = quant_group;
+        return r;
+    }
+};
+
+using GqaExecutionEnvelope = nmi_gqa_envelope;
+using KVCacheAppendPrefixExecutionEnvelope = nmi_commit_envelope;
+using SamplingConfig = nmi_sampling_config; // same 40-byte device layout as the reference
+
+// Caller-owned bump arena over device memory (src/core/arena.h WorkspaceArena semantics: ops take
+// a scope, sub-allocate 256-byte aligned regions, and release them when the scope ends).
+class WorkspaceArena {
+  public:
+    WorkspaceArena(void* base, std::size_t bytes) : base_(static_cast<char*>(base)), cap_(bytes) {}
+    struct Scope {
+        WorkspaceArena* a;
+        std::size_t mark;
+        ~Scope() { a->used_ = mark; }
+    };
+    Scope scope() { return Scope{this, used_}; }
+    void* alloc_bytes(std::size_t n) {
+        const std::size_t at = (used_ + 255) & ~static_cast<std::size_t>(255);
+        if (at + n > cap_) { throw std::invalid_argument("WorkspaceArena: out of capacity"); }
+        used_ = at + n;
+        return base_ + at;
+    }
+    std::size_t remaining() const { return cap_ - ((used_ + 255) & ~static_cast<std::size_t>(255)); }
+
+  private:
+    char* base_;
+    std::size_t cap_;
+    std::size_t used_ = 0;
+};
+
+namespace detail {
+inline void check(int status) {
+    if (status == NMI_OK) { return; }
+    const std::string msg = nmi_last_error();
+    if (status == NMI_INVALID_ARGUMENT) { throw std::invalid_argument(msg); }
+    if (status == NMI_OVERFLOW) { throw std::overflow_error(msg); }
+    throw std::runtime_error(msg);
+}
+inline nmi_stream_t st(hipStream_t s) { return reinterpret_cast<nmi_stream_t>(s); }
+} // namespace detail
+
+namespace ops {
+
+// include/ninfer/ops/gqa_attention.h:50 (geometry and envelope are explicit here).
+[[nodiscard]] inline std::size_t gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads,
+                                                               int32_t head_dim, int32_t tokens,
+                                                               int32_t batch,
+                                                               uint32_t max_visible_keys) {
+    return nmi_gqa_attention_workspace_bytes(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys);
+}
+
+// A1, include/ninfer/ops/gqa_attention.h:71-73.
+inline void gqa_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& positions,
+                          float scale, KVCacheLayerView cache, GqaExecutionEnvelope envelope,
+                          WorkspaceArena& workspace, Tensor& out, hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = gqa_attention_workspace_bytes(q.ne[1], cache.num_kv_heads, q.ne[0], q.ne[2], q.ne[3],
+                                                           envelope.max_visible_keys);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor cq = q.c(), ck = k.c(), cv = v.c(), cp = positions.c();
+    nmi_tensor co = out.c();
+    const nmi_kv_layer_view cc = cache.c();
+    detail::check(nmi_gqa_attention(&cq, &ck, &cv, &cp, scale, &cc, envelope, ws, need, &co, detail::st(stream)));
+}
+
+// A2, include/ninfer/ops/gqa_attention.h:80-81.
+inline void gqa_kv_append(const Tensor& k, const Tensor& v, const Tensor& positions,
+                          KVCacheLayerView cache, hipStream_t stream) {
+    const nmi_tensor ck = k.c(), cv = v.c(), cp = positions.c();
+    const nmi_kv_layer_view cc = cache.c();
+    detail::check(nmi_gqa_kv_append(&ck, &cv, &cp, &cc, detail::st(stream)));
+}
+
+// A3, include/ninfer/ops/gqa_attention.h:89-91.
+inline void gqa_attention_cached(const Tensor& q, const Tensor& positions, float scale,
+                                 const KVCacheLayerView& cache, GqaExecutionEnvelope envelope,
+                                 WorkspaceArena& workspace, Tensor& out, hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = gqa_attention_workspace_bytes(q.ne[1], cache.num_kv_heads, q.ne[0], q.ne[2], q.ne[3],
+                                                           envelope.max_visible_keys);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor cq = q.c(), cp = positions.c();
+    nmi_tensor co = out.c();
+    const nmi_kv_layer_view cc = cache.c();
+    detail::check(nmi_gqa_attention_cached(&cq, &cp, scale, &cc, envelope, ws, need, &co, detail::st(stream)));
+}
+
+// Extension: tree verification (ancestor mask).
+inline void gqa_attention_tree(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& positions,
+                               const Tensor& parents, float scale, KVCacheLayerView cache,
+                               GqaExecutionEnvelope envelope, bool write_cache, WorkspaceArena& workspace,
+                               Tensor& out, hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = gqa_attention_workspace_bytes(q.ne[1], cache.num_kv_heads, q.ne[0], q.ne[2], q.ne[3],
+                                                           envelope.max_visible_keys);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor cq = q.c(), ck = k.c(), cv = v.c(), cp = positions.c(), cpar = parents.c();
+    nmi_tensor co = out.c();
+    const nmi_kv_layer_view cc = cache.c();
+    detail::check(nmi_gqa_attention_tree(&cq, &ck, &cv, &cp, &cpar, scale, &cc, envelope, write_cache ? 1 : 0, ws,
+                                         need, &co, detail::st(stream)));
+}
+
+// include/ninfer/ops/argmax.h:21.
+inline void argmax(const Tensor& logits, Tensor& out, int32_t valid_rows, hipStream_t stream) {
+    const nmi_tensor cl = logits.c();
+    nmi_tensor co = out.c();
+    detail::check(nmi_argmax(&cl, &co, valid_rows, detail::st(stream)));
+}
+
+// include/ninfer/ops/sampling.h:37.
+[[nodiscard]] inline std::size_t sampling_workspace_bytes(int32_t token_domain, int32_t columns) {
+    return nmi_sampling_workspace_bytes(token_domain, columns, 1);
+}
+
+// include/ninfer/ops/speculative_round.h:29-31.
+inline void speculative_prepare_verify_inputs(const Tensor& token, const Tensor& drafts, const Tensor& length,
+                                              Tensor& verify_ids, Tensor& positions, hipStream_t stream) {
+    const nmi_tensor ct = token.c(), cd = drafts.c(), cl = length.c();
+    nmi_tensor cv = verify_ids.c(), cp = positions.c();
+    detail::check(nmi_speculative_prepare_verify_inputs(&ct, &cd, &cl, &cv, &cp, detail::st(stream)));
+}
+
+// include/ninfer/ops/speculative_round.h:68-73.
+inline void speculative_accept_greedy_drafts(const Tensor& target_tokens, const Tensor& logits,
+                                             const Tensor& drafts, Tensor& length, Tensor& token,
+                                             Tensor& sampled_out, Tensor& num_sampled, Tensor& accepted,
+                                             Tensor& stats, int32_t token_domain,
+                                             const SamplingConfig* config, WorkspaceArena& workspace,
+                                             hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = nmi_sampling_workspace_bytes(token_domain, drafts.ne[0] + 1, drafts.ne[1]);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor ct = target_tokens.c(), cl = logits.c(), cd = drafts.c();
+    nmi_tensor clen = length.c(), ctok = token.c(), cso = sampled_out.c(), cns = num_sampled.c(),
+               cacc = accepted.c(), cst = stats.c();
+    detail::check(nmi_speculative_accept_greedy_drafts(&ct, &cl, &cd, &clen, &ctok, &cso, &cns, &cacc, &cst,
+                                                       token_domain, config, ws, need, detail::st(stream)));
+}
+
+// Extension: general min(1, p/q) acceptance with residual resampling.
+inline void speculative_accept_general(const Tensor& logits, const Tensor& draft_logits, const Tensor& drafts,
+                                       const Tensor& u_accept, const Tensor& u_residual, Tensor& length,
+                                       Tensor& token, Tensor& sampled_out, Tensor& num_sampled, Tensor& accepted,
+                                       Tensor& stats, int32_t token_domain, const nmi_general_config* config,
+                                       WorkspaceArena& workspace, hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = nmi_general_accept_workspace_bytes(token_domain, drafts.ne[0], drafts.ne[1]);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor cl = logits.c(), cdl = draft_logits.c(), cd = drafts.c(), cua = u_accept.c(),
+                     cur = u_residual.c();
+    nmi_tensor clen = length.c(), ctok = token.c(), cso = sampled_out.c(), cns = num_sampled.c(),
+               cacc = accepted.c(), cst = stats.c();
+    detail::check(nmi_speculative_accept_general(&cl, &cdl, &cd, &cua, &cur, &clen, &ctok, &cso, &cns, &cacc, &cst,
+                                                 token_domain, config, ws, need, detail::st(stream)));
+}
+
+// include/ninfer/ops/speculative_round.h:86-87.
+inline void speculative_select_accepted_hidden(const Tensor& hidden, const Tensor& accepted, Tensor& out,
+                                               hipStream_t stream) {
+    const nmi_tensor ch = hidden.c(), ca = accepted.c();
+    nmi_tensor co = out.c();
+    detail::check(nmi_speculative_select_accepted_hidden(&ch, &ca, &co, detail::st(stream)));
+}
+
+// include/ninfer/ops/kv_cache_append_prefix.h:34-37 (linear cache; BF16 or INT8-G64).
+inline void kv_cache_append_prefix(const Tensor& k, const Tensor& v, const Tensor& positions,
+                                   const Tensor& commit_count, KVCacheAppendPrefixExecutionEnvelope envelope,
+                                   KVCacheLayerView cache, hipStream_t stream) {
+    const nmi_tensor ck = k.c(), cv = v.c(), cp = positions.c(), cc = commit_count.c();
+    const nmi_kv_layer_view view = cache.c();
+    detail::check(nmi_kv_cache_append_prefix(&ck, &cv, &cp, &cc, envelope, &view, detail::st(stream)));
+}
+
+// Extension: explicit rollback of rejected rows.
+inline void kv_cache_rollback(const Tensor& positions, const Tensor& keep_count, KVCacheLayerView cache,
+                              hipStream_t stream) {
+    const nmi_tensor cp = positions.c(), ck = keep_count.c();
+    const nmi_kv_layer_view view = cache.c();
+    detail::check(nmi_kv_cache_rollback(&cp, &ck, &view, detail::st(stream)));
+}
+
+// Extension: compaction of an accepted tree path.
+inline void kv_cache_compact_path(const Tensor& base_position, const Tensor& path, const Tensor& path_len,
+                                  KVCacheLayerView cache, hipStream_t stream) {
+    const nmi_tensor cb = base_position.c(), cp = path.c(), cl = path_len.c();
+    const nmi_kv_layer_view view = cache.c();
+    detail::check(nmi_kv_cache_compact_path(&cb, &cp, &cl, &view, detail::st(stream)));
+}
+
+// Extension: greedy tree acceptance.
+inline void tree_accept_greedy(const Tensor& parents, const Tensor& node_tokens, const Tensor& target_tokens,
+                               Tensor& path, Tensor& path_len, Tensor& length, Tensor& token, Tensor& sampled_out,
+                               Tensor& num_sampled, Tensor& accepted, Tensor& stats, hipStream_t stream) {
+    const nmi_tensor cpar = parents.c(), cnt = node_tokens.c(), ctt = target_tokens.c();
+    nmi_tensor cpath = path.c(), cpl = path_len.c(), clen = length.c(), ctok = token.c(), cso = sampled_out.c(),
+               cns = num_sampled.c(), cacc = accepted.c(), cst = stats.c();
+    detail::check(nmi_tree_accept_greedy(&cpar, &cnt, &ctt, &cpath, &cpl, &clen, &ctok, &cso, &cns, &cacc, &cst,
+                                         detail::st(stream)));
+}
+
+} // namespace ops
+} // namespace ninfer_amd

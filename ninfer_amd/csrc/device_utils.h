@@ -1,0 +1,87 @@
+// Device helpers shared by the gfx950 kernels: bit conversions, wave reductions, vector types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace nmi {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef int i4 __attribute__((ext_vector_type(4)));
+typedef int i2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even FP32 -> BF16 bits (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+    uint32_t b = __float_as_uint(x);
+    if ((b & 0x7fffffffu) > 0x7f800000u) { return static_cast<uint16_t>((b >> 16) | 0x40u); }
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return static_cast<uint16_t>(b >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) { v = fmaxf(v, __shfl_xor(v, off, 64)); }
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) { v += __shfl_xor(v, off, 64); }
+    return v;
+}
+
+// Reduction across the four 16-lane groups that share one MFMA column (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float group4_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+__device__ __forceinline__ float group4_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// Two signed INT8 codes -> one packed FP16 pair, exactly: byte BYTE of `lo` -> low half, byte BYTE
+// of `hi` -> high half. One SDWA convert per code reads the byte in place (no shifts, no packing).
+template <int BYTE>
+__device__ __forceinline__ uint32_t i8x2_to_f16x2(uint32_t lo, uint32_t hi) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_%2"
+        : "=v"(r)
+        : "v"(lo), "n"(BYTE));
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_%2"
+        : "+v"(r)
+        : "v"(hi), "n"(BYTE));
+    return r;
+}
+
+// Bytes (B0, B1) of one dword -> packed FP16 pair.
+template <int B0, int B1>
+__device__ __forceinline__ uint32_t i8_bytes_to_f16x2(uint32_t x) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_%2"
+        : "=v"(r)
+        : "v"(x), "n"(B0));
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_%2"
+        : "+v"(r)
+        : "v"(x), "n"(B1));
+    return r;
+}
+
+} // namespace nmi

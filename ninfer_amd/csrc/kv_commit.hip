@@ -1,0 +1,161 @@
+// KV cache commit, rollback and tree-path compaction on gfx950.
+//
+// The reference never writes a rejected row's bytes when committing a device-selected prefix
+// (include/ninfer/ops/kv_cache_append_prefix.h:22-32, BF16 kernel
+// src/ops/kernel/kv_cache_append_prefix.cuh) and rolls back implicitly by moving the frontier
+// (src/ops/kernel/speculative_round.cuh:150-158). This file adds the explicit forms the verify step
+// needs for an INT8-G64 cache: zeroing rejected rows, and moving an accepted tree path's rows to
+// contiguous slots. All copies move codes and FP16 scale bits unchanged.
+#include "common.h"
+#include "device_utils.h"
+#include "ops_internal.h"
+
+namespace nmi {
+namespace {
+
+// grid (T, B): block zeroes row positions[t, b] of every KV head when t >= keep_count[b].
+__global__ __launch_bounds__(256) void kv_rollback_kernel(const int32_t* positions,
+                                                          const int32_t* keep_count, int32_t T,
+                                                          int32_t Hkv, int32_t D, int32_t P,
+                                                          int8_t* kc, int8_t* vc, uint16_t* ks,
+                                                          uint16_t* vs, int64_t code_seq,
+                                                          int64_t scale_seq) {
+    const int t = blockIdx.x;
+    const int b = blockIdx.y;
+    if (t < keep_count[b]) { return; }
+    const int pos = positions[static_cast<int64_t>(b) * T + t];
+    if (pos < 0 || pos >= P) { return; }
+    const int G = D / 64;
+    const int vec_per_row = D / 16;
+    for (int i = threadIdx.x; i < Hkv * vec_per_row; i += blockDim.x) {
+        const int h = i / vec_per_row;
+        const int part = i - h * vec_per_row;
+        const int64_t off = static_cast<int64_t>(b) * code_seq + static_cast<int64_t>(D) * (pos + static_cast<int64_t>(P) * h) + 16 * part;
+        *reinterpret_cast<i4*>(kc + off) = i4{0, 0, 0, 0};
+        *reinterpret_cast<i4*>(vc + off) = i4{0, 0, 0, 0};
+    }
+    for (int i = threadIdx.x; i < Hkv * G; i += blockDim.x) {
+        const int h = i / G;
+        const int grp = i - h * G;
+        const int64_t off = static_cast<int64_t>(b) * scale_seq + static_cast<int64_t>(G) * (pos + static_cast<int64_t>(P) * h) + grp;
+        ks[off] = 0;
+        vs[off] = 0;
+    }
+}
+
+// grid (B): one block per sequence. Every source row is staged in LDS before any destination is
+// written, so overlapping moves (path[j] == j' for a later j') are safe.
+__global__ __launch_bounds__(256) void kv_compact_path_kernel(const int32_t* base_position,
+                                                              const int32_t* path,
+                                                              const int32_t* path_len, int32_t T,
+                                                              int32_t Hkv, int32_t D, int32_t P,
+                                                              int8_t* kc, int8_t* vc, uint16_t* ks,
+                                                              uint16_t* vs, int64_t code_seq,
+                                                              int64_t scale_seq) {
+    extern __shared__ int4 smem[];
+    const int b = blockIdx.x;
+    const int base = base_position[b];
+    int len = path_len[b];
+    len = len < 0 ? 0 : (len > T ? T : len);
+    const int32_t* pth = path + static_cast<int64_t>(b) * T;
+    const int G = D / 64;
+    const int vec_per_row = D / 16;
+    // Per head: codes K|V as 16-byte vectors, then scales as 16-bit words.
+    i4* sk = reinterpret_cast<i4*>(smem);
+    i4* sv = sk + T * vec_per_row;
+    uint16_t* sks = reinterpret_cast<uint16_t*>(sv + T * vec_per_row);
+    uint16_t* svs = sks + T * G;
+    for (int h = 0; h < Hkv; ++h) {
+        const int64_t head_code = static_cast<int64_t>(b) * code_seq + static_cast<int64_t>(h) * P * D;
+        const int64_t head_scale = static_cast<int64_t>(b) * scale_seq + static_cast<int64_t>(h) * P * G;
+        for (int i = threadIdx.x; i < len * vec_per_row; i += blockDim.x) {
+            const int j = i / vec_per_row;
+            const int part = i - j * vec_per_row;
+            const int src = base + pth[j];
+            if (src < 0 || src >= P) { continue; }
+            sk[i] = *reinterpret_cast<const i4*>(kc + head_code + static_cast<int64_t>(src) * D + 16 * part);
+            sv[i] = *reinterpret_cast<const i4*>(vc + head_code + static_cast<int64_t>(src) * D + 16 * part);
+        }
+        for (int i = threadIdx.x; i < len * G; i += blockDim.x) {
+            const int j = i / G;
+            const int grp = i - j * G;
+            const int src = base + pth[j];
+            if (src < 0 || src >= P) { continue; }
+            sks[i] = ks[head_scale + static_cast<int64_t>(src) * G + grp];
+            svs[i] = vs[head_scale + static_cast<int64_t>(src) * G + grp];
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < len * vec_per_row; i += blockDim.x) {
+            const int j = i / vec_per_row;
+            const int part = i - j * vec_per_row;
+            const int src = base + pth[j];
+            const int dst = base + j;
+            if (src == dst || src < 0 || src >= P || dst < 0 || dst >= P) { continue; }
+            *reinterpret_cast<i4*>(kc + head_code + static_cast<int64_t>(dst) * D + 16 * part) = sk[i];
+            *reinterpret_cast<i4*>(vc + head_code + static_cast<int64_t>(dst) * D + 16 * part) = sv[i];
+        }
+        for (int i = threadIdx.x; i < len * G; i += blockDim.x) {
+            const int j = i / G;
+            const int grp = i - j * G;
+            const int src = base + pth[j];
+            const int dst = base + j;
+            if (src == dst || src < 0 || src >= P || dst < 0 || dst >= P) { continue; }
+            ks[head_scale + static_cast<int64_t>(dst) * G + grp] = sks[i];
+            vs[head_scale + static_cast<int64_t>(dst) * G + grp] = svs[i];
+        }
+        __syncthreads();
+    }
+}
+
+// BF16 cache prefix commit (reference kv_cache_append_prefix_flat_kernel semantics): column i <
+// *count is copied bit-for-bit into row positions[i].
+__global__ __launch_bounds__(256) void bf16_append_prefix_kernel(const uint16_t* k, const uint16_t* v,
+                                                                 const int32_t* positions,
+                                                                 const int32_t* count, int32_t Hkv,
+                                                                 int32_t D, int32_t P, uint16_t* kc,
+                                                                 uint16_t* vc) {
+    const int t = blockIdx.x;
+    if (t >= *count) { return; }
+    const int pos = positions[t];
+    if (pos < 0 || pos >= P) { return; }
+    const int vec_per_row = D / 8; // 8 BF16 per 16 bytes
+    for (int i = threadIdx.x; i < Hkv * vec_per_row; i += blockDim.x) {
+        const int h = i / vec_per_row;
+        const int part = i - h * vec_per_row;
+        const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(Hkv) * t) + 8 * part;
+        const int64_t dst = static_cast<int64_t>(D) * (pos + static_cast<int64_t>(P) * h) + 8 * part;
+        *reinterpret_cast<i4*>(kc + dst) = *reinterpret_cast<const i4*>(k + src);
+        *reinterpret_cast<i4*>(vc + dst) = *reinterpret_cast<const i4*>(v + src);
+    }
+}
+
+} // namespace
+
+void launch_kv_rollback(const int32_t* positions, const int32_t* keep_count, int32_t T,
+                        const CacheRef& c, hipStream_t stream) {
+    hipLaunchKernelGGL(kv_rollback_kernel, dim3(T, c.B), dim3(256), 0, stream, positions,
+                       keep_count, T, c.Hkv, c.D, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq,
+                       c.scale_seq);
+    check_launch("kv_rollback_kernel");
+}
+
+void launch_kv_compact_path(const int32_t* base_position, const int32_t* path,
+                            const int32_t* path_len, int32_t T, const CacheRef& c,
+                            hipStream_t stream) {
+    const int G = c.D / 64;
+    const size_t lds = static_cast<size_t>(T) * (2 * c.D + 2 * G * 2);
+    hipLaunchKernelGGL(kv_compact_path_kernel, dim3(c.B), dim3(256), lds, stream, base_position,
+                       path, path_len, T, c.Hkv, c.D, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq,
+                       c.scale_seq);
+    check_launch("kv_compact_path_kernel");
+}
+
+void launch_bf16_append_prefix(const uint16_t* k, const uint16_t* v, const int32_t* positions,
+                               const int32_t* count, int32_t T, int32_t Hkv, int32_t D,
+                               int32_t P, uint16_t* kc, uint16_t* vc, hipStream_t stream) {
+    hipLaunchKernelGGL(bf16_append_prefix_kernel, dim3(T), dim3(256), 0, stream, k, v, positions,
+                       count, Hkv, D, P, kc, vc);
+    check_launch("bf16_append_prefix_kernel");
+}
+
+} // namespace nmi

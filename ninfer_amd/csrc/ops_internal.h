@@ -1,0 +1,64 @@
+// Host-side launch interfaces between the C ABI (validation, capi.cpp) and the kernel files.
+#pragma once
+
+#include "common.h"
+
+namespace nmi {
+
+// A validated INT8-G64 cache view (src/core/kv_cache.h:13-24) with an optional batch dimension.
+struct CacheRef {
+    int8_t* kc = nullptr;
+    int8_t* vc = nullptr;
+    uint16_t* ks = nullptr; // FP16 bits
+    uint16_t* vs = nullptr;
+    int64_t code_seq = 0;  // code elements between sequences
+    int64_t scale_seq = 0; // scale elements between sequences
+    int32_t P = 0;         // padded context
+    int32_t Hkv = 0;
+    int32_t D = 0;
+    int32_t B = 1;
+};
+
+// Split-K plan for the verify attention: shared by the workspace query and the launch, like the
+// reference's shared layout builder (src/ops/wrapper/gqa_attention.cpp:138-153,229-245).
+struct SplitPlan {
+    int32_t G = 0;                // query heads per KV head
+    int32_t tokens_per_chunk = 0; // tokens whose G rows fit one 32-row MFMA tile pair
+    int32_t row_chunks = 0;
+    int32_t nsplit = 0;           // key splits per (sequence, row chunk, KV head)
+    int32_t keys_per_split = 0;   // multiple of 128
+    size_t part_o_offset = 0;
+    size_t part_ml_offset = 0;
+    size_t bytes = 0;
+};
+
+inline constexpr int32_t kAttnRowsPerTile = 32;
+inline constexpr int32_t kAttnTargetWorkgroups = 512; // 2 per CU on 256 CUs
+inline constexpr int32_t kAttnMinKeysPerSplit = 256;
+inline constexpr int32_t kAttnMaxTokens = 32;
+
+SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
+                         uint32_t max_visible_keys);
+
+// Quantize-append: columns t (< *count when count != nullptr) of k/v BF16 [D, Hkv, T, B] into
+// rows positions[t + T*b].
+void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
+                      const int32_t* count, int32_t T, const CacheRef& cache, hipStream_t stream);
+
+// Split-K verify attention over cache rows; parents == nullptr is the causal mask.
+void launch_verify_attention(const uint16_t* q, const int32_t* positions, const int32_t* parents,
+                             int32_t T, int32_t Hq, const CacheRef& cache, float scale,
+                             uint32_t max_keys, void* workspace, const SplitPlan& plan, void* out,
+                             bool out_f32, hipStream_t stream);
+
+// Commit helpers (kv_commit.hip).
+void launch_kv_rollback(const int32_t* positions, const int32_t* keep_count, int32_t T,
+                        const CacheRef& cache, hipStream_t stream);
+void launch_kv_compact_path(const int32_t* base_position, const int32_t* path,
+                            const int32_t* path_len, int32_t T, const CacheRef& cache,
+                            hipStream_t stream);
+void launch_bf16_append_prefix(const uint16_t* k, const uint16_t* v, const int32_t* positions,
+                               const int32_t* count, int32_t T, int32_t Hkv, int32_t D,
+                               int32_t P, uint16_t* kc, uint16_t* vc, hipStream_t stream);
+
+} // namespace nmi

@@ -1,0 +1,488 @@
+// On-GPU acceptance for the MTP verify step (gfx950): argmax, verify-input preparation, greedy and
+// reference-stochastic ("Mode R", top-20 candidate cap) speculative acceptance, accepted-hidden
+// selection and greedy tree acceptance.
+//
+// Reference semantics: include/ninfer/ops/{argmax,sampling,speculative_round}.h and
+// src/ops/kernel/{argmax,speculative_round,sampling_device}.cuh. The stochastic route keeps the
+// reference's two-launch shape (per-tile candidates, then merge + accept with a last-block
+// hand-off) but replaces the CUB block merge sort with wave-level extraction over 64-bit ordered
+// keys, and __expf with the deterministic det_expf shared with the CPU oracle.
+#include "common.h"
+#include "device_utils.h"
+#include "sampler_internal.h"
+#include "sampler_common.h"
+
+#pragma clang fp contract(off)
+
+namespace nmi {
+namespace {
+
+// ---- wave top-k over 64-bit keys ------------------------------------------------------------------
+
+template <int N>
+__device__ __forceinline__ void cas_desc(uint64_t (&k)[N], int i, int j) {
+    const uint64_t a = k[i];
+    const uint64_t b = k[j];
+    const bool sw = b > a;
+    k[i] = sw ? b : a;
+    k[j] = sw ? a : b;
+}
+
+// Bitonic sort, descending, fully unrolled (N a power of two).
+template <int N>
+__device__ __forceinline__ void sort_desc(uint64_t (&k)[N]) {
+#pragma unroll
+    for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    if ((i & size) == 0) {
+                        cas_desc(k, i, j);
+                    } else {
+                        cas_desc(k, j, i);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Writes the wave's `cap` largest keys (descending, 0-padded) to out[0..cap). Keys are unique
+// except the 0 pad, so exactly one lane owns each extracted nonzero key.
+template <int N>
+__device__ __forceinline__ void wave_topk(uint64_t (&k)[N], int cap, uint64_t* out) {
+    sort_desc(k);
+    const int lane = threadIdx.x & 63;
+    for (int r = 0; r < cap; ++r) {
+        const uint64_t best = wave_max_u64(k[0]);
+        if (lane == 0) { out[r] = best; }
+        if (best != 0 && k[0] == best) {
+#pragma unroll
+            for (int i = 0; i + 1 < N; ++i) { k[i] = k[i + 1]; }
+            k[N - 1] = 0;
+        }
+    }
+}
+
+__device__ __forceinline__ int candidate_cap(const nmi_sampling_config& cfg, int32_t vocab) {
+    int cap = kCandidateCap; // src/ops/kernel/sampling_device.cuh:110-118
+    if (cfg.top_k > 0 && cfg.top_k < cap) { cap = cfg.top_k; }
+    if (vocab < cap) { cap = vocab; }
+    return cap;
+}
+
+// src/ops/kernel/sampling_device.cuh:137-149; overlay = drafts[0..col-1].
+__device__ __forceinline__ float adjusted_logit(float raw, int v, const nmi_sampling_config& c,
+                                                const int32_t* overlay, int overlay_len) {
+    float x = raw;
+    if (c.presence_penalty == 0.0f && c.frequency_penalty == 0.0f) { return x; }
+    int cnt = c.token_counts != nullptr ? c.token_counts[v] : 0;
+    for (int j = 0; j < overlay_len; ++j) {
+        if (overlay[j] == v) { ++cnt; }
+    }
+    if (cnt > 0) { x = x - c.presence_penalty; }
+    if (c.frequency_penalty != 0.0f) { x = x - c.frequency_penalty * static_cast<float>(cnt); }
+    return x;
+}
+
+// ---- argmax ---------------------------------------------------------------------------------------
+
+// One 1024-thread block per column: 16-byte loads, packed (ordered value, ~id) max.
+__global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* logits, int32_t* out,
+                                                      int32_t physical_rows, int32_t valid_rows,
+                                                      int64_t column_stride) {
+    const int col = blockIdx.x;
+    const uint16_t* x = logits + static_cast<int64_t>(col) * column_stride;
+    uint64_t best = 0;
+    const int vec = valid_rows / 8;
+    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    if (aligned) {
+        for (int i = threadIdx.x; i < vec; i += blockDim.x) {
+            const i4 raw = *reinterpret_cast<const i4*>(x + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t w = static_cast<uint32_t>(raw[e >> 1]);
+                const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+                const uint64_t key = sort_key(bf16_to_f32(bits), 8 * i + e);
+                best = key > best ? key : best;
+            }
+        }
+    }
+    for (int v = (aligned ? 8 * vec : 0) + threadIdx.x; v < valid_rows; v += blockDim.x) {
+        const uint64_t key = sort_key(bf16_to_f32(x[v]), v);
+        best = key > best ? key : best;
+    }
+    best = wave_max_u64(best);
+    __shared__ uint64_t wbest[16];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (lane == 0) { wbest[wave] = best; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = 0;
+        for (int w = 0; w < static_cast<int>(blockDim.x / 64); ++w) { b = wbest[w] > b ? wbest[w] : b; }
+        out[col] = key_index(b);
+    }
+    (void)physical_rows;
+}
+
+// ---- verify inputs ---------------------------------------------------------------------------------
+
+// src/ops/kernel/speculative_round.cuh:19-28, per sequence b.
+__global__ void prepare_verify_inputs_kernel(const int32_t* token, const int32_t* drafts,
+                                             const int32_t* length, int32_t* verify_ids,
+                                             int32_t* positions, int32_t K) {
+    const int b = blockIdx.x;
+    for (int i = threadIdx.x; i <= K; i += blockDim.x) {
+        verify_ids[b * (K + 1) + i] = i == 0 ? token[b] : drafts[b * K + i - 1];
+        positions[b * (K + 1) + i] = length[b] + i;
+    }
+}
+
+// ---- commit epilogue (src/ops/kernel/speculative_round.cuh:145-166) --------------------------------
+__device__ void commit_round(const int32_t* drafts, int K, int a, int tstar, int L, int32_t* length,
+                             int32_t* token, int32_t* sampled_out, int32_t* num_sampled,
+                             int32_t* accepted, int64_t* stats) {
+    for (int i = 0; i <= K; ++i) { sampled_out[i] = 0; }
+    for (int i = 0; i < a; ++i) { sampled_out[i] = drafts[i]; }
+    sampled_out[a] = tstar;
+    const int produced = a + 1;
+    *num_sampled = produced;
+    *accepted = a;
+    *token = tstar;
+    *length = L + produced;
+    stats[0] += K;
+    stats[1] += a;
+    stats[2] += 1;
+    for (int i = 0; i < a; ++i) { stats[kStatsPerPositionOffset + i] += 1; }
+}
+
+__device__ int pick_from_support(const int32_t* cand_idx, const float* prob, int n, int exclude, float u) {
+    float mass = 0.0f; // src/ops/kernel/sampling_device.cuh:307-329
+    for (int j = 0; j < n; ++j) {
+        if (cand_idx[j] == exclude) { continue; }
+        mass = mass + prob[j];
+    }
+    if (mass <= 0.0f) { return cand_idx[0]; }
+    const float goal = u * mass;
+    float acc = 0.0f;
+    int picked = -1;
+    for (int j = 0; j < n; ++j) {
+        if (cand_idx[j] == exclude) { continue; }
+        acc = acc + prob[j];
+        picked = cand_idx[j];
+        if (goal < acc) { return picked; }
+    }
+    return picked;
+}
+
+// ---- Mode R launch 1: per-tile top-cap candidates ------------------------------------------------
+
+__global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
+    const int tile = blockIdx.x;
+    const int col = blockIdx.y;
+    const int b = blockIdx.z;
+    const nmi_sampling_config cfg = a.config[b];
+    if (tile == 0 && col == 0 && threadIdx.x == 0) { a.counters[b] = 0; }
+    if (!(cfg.temperature > 0.0f)) { return; }
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cap = candidate_cap(cfg, a.token_domain);
+    const uint16_t* x = a.logits + static_cast<int64_t>(b) * a.logits_seq_stride + static_cast<int64_t>(col) * a.physical_rows;
+    const int32_t* drafts = a.drafts + static_cast<int64_t>(b) * a.K;
+    const int base = tile * kTileTokens + wave * 1024 + lane * 16;
+    uint64_t keys[16];
+    const bool vec_ok = base + 16 <= a.token_domain && ((reinterpret_cast<uintptr_t>(x + base) & 15u) == 0);
+    if (vec_ok) {
+        const i4 r0 = *reinterpret_cast<const i4*>(x + base);
+        const i4 r1 = *reinterpret_cast<const i4*>(x + base + 8);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t w = static_cast<uint32_t>(e < 8 ? r0[e >> 1] : r1[(e - 8) >> 1]);
+            const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+            const float v = adjusted_logit(bf16_to_f32(bits), base + e, cfg, drafts, col);
+            keys[e] = sort_key(v, base + e);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int v = base + e;
+            keys[e] = v < a.token_domain ? sort_key(adjusted_logit(bf16_to_f32(x[v]), v, cfg, drafts, col), v) : 0ull;
+        }
+    }
+    __shared__ uint64_t wtop[4][kCandidateCap];
+    wave_topk(keys, cap, wtop[wave]);
+    __syncthreads();
+    if (wave == 0) {
+        uint64_t k2[2];
+        k2[0] = lane < 4 * cap && (lane / cap) < 4 ? wtop[lane / cap][lane % cap] : 0ull;
+        const int l2 = lane + 64;
+        k2[1] = l2 < 4 * cap ? wtop[l2 / cap][l2 % cap] : 0ull;
+        uint64_t* dst = a.partial + ((static_cast<int64_t>(b) * a.columns + col) * a.ntiles + tile) * kCandidateCap;
+        __shared__ uint64_t btop[kCandidateCap];
+        wave_topk(k2, cap, btop);
+        if (lane < cap) { dst[lane] = btop[lane]; }
+    }
+}
+
+// ---- Mode R launch 2: per-column merge + normalize, last column accepts ---------------------------
+
+__global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
+    const int col = blockIdx.x;
+    const int b = blockIdx.y;
+    const nmi_sampling_config cfg = a.config[b];
+    const int K = a.K;
+    const int32_t* drafts = a.drafts + static_cast<int64_t>(b) * K;
+    int32_t* length = a.length + b;
+    int32_t* token = a.token + b;
+    int32_t* sampled_out = a.sampled_out + static_cast<int64_t>(b) * (K + 1);
+    int32_t* num_sampled = a.num_sampled + b;
+    int32_t* accepted = a.accepted + b;
+    int64_t* stats = a.stats + static_cast<int64_t>(b) * a.stats_stride;
+
+    if (!(cfg.temperature > 0.0f)) {
+        // Greedy: src/ops/kernel/speculative_round.cuh:51-72.
+        if (col == 0 && threadIdx.x == 0) {
+            const int32_t* target = a.target_tokens + static_cast<int64_t>(b) * (K + 1);
+            int acc = 0;
+            while (acc < K && target[acc] == drafts[acc]) { ++acc; }
+            commit_round(drafts, K, acc, target[acc], *length, length, token, sampled_out,
+                         num_sampled, accepted, stats);
+        }
+        return;
+    }
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cap = candidate_cap(cfg, a.token_domain);
+    const uint64_t* part = a.partial + (static_cast<int64_t>(b) * a.columns + col) * a.ntiles * kCandidateCap;
+    const int nkeys = a.ntiles * cap;
+    uint64_t keys[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int p = wave * 512 + i * 64 + lane; // wave w owns keys [512w, 512w + 512)
+        if (p < nkeys) {
+            const int t = p / cap;
+            keys[i] = part[t * kCandidateCap + (p - t * cap)];
+        } else {
+            keys[i] = 0ull;
+        }
+    }
+    __shared__ uint64_t wtop[4][kCandidateCap];
+    wave_topk(keys, cap, wtop[wave]);
+    __syncthreads();
+    __shared__ float e_sh[kCandidateCap];
+    __shared__ float x_sh[kCandidateCap];
+    __shared__ int32_t idx_sh[kCandidateCap];
+    if (wave == 0) {
+        uint64_t k2[2];
+        k2[0] = lane < 4 * cap ? wtop[lane / cap][lane % cap] : 0ull;
+        const int l2 = lane + 64;
+        k2[1] = l2 < 4 * cap ? wtop[l2 / cap][l2 % cap] : 0ull;
+        __shared__ uint64_t top[kCandidateCap];
+        wave_topk(k2, cap, top);
+        // src/ops/kernel/sampling_device.cuh:190-223 with det_expf(fma(x, inv_temp, -m)).
+        const float inv_temp = 1.0f / cfg.temperature;
+        const float x0 = key_float(top[0]);
+        const float m = x0 * inv_temp;
+        if (lane < cap) {
+            const float xj = key_float(top[lane]);
+            x_sh[lane] = xj;
+            idx_sh[lane] = key_index(top[lane]);
+            e_sh[lane] = det_expf(__builtin_fmaf(xj, inv_temp, -m));
+        }
+        if (lane == 0) {
+            float sum = 0.0f;
+            for (int j = 0; j < cap; ++j) { sum = sum + e_sh[j]; }
+            const float e0 = e_sh[0];
+            const float min_p_thresh = (cfg.min_p > 0.0f) ? cfg.min_p * e0 : -1.0f;
+            const bool top_p_active = cfg.top_p < 1.0f;
+            const float top_p_target = cfg.top_p * sum;
+            float cum = 0.0f;
+            int support = 0;
+            for (int j = 0; j < cap; ++j) {
+                if (min_p_thresh >= 0.0f && e_sh[j] < min_p_thresh) { break; }
+                cum = cum + e_sh[j];
+                support = j + 1;
+                if (top_p_active && cum >= top_p_target) { break; }
+            }
+            if (support < 1) { support = 1; }
+            float ssum = 0.0f;
+            for (int j = 0; j < support; ++j) { ssum = ssum + e_sh[j]; }
+            const float inv = 1.0f / ssum;
+            const int64_t d = (static_cast<int64_t>(b) * a.columns + col) * kCandidateCap;
+            for (int j = 0; j < support; ++j) {
+                a.dist_idx[d + j] = idx_sh[j];
+                a.dist_prob[d + j] = e_sh[j] * inv;
+            }
+            a.dist_support[static_cast<int64_t>(b) * a.columns + col] = support;
+            __threadfence();
+            const int done = atomicAdd(&a.counters[b], 1) + 1;
+            if (done == K + 1) {
+                __threadfence();
+                // Sequential accept: src/ops/kernel/speculative_round.cuh:337-366.
+                const int L = *length;
+                int acc = 0;
+                int tstar = 0;
+                for (int i = 0; i <= K; ++i) {
+                    const int64_t di = (static_cast<int64_t>(b) * a.columns + i) * kCandidateCap;
+                    const int n = __atomic_load_n(&a.dist_support[static_cast<int64_t>(b) * a.columns + i], __ATOMIC_RELAXED);
+                    const int32_t* cidx = a.dist_idx + di;
+                    const float* cprob = a.dist_prob + di;
+                    if (i < K) {
+                        const int dtok = drafts[i];
+                        float pd = 0.0f;
+                        for (int j = 0; j < n; ++j) {
+                            if (cidx[j] == dtok) {
+                                pd = cprob[j];
+                                break;
+                            }
+                        }
+                        const float u = sampling_uniform(cfg.seed, L + i + 1, kPurposeAccept, 0u);
+                        if (u < pd) {
+                            acc = i + 1;
+                            continue;
+                        }
+                        const float ur = sampling_uniform(cfg.seed, L + i + 1, kPurposeCorrection, 0u);
+                        tstar = pick_from_support(cidx, cprob, n, dtok, ur);
+                        break;
+                    }
+                    const float u = sampling_uniform(cfg.seed, L + K + 1, kPurposeBonus, 0u);
+                    tstar = pick_from_support(cidx, cprob, n, -1, u);
+                }
+                commit_round(drafts, K, acc, tstar, L, length, token, sampled_out, num_sampled,
+                             accepted, stats);
+                if (cfg.token_counts != nullptr) {
+                    for (int i = 0; i <= acc; ++i) { atomicAdd(&cfg.token_counts[sampled_out[i]], 1); }
+                }
+                a.counters[b] = 0;
+            }
+        }
+    }
+}
+
+// ---- accepted hidden (include/ninfer/ops/speculative_round.h:76-87) -------------------------------
+__global__ void select_hidden_kernel(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,
+                                     int32_t rows, int32_t cols) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) { return; }
+    const int c = *accepted;
+    if (c < 0 || c >= cols) { return; }
+    out[row] = hidden[static_cast<int64_t>(c) * rows + row];
+}
+
+// ---- greedy tree acceptance ------------------------------------------------------------------------
+// Node u > 0 is accepted iff its parent is accepted and node_tokens[u] == target_tokens[parent];
+// the deepest accepted node wins (lowest index on ties).
+__global__ void tree_accept_kernel(const int32_t* parents, const int32_t* node_tokens,
+                                   const int32_t* target_tokens, int32_t N, int32_t* path,
+                                   int32_t* path_len, int32_t* length, int32_t* token,
+                                   int32_t* sampled_out, int32_t* num_sampled, int32_t* accepted,
+                                   int64_t* stats, int32_t stats_stride) {
+    const int b = blockIdx.x;
+    if (threadIdx.x != 0) { return; }
+    const int32_t* par = parents + static_cast<int64_t>(b) * N;
+    const int32_t* tok = node_tokens + static_cast<int64_t>(b) * N;
+    const int32_t* tgt = target_tokens + static_cast<int64_t>(b) * N;
+    int32_t* pth = path + static_cast<int64_t>(b) * N;
+    int32_t* so = sampled_out + static_cast<int64_t>(b) * N;
+    int64_t* st = stats + static_cast<int64_t>(b) * stats_stride;
+    int depth[kMaxTreeNodes];
+    depth[0] = 0;
+    int best = 0;
+    for (int u = 1; u < N; ++u) {
+        depth[u] = -1;
+        const int p = par[u];
+        if (p < 0 || p >= u || depth[p] < 0) { continue; }
+        if (tok[u] != tgt[p]) { continue; }
+        depth[u] = depth[p] + 1;
+        if (depth[u] > depth[best]) { best = u; }
+    }
+    const int len = depth[best] + 1;
+    int u = best;
+    for (int j = len - 1; j >= 0; --j) {
+        pth[j] = u;
+        u = par[u];
+    }
+    for (int j = len; j < N; ++j) { pth[j] = 0; }
+    const int acc = len - 1;
+    for (int j = 0; j < N; ++j) { so[j] = 0; }
+    for (int j = 0; j < acc; ++j) { so[j] = tok[pth[j + 1]]; }
+    so[acc] = tgt[best];
+    path_len[b] = len;
+    num_sampled[b] = acc + 1;
+    accepted[b] = acc;
+    token[b] = tgt[best];
+    length[b] = length[b] + acc + 1;
+    st[0] += N - 1;
+    st[1] += acc;
+    st[2] += 1;
+    for (int j = 0; j < acc && kStatsPerPositionOffset + j < stats_stride; ++j) { st[kStatsPerPositionOffset + j] += 1; }
+}
+
+} // namespace
+
+SpecPlan plan_spec(int32_t token_domain, int32_t columns, int32_t batch) {
+    SpecPlan p;
+    p.ntiles = (token_domain + kTileTokens - 1) / kTileTokens;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off = (off + bytes + 255) & ~static_cast<size_t>(255);
+        return at;
+    };
+    const size_t cols = static_cast<size_t>(columns) * batch;
+    p.partial_offset = take(cols * p.ntiles * kCandidateCap * sizeof(uint64_t));
+    p.dist_idx_offset = take(cols * kCandidateCap * sizeof(int32_t));
+    p.dist_prob_offset = take(cols * kCandidateCap * sizeof(float));
+    p.dist_support_offset = take(cols * sizeof(int32_t));
+    p.counters_offset = take(static_cast<size_t>(batch) * sizeof(int32_t));
+    p.bytes = off;
+    return p;
+}
+
+void launch_argmax(const uint16_t* logits, int32_t* out, int32_t physical_rows, int32_t valid_rows,
+                   int32_t columns, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(columns), dim3(1024), 0, stream, logits, out,
+                       physical_rows, valid_rows, static_cast<int64_t>(physical_rows));
+    check_launch("argmax_kernel");
+}
+
+void launch_prepare_verify_inputs(const int32_t* token, const int32_t* drafts, const int32_t* length,
+                                  int32_t* verify_ids, int32_t* positions, int32_t K, int32_t B,
+                                  hipStream_t stream) {
+    hipLaunchKernelGGL(prepare_verify_inputs_kernel, dim3(B), dim3(64), 0, stream, token, drafts,
+                       length, verify_ids, positions, K);
+    check_launch("prepare_verify_inputs_kernel");
+}
+
+void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream) {
+    hipLaunchKernelGGL(spec_tile_topk_kernel, dim3(args.ntiles, args.K + 1, batch), dim3(256), 0,
+                       stream, args);
+    check_launch("spec_tile_topk_kernel");
+    hipLaunchKernelGGL(spec_merge_accept_kernel, dim3(args.K + 1, batch), dim3(256), 0, stream, args);
+    check_launch("spec_merge_accept_kernel");
+}
+
+void launch_select_hidden(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,
+                          int32_t rows, int32_t cols, hipStream_t stream) {
+    hipLaunchKernelGGL(select_hidden_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, hidden,
+                       accepted, out, rows, cols);
+    check_launch("select_hidden_kernel");
+}
+
+void launch_tree_accept(const int32_t* parents, const int32_t* node_tokens,
+                        const int32_t* target_tokens, int32_t N, int32_t B, int32_t* path,
+                        int32_t* path_len, int32_t* length, int32_t* token, int32_t* sampled_out,
+                        int32_t* num_sampled, int32_t* accepted, int64_t* stats,
+                        int32_t stats_stride, hipStream_t stream) {
+    hipLaunchKernelGGL(tree_accept_kernel, dim3(B), dim3(64), 0, stream, parents, node_tokens,
+                       target_tokens, N, path, path_len, length, token, sampled_out, num_sampled,
+                       accepted, stats, stats_stride);
+    check_launch("tree_accept_kernel");
+}
+
+} // namespace nmi

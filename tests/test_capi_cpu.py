@@ -1,0 +1,178 @@
+"""CPU-side checks of the drop-in boundary: the library loads, exports every entry point the
+public headers declare, and rejects invalid arguments on the host before any launch (the
+reference wrappers' validation, e.g. src/ops/wrapper/gqa_attention.cpp:59-136). No call here
+reaches a kernel, so no GPU is needed."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import ninfer_amd as na
+from ninfer_amd import ops
+from ninfer_amd._capi import Tensor, lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared(header):
+    text = (ROOT / "include" / header).read_text()
+    return sorted(set(re.findall(r"\b(nmi_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = lib()
+    names = _declared("ninfer_amd.h") + _declared("ninfer_amd_runtime.h")
+    assert len(names) >= 38
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_cpp_header_wraps_every_op():
+    hpp = (ROOT / "include" / "ninfer_amd" / "ops.hpp").read_text()
+    for name in _declared("ninfer_amd.h"):
+        if name in ("nmi_last_error", "nmi_build_info"):
+            continue
+        assert name in hpp, f"ops.hpp does not wrap {name}"
+
+
+def test_build_info_names_gfx950():
+    assert "gfx950" in na.build_info()
+
+
+def _t(dtype, shape, ptr=0x10000):
+    return Tensor.make(ptr, dtype, shape)
+
+
+def _cache(Hkv=8, D=128, P=4224, max_ctx=4100, B=1):
+    v = na.KVLayerView()
+    v.k = _t(na.I8, (D, P, Hkv, B))
+    v.v = _t(na.I8, (D, P, Hkv, B))
+    v.k_scale = _t(na.FP16, (D // 64, P, Hkv, B))
+    v.v_scale = _t(na.FP16, (D // 64, P, Hkv, B))
+    v.max_context, v.padded_context = max_ctx, P
+    v.num_kv_heads, v.head_dim, v.dtype, v.quant_group = Hkv, D, na.I8, 64
+    return v
+
+
+class _WS:
+    def __init__(self, n):
+        self._buf = (C.c_uint8 * (n + 512))()
+        base = C.addressof(self._buf)
+        self.ptr = (base + 255) & ~255
+        self.nbytes = n
+
+
+def _attention_args(**over):
+    D, Hq, Hkv, T = 128, 40, 8, 4
+    a = dict(q=_t(na.BF16, (D, Hq, T)), k=_t(na.BF16, (D, Hkv, T)), v=_t(na.BF16, (D, Hkv, T)),
+             positions=_t(na.I32, (T,)), scale=float(np.float32(1 / np.sqrt(128))), cache=_cache(),
+             envelope=(1, 4100), out=_t(na.BF16, (D, Hq, T)))
+    a.update(over)
+    ws = _WS(ops.gqa_attention_workspace_bytes(Hq, Hkv, D, T, 1, a["envelope"][1]))
+    return a, ws
+
+
+@pytest.mark.parametrize("override,needle", [
+    (dict(scale=0.0625), "scale must be 1/sqrt(head_dim)"),
+    (dict(q=_t(na.FP32, (128, 40, 4))), "q/out must be BF16"),
+    (dict(positions=_t(na.I64, (4,))), "positions must be I32"),
+    (dict(positions=_t(na.I32, (5,))), "invalid shape for positions"),
+    (dict(envelope=(0, 4100)), "invalid execution envelope"),
+    (dict(envelope=(1, 5000)), "invalid execution envelope"),
+    (dict(envelope=(1, 3)), "execution envelope is shorter than T"),
+    (dict(k=_t(na.BF16, (128, 4, 4))), "invalid shape for k"),
+    (dict(q=_t(na.BF16, (128, 36, 4))), "unsupported Q/KV head geometry"),
+    (dict(q=_t(na.BF16, (128, 40, 33)), out=_t(na.BF16, (128, 40, 33)), k=_t(na.BF16, (128, 8, 33)),
+          v=_t(na.BF16, (128, 8, 33)), positions=_t(na.I32, (33,))), "T exceeds 32"),
+])
+def test_gqa_attention_validation(override, needle):
+    a, ws = _attention_args(**override)
+    with pytest.raises(ValueError, match=re.escape(needle)):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], a["cache"], a["envelope"], ws,
+                          a["out"])
+
+
+def test_gqa_attention_cache_validation():
+    c = _cache()
+    c.quant_group = 32
+    a, ws = _attention_args(cache=c)
+    with pytest.raises(ValueError, match="quant_group 64"):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], ws, a["out"])
+    c = _cache()
+    c.padded_context = 4100
+    with pytest.raises(ValueError, match="multiple of 128"):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], ws, a["out"])
+    c = _cache()
+    c.k_scale = _t(na.BF16, (2, 4224, 8, 1))
+    with pytest.raises(ValueError, match="scale dtype"):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], ws, a["out"])
+
+
+def test_overflow_error_for_huge_padded_context():
+    c = _cache(P=0x80000000, max_ctx=0x7FFFFFFF)
+    a, ws = _attention_args(cache=c, envelope=(1, 4100))
+    with pytest.raises(OverflowError):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], ws, a["out"])
+
+
+def test_workspace_too_small_is_rejected():
+    a, _ = _attention_args()
+    small = _WS(1024)
+    with pytest.raises(ValueError, match="workspace"):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], a["cache"], a["envelope"], small,
+                          a["out"])
+
+
+def test_workspace_sizing_grows_with_envelope():
+    small = ops.gqa_attention_workspace_bytes(40, 8, 128, 4, 1, 8192)
+    large = ops.gqa_attention_workspace_bytes(40, 8, 128, 4, 1, 262144)
+    assert 0 < small <= large
+    assert ops.gqa_attention_workspace_bytes(40, 8, 128, 0, 1, 8192) == 0
+    assert ops.sampling_workspace_bytes(248320, 4) > 0
+
+
+def test_accept_validation():
+    K = 3
+    args = [_t(na.I32, (K + 1,)), _t(na.BF16, (248320, K + 1)), _t(na.I32, (K,)), _t(na.I32, (1,)),
+            _t(na.I32, (1,)), _t(na.I32, (K + 1,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I64, (4 + K,))]
+    ws = _WS(ops.sampling_workspace_bytes(248320, K + 1))
+    with pytest.raises(ValueError, match="token_domain"):
+        ops.speculative_accept_greedy_drafts(*args, 248321, 0x1000, ws)
+    bad = list(args)
+    bad[8] = _t(na.I64, (3 + K,))
+    with pytest.raises(ValueError, match="stats"):
+        ops.speculative_accept_greedy_drafts(*bad, 248320, 0x1000, ws)
+    with pytest.raises(ValueError, match="config must be non-null"):
+        ops.speculative_accept_greedy_drafts(*args, 248320, 0, ws)
+    bad = list(args)
+    bad[2] = _t(na.I32, (0,))
+    with pytest.raises(ValueError, match="K must be >=1"):
+        ops.speculative_accept_greedy_drafts(*bad, 248320, 0x1000, ws)
+
+
+def test_argmax_validation():
+    with pytest.raises(ValueError, match="valid_rows"):
+        ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (4,)), 101)
+    with pytest.raises(ValueError, match="out shape"):
+        ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (3,)), 100)
+    with pytest.raises(ValueError, match="logits must be BF16"):
+        ops.argmax(_t(na.FP32, (100, 4)), _t(na.I32, (4,)), 100)
+
+
+def test_commit_validation():
+    k = _t(na.BF16, (128, 8, 4))
+    with pytest.raises(ValueError, match="invalid execution envelope"):
+        ops.kv_cache_append_prefix(k, k, _t(na.I32, (4,)), _t(na.I32, (1,)), (0, 5), _cache())
+    with pytest.raises(ValueError, match="commit_count"):
+        ops.kv_cache_append_prefix(k, k, _t(na.I32, (4,)), _t(na.I32, (2,)), (0, 4), _cache())
+    with pytest.raises(ValueError, match="path capacity"):
+        ops.kv_cache_compact_path(_t(na.I32, (1,)), _t(na.I32, (40,)), _t(na.I32, (1,)), _cache())
+
+
+def test_sampling_config_layout_matches_reference():
+    """SamplingConfig is device-resident and shared with reference callers: same 40-byte layout
+    (include/ninfer/ops/sampling.h:24-33)."""
+    assert C.sizeof(na.SamplingConfig) == 40
+    assert na.SamplingConfig.seed.offset == 24 and na.SamplingConfig.token_counts.offset == 32

@@ -1,0 +1,145 @@
+"""GPU parity of the verify attention (A1/A2/A3, trees, batches) against the CPU oracle.
+
+Criteria (BASELINE): INT8 codes and FP16 scale bits bit-exact; attention output within 2e-3
+relative L2 error against the FP64 oracle (BF16 output, the reference's contract) and the
+reference's attention_bf16 composite (tests/ops/op_check.h:61); the FP32-output extension is held
+to 1e-3, which isolates the kernel's own arithmetic from the final BF16 rounding.
+"""
+import numpy as np
+import pytest
+
+from helpers import AttnCase, reference_composite_ok, rel_l2
+import gpu_runner
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_BF16 = 2e-3
+REL_L2_F32 = 1e-3
+
+
+def _check_cache(cache, expected):
+    kc, vc, ks, vs = cache.download()
+    ekc, evc, eks, evs = expected
+    assert np.array_equal(kc, ekc), "K codes differ"
+    assert np.array_equal(vc, evc), "V codes differ"
+    assert np.array_equal(ks, eks), "K scale bits differ"
+    assert np.array_equal(vs, evs), "V scale bits differ"
+
+
+def _check_out(got, ref, bound):
+    err = rel_l2(got, ref)
+    ok, msg = reference_composite_ok(got, ref)
+    print(f"rel_l2={err:.3e} composite: {msg}", flush=True)
+    assert err <= bound, f"rel_l2 {err:.3e} > {bound:.1e}"
+    return ok
+
+
+@pytest.mark.parametrize("L,T", [(4096, 4), (0, 4), (1, 1), (17, 3), (100, 6), (127, 4), (128, 4),
+                                 (255, 2), (256, 5), (1000, 4), (2882, 4), (7680, 4)])
+def test_a1_parity(gpu, L, T):
+    print(f"case A1 L={L} T={T}", flush=True)
+    case = AttnCase([L], T=T, seed=1000 + L + T)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=False)
+    _check_cache(cache, expected_cache)
+    assert _check_out(out, ref, REL_L2_BF16)
+    out32, _ = gpu_runner.run_attention(case, out_f32=True)
+    _check_out(out32, ref, REL_L2_F32)
+
+
+def test_c1_config_seed0(gpu):
+    """Config 1: batch 1, q_len 4, 40/8/128, context 4096, seed 0."""
+    case = AttnCase([4096], T=4, seed=0)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=False)
+    _check_cache(cache, expected_cache)
+    assert _check_out(out, ref, REL_L2_BF16)
+
+
+def test_outliers_long(gpu):
+    """Config 3 statistics (1% outliers at +-20) at a context the oracle finishes quickly."""
+    case = AttnCase([16384], T=4, seed=3, outliers=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def test_a2_then_a3_equals_a1(gpu):
+    case = AttnCase([3000], T=4, seed=11)
+    expected_cache, ref = case.oracle_after_append()
+    cache = gpu_runner.upload_cache(case)
+    gpu_runner.append(case, cache)
+    _check_cache(cache, expected_cache)
+    out3, _ = gpu_runner.run_attention(case, out_f32=True, mode="A3", cache=cache)
+    out1, _ = gpu_runner.run_attention(case, out_f32=True, mode="A1")
+    assert np.array_equal(out1, out3), "A1 and A2+A3 differ"
+    _check_out(out3, ref, REL_L2_F32)
+
+
+def test_future_token_isolation(gpu):
+    """Changing the last token's K/V must not change earlier tokens' outputs (bit-exact)."""
+    case = AttnCase([2500], T=4, seed=12)
+    out_a, _ = gpu_runner.run_attention(case, out_f32=True)
+    per_tok = case.D * case.Hkv
+    case.k_new = case.k_new.copy()
+    case.v_new = case.v_new.copy()
+    case.k_new[3 * per_tok:] ^= np.uint16(0x0040)
+    case.v_new[3 * per_tok:] ^= np.uint16(0x0040)
+    out_b, _ = gpu_runner.run_attention(case, out_f32=True)
+    per_q = case.D * case.Hq
+    assert np.array_equal(out_a[: 3 * per_q], out_b[: 3 * per_q])
+    assert not np.array_equal(out_a[3 * per_q:], out_b[3 * per_q:])
+
+
+def test_split_count_independence(gpu):
+    """The same problem under two envelopes (different split plans) stays within tolerance of the
+    oracle both ways; the two differ only by the FP16 rounding of probabilities, which is relative
+    to each split's running maximum."""
+    case = AttnCase([9000], T=4, seed=13, max_context=200000)
+    _, ref = case.oracle_after_append()
+    out_small, _ = gpu_runner.run_attention(case, out_f32=True, envelope=(1, 9004))
+    out_large, _ = gpu_runner.run_attention(case, out_f32=True, envelope=(1, 200000))
+    _check_out(out_small, ref, REL_L2_F32)
+    _check_out(out_large, ref, REL_L2_F32)
+    assert rel_l2(out_small, out_large) < 1e-3
+
+
+def test_batch_ragged(gpu):
+    case = AttnCase([1024, 5000, 17, 3000], T=4, seed=21)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def _bfs_tree(n):
+    """Binary tree in BFS order pruned to n nodes: parent(u) = (u - 1) // 2."""
+    return [-1] + [(u - 1) // 2 for u in range(1, n)]
+
+
+def test_tree_attention(gpu):
+    parents = np.array([_bfs_tree(16), _bfs_tree(16)], dtype=np.int32).reshape(-1)
+    case = AttnCase([1500, 4000], T=16, seed=31, parents=parents)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, mode="TREE")
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def test_chain_tree_equals_causal(gpu):
+    T = 6
+    parents = np.array([-1] + list(range(T - 1)), dtype=np.int32)
+    case = AttnCase([2000], T=T, seed=32, parents=parents)
+    out_tree, _ = gpu_runner.run_attention(case, out_f32=True, mode="TREE")
+    out_causal, _ = gpu_runner.run_attention(case, out_f32=True, mode="A1")
+    assert np.array_equal(out_tree, out_causal)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(24, 4), (16, 2), (8, 8)])
+def test_other_group_sizes(gpu, Hq, Hkv):
+    case = AttnCase([1777], T=4, Hq=Hq, Hkv=Hkv, seed=40 + Hq)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
