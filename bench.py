@@ -1,0 +1,372 @@
+"""Benchmark of the MTP verify step on one MI355X.
+
+Workload ("C2"): one sequence, q_len 4 (3 drafts + 1), 40 query / 8 KV heads,
+head_dim 128, INT8 group-64 KV with FP16 scales, context 7,680, 64 layers with independent seeded
+KV (1.05 GB, larger than the 256 MB Infinity Cache), then greedy acceptance over a 248,320-row
+vocabulary with drafts 1..3 agreeing with the target argmax with probability 0.8 each. A "step"
+is one verify step: 64 layers of verify attention (quantize-append + split-K attention + merge)
+followed by argmax and greedy acceptance, replayed from one captured HIP graph with every input
+already resident in HBM.
+
+Also measured in the same run: the long-context layer (configs[2], "C3": context 260,096, 1%
+outliers at +-20), the top-20 stochastic sampler at batch 1 and batch 16 (configs[3] sampler
+shape: temperature 0.7, top-p 0.95, N(0, 3) logits), and the CPU oracle on the host as a reported
+baseline.
+
+Prints ONE JSON line. `value` is the C2 verify attention's achieved HBM bandwidth (algorithmic
+bytes / time, GB/s).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "verify µs/layer & HBM GB/s (INT8-KV, q_len=4, ctx 7.7K/260K); accept µs"
+HBM_PEAK_GBS = 8000.0
+HQ, HKV, D, T = 40, 8, 128, 4
+VOCAB = 248320
+BYTES_PER_TOKEN = 2 * HKV * (D + 2 * (D // 64))  # K+V codes + FP16 scales over 8 heads = 2,112
+
+
+def attn_bytes(L: int) -> int:
+    """Algorithmic bytes of one layer: codes+scales of all L+T visible keys, Q read, output write,
+    new BF16 K/V read and new codes+scales written (scratch excluded)."""
+    q = D * HQ * T * 2
+    out = D * HQ * T * 2
+    new_kv = D * HKV * T * 2 * 2
+    new_codes = T * HKV * 2 * (D + 2 * (D // 64))
+    return (L + T) * BYTES_PER_TOKEN + q + out + new_kv + new_codes
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Layer:
+    """One attention layer: its own cache planes, inputs, output and positions."""
+
+    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22):
+        import ninfer_amd as na
+        from ninfer_amd import ops, synthetic as syn
+        from ninfer_amd.device import DeviceArray, synchronize
+        from ninfer_amd.kv_cache import KVCacheLayer
+
+        self.L = L
+        self.cache = KVCacheLayer(max_context, HKV, D)
+        # History K/V: BF16 N(0,1) (optionally 1% outliers at +-20), quantized on the GPU in chunks.
+        rng = np.random.default_rng(seed)
+        per_tok = D * HKV
+        chunk = max(1, gen_chunk // per_tok)
+        for start in range(0, L, chunk):
+            n = min(chunk, L - start)
+            kv = []
+            for _ in range(2):
+                x = rng.standard_normal(n * per_tok, dtype=np.float32)
+                if outliers:
+                    sel = rng.random(n * per_tok) < 0.01
+                    x[sel] = np.where(rng.random(int(sel.sum())) < 0.5, -20.0, 20.0).astype(np.float32)
+                kv.append(syn.f32_to_bf16_bits(x))
+            dk = DeviceArray.from_numpy(na.BF16, kv[0], (D, HKV, n))
+            dv = DeviceArray.from_numpy(na.BF16, kv[1], (D, HKV, n))
+            dp = DeviceArray.from_numpy(na.I32, np.arange(start, start + n, dtype=np.int32), (n,))
+            ops.gqa_kv_append(dk.tensor(), dv.tensor(), dp.tensor(), self.cache.view())
+            synchronize()
+        self.q = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * T, dtype=np.float32)), (D, HQ, T))
+        self.k = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * T, dtype=np.float32)), (D, HKV, T))
+        self.v = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * T, dtype=np.float32)), (D, HKV, T))
+        self.pos = DeviceArray.from_numpy(na.I32, np.arange(L, L + T, dtype=np.int32), (T,))
+        self.out = DeviceArray(na.BF16, (D, HQ, T))
+        self.view = self.cache.view()
+        self.envelope = (1, max_context)
+
+    def launch(self, ws, stream):
+        from ninfer_amd import ops
+        ops.gqa_attention(self.q.tensor(), self.k.tensor(), self.v.tensor(), self.pos.tensor(),
+                          float(np.float32(1.0 / np.sqrt(D))), self.view, self.envelope, ws,
+                          self.out.tensor(), stream)
+
+
+def time_graph(graph, stream, reps, warmup):
+    from ninfer_amd.device import Event
+    for _ in range(warmup):
+        graph.launch()
+    stream.synchronize()
+    times = []
+    for _ in range(reps):
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        graph.launch()
+        e1.record(stream)
+        times.append(e0.elapsed_ms(e1))
+    stream.synchronize()
+    return float(np.median(times)), float(np.percentile(times, 95)), times
+
+
+def capture(stream, fn):
+    from ninfer_amd.device import Graph
+    g = Graph(stream)
+    with g:
+        fn()
+    return g
+
+
+def make_accept_inputs(B, K, seed, stochastic):
+    """Logits [V, K+1, B]. Greedy: N(0,4) with drafts agreeing with the planted argmax w.p. 0.8.
+    Stochastic: N(0,3) target logits, temperature 0.7, top-p 0.95."""
+    import ninfer_amd as na
+    from ninfer_amd import synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    rng = np.random.default_rng(seed)
+    std = np.sqrt(3.0) if stochastic else 2.0
+    logits = syn.f32_to_bf16_bits((rng.standard_normal((B, K + 1, VOCAB), dtype=np.float32) * std))
+    drafts = np.zeros((B, K), np.int32)
+    targets = np.zeros((B, K + 1), np.int32)
+    top_bits = syn.f32_to_bf16_bits(np.array([30.0], np.float32))[0]
+    for b in range(B):
+        for c in range(K + 1):
+            tok = int(rng.integers(0, VOCAB))
+            logits[b, c, tok] = top_bits  # planted maximum
+            targets[b, c] = tok
+            if c < K:
+                drafts[b, c] = tok if rng.random() < 0.8 else int(rng.integers(0, VOCAB))
+    dev = dict(
+        logits=DeviceArray.from_numpy(na.BF16, logits, (VOCAB, K + 1, B)),
+        drafts=DeviceArray.from_numpy(na.I32, drafts, (K, B)),
+        targets=DeviceArray(na.I32, (K + 1, B)),
+        length=DeviceArray.from_numpy(na.I32, np.full(B, 7680, np.int32), (B,)),
+        token=DeviceArray(na.I32, (B,)),
+        sampled=DeviceArray(na.I32, (K + 1, B)),
+        num=DeviceArray(na.I32, (B,)),
+        acc=DeviceArray(na.I32, (B,)),
+        stats=DeviceArray.from_numpy(na.I64, np.zeros((B, 4 + K), np.int64), (4 + K, B)),
+    )
+    cfgs = []
+    for b in range(B):
+        c = na.SamplingConfig()
+        if stochastic:
+            c.temperature, c.top_p, c.seed = 0.7, 0.95, int(seed * 1000 + b)
+        cfgs.append(c)
+    blob = b"".join(bytes(memoryview(c)) for c in cfgs)
+    cfg = DeviceBuffer(len(blob))
+    cfg.upload(np.frombuffer(blob, np.uint8))
+    dev["cfg"] = cfg
+    dev["ws"] = DeviceBuffer(max(256, __import__("ninfer_amd").ops.sampling_workspace_bytes(VOCAB, K + 1, B)))
+    dev["host"] = dict(logits=logits, drafts=drafts, targets=targets, cfgs=cfgs)
+    return dev
+
+
+def accept_launch(dev, stream, greedy_argmax):
+    from ninfer_amd import ops
+    if greedy_argmax:
+        ops.argmax(dev["logits"].tensor(), dev["targets"].tensor(), VOCAB, stream)
+    ops.speculative_accept_greedy_drafts(dev["targets"].tensor(), dev["logits"].tensor(), dev["drafts"].tensor(),
+                                         dev["length"].tensor(), dev["token"].tensor(), dev["sampled"].tensor(),
+                                         dev["num"].tensor(), dev["acc"].tensor(), dev["stats"].tensor(), VOCAB,
+                                         dev["cfg"].ptr, dev["ws"], stream)
+
+
+def cpu_baseline(sample_layers: int):
+    """Oracle attention on the host for `sample_layers` C2 layers (reported only)."""
+    from oracle import pyoracle
+    from ninfer_amd import synthetic as syn
+    from ninfer_amd.kv_cache import align_up
+    L, Pn = 7680, align_up(7684, 128)
+    rng = np.random.default_rng(99)
+    kc = rng.integers(-127, 128, (HKV, Pn, D)).astype(np.int8)
+    vc = rng.integers(-127, 128, (HKV, Pn, D)).astype(np.int8)
+    sc = np.float16(rng.uniform(0.01, 0.03, (HKV, Pn, 2))).view(np.uint16)
+    q = syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * T, dtype=np.float32))
+    pos = np.arange(L, L + T, dtype=np.int32)
+    threads = min(os.cpu_count() or 1, HKV)
+    t0 = time.perf_counter()
+    for _ in range(sample_layers):
+        pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=threads)
+    dt = (time.perf_counter() - t0) / sample_layers
+    t0 = time.perf_counter()
+    pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=1)
+    dt1 = time.perf_counter() - t0
+    # Sampler: one stochastic top-20 round over the full vocabulary on one core.
+    logits = syn.f32_to_bf16_bits(rng.standard_normal(VOCAB * T, dtype=np.float32) * np.float32(np.sqrt(3)))
+    cfg = pyoracle.SamplingConfig()
+    cfg.temperature, cfg.top_p, cfg.seed = 0.7, 0.95, 5
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        pyoracle.speculative_accept(None, logits, VOCAB, [1, 2, 3], 7680, [0] * 7, VOCAB, cfg)
+    ds = (time.perf_counter() - t0) / reps
+    return dict(us_per_layer=dt * 1e6, us_per_layer_1thread=dt1 * 1e6, threads=threads,
+                hardware_concurrency=os.cpu_count(), sampler_us_per_seq=ds * 1e6)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=64)
+    ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
+    ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--only", choices=["c2", "c3", "sampler"], default=None,
+                    help="profile helper: run one workload's replays and exit (no JSON line)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}). "
+              "The verify step shards by KV head or by context; see DESIGN.md.", file=sys.stderr)
+        sys.exit(2)
+
+    import ninfer_amd as na
+    from ninfer_amd import device, ops
+    from ninfer_amd.device import DeviceBuffer, Stream
+
+    log(f"device: {device.device_name()}")
+    stream = Stream()
+    result = {}
+
+    # ---- C2: 64 layers at context 7680 + greedy acceptance --------------------------------------
+    if args.only in (None, "c2"):
+        L2 = 7680
+        t0 = time.perf_counter()
+        layers = [Layer(L2, L2 + T, seed=1000 + i) for i in range(args.layers)]
+        log(f"C2: {args.layers} layers generated + quantized in {time.perf_counter() - t0:.1f}s")
+        ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L2 + T))
+        acc = make_accept_inputs(1, 3, seed=2, stochastic=False)
+        g_attn = capture(stream, lambda: [ly.launch(ws, stream) for ly in layers])
+        g_acc = capture(stream, lambda: accept_launch(acc, stream, greedy_argmax=True))
+
+        def step():
+            for ly in layers:
+                ly.launch(ws, stream)
+            accept_launch(acc, stream, greedy_argmax=True)
+        g_step = capture(stream, step)
+        attn_ms, attn_p95, _ = time_graph(g_attn, stream, args.steps, args.warmup)
+        acc_ms, acc_p95, _ = time_graph(g_acc, stream, args.steps, args.warmup)
+        step_ms, step_p95, _ = time_graph(g_step, stream, args.steps, args.warmup)
+        if args.only:
+            log(f"C2 attention {attn_ms / args.layers * 1e3:.2f} us/layer")
+            return
+        us_layer = attn_ms * 1e3 / args.layers
+        gbs = attn_bytes(L2) / (us_layer * 1e-6) / 1e9
+        # expected produced tokens per greedy round when each draft agrees w.p. 0.8 (prefix stops at
+        # the first disagreement): 1 + 0.8 + 0.8^2 + 0.8^3
+        produced = 1 + 0.8 + 0.8 ** 2 + 0.8 ** 3
+        host = acc["host"]
+        a_planted = 0
+        while a_planted < 3 and host["drafts"][0, a_planted] == host["targets"][0, a_planted]:
+            a_planted += 1
+        result["c2"] = dict(us_per_layer=us_layer, us_per_layer_p95=attn_p95 * 1e3 / args.layers, gbs=gbs,
+                            bytes_per_layer=attn_bytes(L2), accept_us=acc_ms * 1e3, accept_p95_us=acc_p95 * 1e3,
+                            step_ms=step_ms, step_p95_ms=step_p95, expected_tokens_per_step=produced,
+                            planted_accepted=a_planted, tokens_per_s=produced / (step_ms * 1e-3))
+        log(f"C2: {us_layer:.2f} us/layer, {gbs:.0f} GB/s, accept {acc_ms * 1e3:.1f} us, step {step_ms:.3f} ms")
+        del layers, g_attn, g_step
+        device.synchronize()
+
+    # ---- C3: one layer at context 260,096 -----------------------------------------------------------
+    if (args.only in (None, "c3")) and not args.skip_long:
+        L3 = 260096
+        t0 = time.perf_counter()
+        layer = Layer(L3, L3 + T, seed=3, outliers=True)
+        log(f"C3: layer generated + quantized in {time.perf_counter() - t0:.1f}s")
+        ws3 = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L3 + T))
+        g3 = capture(stream, lambda: layer.launch(ws3, stream))
+        ms3, p95_3, _ = time_graph(g3, stream, max(args.steps, 20), args.warmup)
+        if args.only:
+            log(f"C3 {ms3 * 1e3:.1f} us/layer")
+            return
+        gbs3 = attn_bytes(L3) / (ms3 * 1e-3) / 1e9
+        result["c3"] = dict(us_per_layer=ms3 * 1e3, us_per_layer_p95=p95_3 * 1e3, gbs=gbs3,
+                            bytes_per_layer=attn_bytes(L3), frac_of_peak=gbs3 / HBM_PEAK_GBS,
+                            target_us=attn_bytes(L3) / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6)
+        log(f"C3: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+        del layer, g3
+        device.synchronize()
+
+    # ---- sampler: top-20 stochastic acceptance at B=1 and B=16 --------------------------------------
+    if args.only in (None, "sampler"):
+        sres = {}
+        for B in (1, 16):
+            dev = make_accept_inputs(B, 3, seed=40 + B, stochastic=True)
+            g = capture(stream, lambda: accept_launch(dev, stream, greedy_argmax=False))
+            ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)
+            sres[f"b{B}_us"] = ms * 1e3
+            sres[f"b{B}_us_per_seq"] = ms * 1e3 / B
+            sres[f"b{B}_p95_us"] = p95 * 1e3
+        if args.only:
+            log(f"sampler {sres}")
+            return
+        result["sampler"] = sres
+        log(f"sampler: B=1 {sres['b1_us']:.1f} us, B=16 {sres['b16_us_per_seq']:.2f} us/seq")
+
+    cpu = None
+    if not args.skip_cpu:
+        t0 = time.perf_counter()
+        cpu = cpu_baseline(sample_layers=2)
+        log(f"CPU baseline in {time.perf_counter() - t0:.1f}s: {cpu}")
+
+    c2 = result["c2"]
+    line = {
+        "metric": METRIC,
+        "value": round(c2["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8 KV codes, fp16 MFMA, fp32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V quantized to INT8-G64; planted greedy logits)",
+        "config": {
+            "workload": "C2 verify step: batch 1, q_len 4, 40Q/8KV heads, head_dim 128, INT8-G64 KV, "
+                        "context 7680, 64 layers independent KV, greedy accept over vocab 248320",
+            "layers": args.layers, "context": 7680, "q_len": T, "q_heads": HQ, "kv_heads": HKV,
+            "head_dim": D, "vocab": VOCAB,
+        },
+        "us_per_layer": round(c2["us_per_layer"], 3),
+        "tokens_per_s": round(c2["tokens_per_s"], 1),
+        "accept_us": round(c2["accept_us"], 2),
+        "c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c2.items()},
+    }
+    if "c3" in result:
+        line["long_context"] = {"workload": "C3: context 260096, 1% outliers +-20, one layer",
+                                **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3"].items()}}
+    if "sampler" in result:
+        line["sampler"] = {"workload": "top-20 stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95",
+                           **{k: round(v, 2) for k, v in result["sampler"].items()}}
+    line["roofline"] = {
+        "bound": "hbm",
+        "achieved": round(c2["gbs"], 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "kernel": "verify attention op per layer (kv_quant_append + verify_attn_partial + verify_attn_merge)",
+        "bytes_per_launch": attn_bytes(7680),
+    }
+    if cpu is not None:
+        line["cpu_baseline"] = {
+            "value": round(attn_bytes(7680) / (cpu["us_per_layer"] * 1e-6) / 1e9, 3),
+            "unit": "GB/s",
+            "cores": cpu["threads"],
+            "kind": "port",
+            "sample": "oracle FP64 attention, 2 C2 layers (context 7680, 40Q/8KV, q_len 4), threads over KV heads",
+            "us_per_layer": round(cpu["us_per_layer"], 1),
+            "us_per_layer_1thread": round(cpu["us_per_layer_1thread"], 1),
+            "hardware_concurrency": cpu["hardware_concurrency"],
+            "sampler_us_per_seq_1thread": round(cpu["sampler_us_per_seq"], 1),
+        }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
