@@ -179,11 +179,9 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
         require_built(c, op);
         const SplitPlan plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys);
         require_workspace(ws, ws_bytes, plan.bytes, op);
-        if (write_cache) {
-            launch_kv_append(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                             static_cast<const int32_t*>(positions->data), nullptr, s.T, c, stream);
-        }
         launch_verify_attention(static_cast<const uint16_t*>(q->data),
+                                write_cache ? static_cast<const uint16_t*>(k->data) : nullptr,
+                                write_cache ? static_cast<const uint16_t*>(v->data) : nullptr,
                                 static_cast<const int32_t*>(positions->data),
                                 parents ? static_cast<const int32_t*>(parents->data) : nullptr, s.T,
                                 s.Hq, c, scale, env.max_visible_keys, ws, plan, out->data,

@@ -45,11 +45,13 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
                       const int32_t* count, int32_t T, const CacheRef& cache, hipStream_t stream);
 
-// Split-K verify attention over cache rows; parents == nullptr is the causal mask.
-void launch_verify_attention(const uint16_t* q, const int32_t* positions, const int32_t* parents,
-                             int32_t T, int32_t Hq, const CacheRef& cache, float scale,
-                             uint32_t max_keys, void* workspace, const SplitPlan& plan, void* out,
-                             bool out_f32, hipStream_t stream);
+// Split-K verify attention over cache rows; parents == nullptr is the causal mask. With k_new/v_new
+// (A1) the new columns are quantized into rows positions[t] first, by the owning split.
+void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                             const int32_t* positions, const int32_t* parents, int32_t T,
+                             int32_t Hq, const CacheRef& cache, float scale, uint32_t max_keys,
+                             void* workspace, const SplitPlan& plan, void* out, bool out_f32,
+                             hipStream_t stream);
 
 // Commit helpers (kv_commit.hip).
 void launch_kv_rollback(const int32_t* positions, const int32_t* keep_count, int32_t T,

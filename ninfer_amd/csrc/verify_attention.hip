@@ -3,21 +3,27 @@
 // Semantics (reference include/ninfer/ops/gqa_attention.h:52-91): for sequence b, query token t
 // and query head qh (KV head h = qh / G), attend over cache rows [0, positions[0]) plus the new
 // rows positions[u] with u visible from t (u <= t causal; u an ancestor-or-self of t for trees),
-// reading INT8-G64 codes with FP16 scales. Split-K over keys with an online softmax per split and
-// a log-sum-exp merge (reference split reducer src/ops/kernel/gqa_attention_decode.cuh:144-227).
+// reading INT8-G64 codes with FP16 scales. A1 first quantizes the new K/V columns into their rows
+// (the split owning a row writes it, as the reference's decode kernel does,
+// src/ops/kernel/gqa_attention_decode_i8.cuh:168-209). Split-K over keys with an online softmax
+// per split and a log-sum-exp merge (reference reducer src/ops/kernel/gqa_attention_decode.cuh:
+// 144-227).
 //
 // MI355X design:
-//  * One workgroup = 4 waves = one (sequence, row chunk, KV head, key split). Each wave streams
-//    32-key chunks (chunk w, w+4, ...) with 128-bit loads straight into MFMA operand registers,
-//    double buffered; no LDS on the hot path.
+//  * One workgroup = 4 waves = one (sequence, row chunk, KV head, key split); 2 workgroups per CU.
+//    Each wave streams 32-key chunks (chunk w, w+4, ...). A chunk (K codes, V codes, FP16 scales:
+//    8,448 bytes) moves HBM -> LDS by asynchronous global_load_lds DMA into a per-wave two-stage
+//    ring with a lookahead of two chunks: 16.5 KB per wave, 132 KB per CU stay in flight while
+//    the current chunk is computed, at no VGPR cost.
 //  * QK^T runs as S^T = K * Q^T on v_mfma_f32_16x16x32_f16: K codes (exact in FP16) are the A
-//    operand (16 keys x 32 dims per step, each 32-dim step inside one 64-wide quant group), Q
-//    (BF16 -> FP16 exact after a per-row power-of-two rescale) is the B operand. Each quant group
-//    accumulates separately so the per-(key, group) FP16 scale is applied exactly in FP32.
+//    operand, Q (BF16 -> FP16 exact after a per-row power-of-two rescale) the B operand. Each
+//    32-dim MFMA step stays inside one 64-wide quant group and each group accumulates separately,
+//    so the per-(key, group) FP16 scale is applied exactly in FP32. The K DMA writes LDS in MFMA
+//    operand order, so every lane reads its own 16 bytes (conflict-free ds_read_b128).
 //  * PV runs as O^T = V^T * P^T on the same instruction. The S^T accumulator layout (lane = query
 //    row, 4 keys per 16-key tile) is exactly the B-operand layout of P^T, so probabilities never
-//    leave registers. V is the A operand with the dimension permutation d = 8*lane16 + tile: each
-//    lane loads 8 bytes per key (fully coalesced 128 B rows) and transposes in registers.
+//    leave registers. V rows land in LDS in their natural layout; each lane reads 8 bytes of 8 keys
+//    (dims 8c..8c+7) and transposes in registers with SDWA converts.
 //  * GQA x q_len rows (5 x 4 = 20 for the 40/8 geometry) are padded to two 16-row MFMA tiles.
 #include "common.h"
 #include "device_utils.h"
@@ -26,20 +32,32 @@
 #include <algorithm>
 #include <cmath>
 
+#define NMI_AS1 __attribute__((address_space(1)))
+#define NMI_AS3 __attribute__((address_space(3)))
+
 namespace nmi {
 namespace {
 
 constexpr int kWaves = 4;
 constexpr int kChunk = 32;
+constexpr int kStageK = 0;       // 4 x 1 KB, MFMA operand order
+constexpr int kStageV = 4096;    // 32 rows x 128 B, natural order
+constexpr int kStageS = 8192;    // 32 K scale words then 32 V scale words
+constexpr int kStageBytes = 8448;
+constexpr int kSmemBytes = kWaves * 2 * kStageBytes; // 67,584 B; the epilogue merge reuses it
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 struct AttnArgs {
     const uint16_t* q;
+    const uint16_t* k_new; // fused A1 append (single row chunk only): BF16 [D, Hkv, T, B]
+    const uint16_t* v_new;
     const int32_t* positions;
     const int32_t* parents;
-    const int8_t* kc;
-    const int8_t* vc;
-    const uint16_t* ks;
-    const uint16_t* vs;
+    int8_t* kc;
+    int8_t* vc;
+    uint16_t* ks;
+    uint16_t* vs;
     float* part_o;  // [unit][nsplit][32][D]
     float* part_ml; // [unit][nsplit][32][2]
     int64_t code_seq;
@@ -81,53 +99,10 @@ __device__ __forceinline__ h8 cvt_codes8(int lo, int hi) {
     return __builtin_bit_cast(h8, w);
 }
 
-// Byte (t & 3) of word (t >> 2) from key slots 2w and 2w+1 -> packed FP16 pair (V transpose).
+// Byte (T & 3) of word (T >> 2) from key slots 2w and 2w+1 -> packed FP16 pair (V transpose).
 template <int T>
 __device__ __forceinline__ uint32_t v_pair(const i2& a, const i2& b) {
     return i8x2_to_f16x2<T & 3>(static_cast<uint32_t>(a[T >> 2]), static_cast<uint32_t>(b[T >> 2]));
-}
-
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-
-// K half of a 32-key chunk: lane (c, g) holds key tile kt's row c0+16kt+c at dims 64gq+16g..+15,
-// and the FP16 scales of keys c0+16kt+4g..+3 (both groups, interleaved per key).
-template <int D>
-struct KRegs {
-    i4 k[2][D / 64];
-    i4 sc[2];
-};
-// V half: 8 key slots (4g+j and 16+4g+j) x 8 dims at d = 8c..8c+7, plus the same scale words.
-struct VRegs {
-    i2 v[8];
-    i4 sc[2];
-};
-
-template <int D>
-__device__ __forceinline__ void load_k(KRegs<D>& r, const int8_t* kbase, const uint16_t* ksbase,
-                                       int c0, int c, int g) {
-    constexpr int G = D / 64;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-        const int8_t* krow = kbase + static_cast<int64_t>(c0 + 16 * kt + c) * D + 16 * g;
-#pragma unroll
-        for (int gq = 0; gq < G; ++gq) { r.k[kt][gq] = *reinterpret_cast<const i4*>(krow + 64 * gq); }
-        r.sc[kt] = *reinterpret_cast<const i4*>(ksbase + static_cast<int64_t>(c0 + 16 * kt + 4 * g) * G);
-    }
-}
-
-template <int D>
-__device__ __forceinline__ void load_v(VRegs& r, const int8_t* vbase, const uint16_t* vsbase, int c0,
-                                       int c, int g) {
-    constexpr int G = D / 64;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
-        r.v[j] = *reinterpret_cast<const i2*>(vbase + static_cast<int64_t>(key) * D + 8 * c);
-    }
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-        r.sc[kt] = *reinterpret_cast<const i4*>(vsbase + static_cast<int64_t>(c0 + 16 * kt + 4 * g) * G);
-    }
 }
 
 __device__ __forceinline__ _Float16 half_bits_at(const i4& v, int idx) {
@@ -135,26 +110,85 @@ __device__ __forceinline__ _Float16 half_bits_at(const i4& v, int idx) {
     return __builtin_bit_cast(_Float16, static_cast<uint16_t>((idx & 1) ? (word >> 16) : (word & 0xffffu)));
 }
 
-__device__ __forceinline__ float half_at(const i4& v, int idx) {
-    const int word = v[idx >> 1];
-    const uint16_t bits = static_cast<uint16_t>((idx & 1) ? (static_cast<uint32_t>(word) >> 16)
-                                                          : (static_cast<uint32_t>(word) & 0xffffu));
-    return f16_bits_to_f32(bits);
+// Issue the DMA of one 32-key chunk (the caller guarantees c0 + 32 <= P) into `stage`.
+__device__ __forceinline__ void issue_chunk(NMI_AS3 char* stage, const int8_t* kbase, const int8_t* vbase,
+                                            const uint16_t* ksbase, const uint16_t* vsbase, int c0,
+                                            int lane) {
+    const int c = lane & 15;
+    const int g = lane >> 4;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) {
+            const int8_t* src = kbase + static_cast<int64_t>(c0 + 16 * kt + c) * 128 + 64 * gq + 16 * g;
+            __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(stage + kStageK + (2 * kt + gq) * 1024), 16, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r8 = 0; r8 < 4; ++r8) {
+        const int8_t* src = vbase + static_cast<int64_t>(c0 + 8 * r8 + (lane >> 3)) * 128 + 16 * (lane & 7);
+        __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(stage + kStageV + r8 * 1024), 16, 0, 0);
+    }
+    const uint16_t* ssrc = (lane < 32 ? ksbase + static_cast<int64_t>(c0 + lane) * 2 : vsbase + static_cast<int64_t>(c0 + lane - 32) * 2);
+    __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)ssrc, (NMI_AS3 void*)(stage + kStageS), 4, 0, 0);
 }
 
-template <int D, int NT>
+// Quantize-append one new token row of one KV head (one wave: lane owns dims lane and lane + 64 of
+// K and V), reference contract include/ninfer/ops/gqa_attention.h:25-30.
+__device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t* vsrc, int8_t* kdst,
+                                           int8_t* vdst, uint16_t* ksdst, uint16_t* vsdst, int lane) {
+    const float x[4] = {bf16_to_f32(ksrc[lane]), bf16_to_f32(ksrc[64 + lane]), bf16_to_f32(vsrc[lane]),
+                        bf16_to_f32(vsrc[64 + lane])};
+    uint16_t sbits[4];
+    int8_t code[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float amax = wave_max(fabsf(x[i]));
+        sbits[i] = f32_to_f16_bits(amax > 0.0f ? amax / 127.0f : 0.0f);
+        const float s = f16_bits_to_f32(sbits[i]);
+        const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+        float r = inv != 0.0f ? rintf(x[i] * inv) : 0.0f;
+        r = fminf(127.0f, fmaxf(-127.0f, r));
+        code[i] = static_cast<int8_t>(r);
+    }
+    kdst[lane] = code[0];
+    kdst[64 + lane] = code[1];
+    vdst[lane] = code[2];
+    vdst[64 + lane] = code[3];
+    if (lane == 0) {
+        *reinterpret_cast<uint32_t*>(ksdst) = static_cast<uint32_t>(sbits[0]) | (static_cast<uint32_t>(sbits[1]) << 16);
+        *reinterpret_cast<uint32_t*>(vsdst) = static_cast<uint32_t>(sbits[2]) | (static_cast<uint32_t>(sbits[3]) << 16);
+    }
+}
+
+template <int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void verify_attn_partial_kernel(AttnArgs a) {
-    static_assert(D == 128, "head_dim 128 kernel");
-    constexpr int G = D / 64;
+    constexpr int D = 128;
+    constexpr int G = 2;       // quant groups per row
     constexpr int DT = D / 16; // O^T tiles of 16 dims
+    __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
     const int split = blockIdx.x;
     const int h = blockIdx.y;
     const int b = blockIdx.z / a.row_chunks;
     const int rc = blockIdx.z - b * a.row_chunks;
+    const int k0 = split * a.kps;
+
+    const int64_t head_code = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
+    const int64_t head_scale = static_cast<int64_t>(b) * a.scale_seq + static_cast<int64_t>(h) * a.P * G;
+    int8_t* kbase = a.kc + head_code;
+    int8_t* vbase = a.vc + head_code;
+    uint16_t* ksbase = a.ks + head_scale;
+    uint16_t* vsbase = a.vs + head_scale;
+    NMI_AS3 char* my_stage0 = (NMI_AS3 char*)smem + wave * 2 * kStageBytes;
+
+    // The first chunk does not depend on the positions: start its DMA right away.
+    const int first = k0 + kChunk * wave;
+    if (first + kChunk <= a.P) { issue_chunk(my_stage0, kbase, vbase, ksbase, vsbase, first, lane); }
 
     const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
     const int32_t* par = a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr;
@@ -163,14 +197,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int t0 = rc * a.tokens_per_chunk;
     const int Tc = min(a.tokens_per_chunk, a.T - t0);
     const int R = Tc * a.G;
-    const int k0 = split * a.kps;
     const int k1 = min(k0 + a.kps, window);
     const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
     const int64_t pidx = unit * a.nsplit + split;
     float* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
 
+    // ---- fused A1 append: this split writes the new rows inside [k0, k0 + kps). Only launched
+    // with a single row chunk, so no other workgroup reads these rows concurrently.
+    if (a.k_new != nullptr) {
+        bool owner = false;
+        for (int t = 0; t < a.T; ++t) {
+            const int p = pos[t];
+            const bool mine = p >= k0 && p < k0 + a.kps && p >= 0 && p < a.P;
+            owner |= mine;
+            if (mine && (t & (kWaves - 1)) == wave) {
+                const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (t + static_cast<int64_t>(a.T) * b));
+                append_row(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D,
+                           vbase + static_cast<int64_t>(p) * D, ksbase + static_cast<int64_t>(p) * G,
+                           vsbase + static_cast<int64_t>(p) * G, lane);
+            }
+        }
+        if (owner) {
+            // Stores visible (and this CU's L1 invalidated) before any DMA of the new rows.
+            __threadfence();
+            __syncthreads();
+            if (first + kChunk <= a.P && first < pos[a.T - 1] + 1 && first + kChunk > pos[0]) {
+                issue_chunk(my_stage0, kbase, vbase, ksbase, vsbase, first, lane); // re-fetch
+            }
+        }
+    }
+
     if (k0 >= k1) {
+        __builtin_amdgcn_s_waitcnt(0);
         if (threadIdx.x < 32) {
             out_ml[2 * threadIdx.x] = -INFINITY;
             out_ml[2 * threadIdx.x + 1] = 0.0f;
@@ -227,13 +286,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         nmask[nt] = valid ? new_key_mask(par, t) : 0u;
     }
 
-    const int64_t head_code = (static_cast<int64_t>(b) * a.code_seq) + static_cast<int64_t>(h) * a.P * D;
-    const int64_t head_scale = (static_cast<int64_t>(b) * a.scale_seq) + static_cast<int64_t>(h) * a.P * G;
-    const int8_t* kbase = a.kc + head_code;
-    const int8_t* vbase = a.vc + head_code;
-    const uint16_t* ksbase = a.ks + head_scale;
-    const uint16_t* vsbase = a.vs + head_scale;
-
     float m[NT];
     float l[NT];
     f4 O[NT][DT];
@@ -246,21 +298,45 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 
     const int hist_end = min(L, k1); // keys below this are visible to every row
-    const int vgroup = (8 * c) / 64; // quant group of this lane's V dims (D == 128)
+    const int vgroup = c >> 3;       // quant group of this lane's V dims 8c..8c+7
 
-    // Software pipeline with one register set per operand: the next chunk's K is requested as soon
-    // as this chunk's QK^T has consumed K, and its V as soon as PV has consumed V.
-    KRegs<D> kr;
-    VRegs vr;
-    int c0 = k0 + kChunk * wave;
-    if (c0 < k1) {
-        load_k<D>(kr, kbase, ksbase, c0, c, g);
-        load_v<D>(vr, vbase, vsbase, c0, c, g);
-    }
+    // Lookahead of two chunks: while chunk i is computed, chunks i+1 and i+2 are in flight. Chunk
+    // i+2 reuses chunk i's stage once chunk i sits in registers.
+    constexpr int kStride = kChunk * kWaves;
+    if (first + kStride < k1) { issue_chunk(my_stage0 + kStageBytes, kbase, vbase, ksbase, vsbase, first + kStride, lane); }
+    int stage = 0;
 #pragma unroll 1
-    while (c0 < k1) {
-        const int c1 = c0 + kChunk * kWaves;
-        const bool more = c1 < k1;
+    for (int c0 = first; c0 < k1; c0 += kStride) {
+        NMI_AS3 char* st = my_stage0 + stage * kStageBytes;
+        // Wait for this chunk's 9 DMA instructions; the next chunk's 9 may stay outstanding.
+        if (c0 + kStride < k1) {
+            __builtin_amdgcn_s_waitcnt(0x0f79); // vmcnt(9)
+        } else {
+            __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+        }
+        i4 kr[2][G];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int gq = 0; gq < G; ++gq) { kr[kt][gq] = *(NMI_AS3 const i4*)(st + kStageK + (2 * kt + gq) * 1024 + 16 * lane); }
+        }
+        const i4 ksw0 = *(NMI_AS3 const i4*)(st + kStageS + (4 * g) * 4);
+        const i4 ksw1 = *(NMI_AS3 const i4*)(st + kStageS + (16 + 4 * g) * 4);
+        const i4 vsw0 = *(NMI_AS3 const i4*)(st + kStageS + 128 + (4 * g) * 4);
+        const i4 vsw1 = *(NMI_AS3 const i4*)(st + kStageS + 128 + (16 + 4 * g) * 4);
+        i2 vr[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+            vr[j] = *(NMI_AS3 const i2*)(st + kStageV + row * 128 + 8 * c);
+        }
+        // Chunk i is in registers once these reads retire; then its stage takes chunk i+2.
+        const int c2 = c0 + 2 * kStride;
+        if (c2 < k1) {
+            __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
+            issue_chunk(st, kbase, vbase, ksbase, vsbase, c2, lane);
+        }
+        stage ^= 1;
 
         // ---- S^T = K Q^T per quant group
         f4 sacc[2][NT][G];
@@ -268,8 +344,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
             for (int gq = 0; gq < G; ++gq) {
-                const h8 ka0 = cvt_codes8(kr.k[kt][gq][0], kr.k[kt][gq][1]);
-                const h8 ka1 = cvt_codes8(kr.k[kt][gq][2], kr.k[kt][gq][3]);
+                const h8 ka0 = cvt_codes8(kr[kt][gq][0], kr[kt][gq][1]);
+                const h8 ka1 = cvt_codes8(kr[kt][gq][2], kr[kt][gq][3]);
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt) {
                     f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka0, qop[nt][gq][0], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -277,16 +353,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 }
             }
         }
-        float kscale[2][4][G];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-#pragma unroll
-                for (int gq = 0; gq < G; ++gq) { kscale[kt][e][gq] = static_cast<float>(half_bits_at(kr.sc[kt], G * e + gq)); }
-            }
-        }
-        if (more) { load_k<D>(kr, kbase, ksbase, c1, c, g); }
 
         const bool full = (c0 + kChunk) <= hist_end;
         h8 pop[NT];
@@ -296,11 +362,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             float cmax = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
+                const i4& ksw = kt ? ksw1 : ksw0;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float s = 0.0f;
-#pragma unroll
-                    for (int gq = 0; gq < G; ++gq) { s = fmaf(kscale[kt][e][gq], sacc[kt][nt][gq][e], s); }
+                    float s = static_cast<float>(half_bits_at(ksw, 2 * e)) * sacc[kt][nt][0][e];
+                    s = fmaf(static_cast<float>(half_bits_at(ksw, 2 * e + 1)), sacc[kt][nt][1][e], s);
                     s *= rowmul[nt];
                     if (!full) {
                         const int key = c0 + 16 * kt + 4 * g + e;
@@ -318,32 +384,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             cmax = group4_max(cmax);
             const float mnew = fmaxf(m[nt], cmax);
             const bool live = mnew != -INFINITY;
-            const float alpha = live ? __builtin_amdgcn_exp2f(m[nt] - mnew) : 1.0f;
+            // Probabilities carry a 2^15 factor (exact in FP16, cancels in O / l) so the PV operand
+            // stays in FP16's normal range down to 2^-29 of the row maximum.
+            const float mref = mnew - 15.0f;
             float lsum = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float pe = live ? __builtin_amdgcn_exp2f(sv[kt][e] - mnew) : 0.0f;
+                    const float pe = live ? __builtin_amdgcn_exp2f(sv[kt][e] - mref) : 0.0f;
                     lsum += pe;
-                    pop[nt][4 * kt + e] = static_cast<_Float16>(pe * 32768.0f);
+                    pop[nt][4 * kt + e] = static_cast<_Float16>(pe);
                 }
             }
-            l[nt] = l[nt] * alpha + lsum;
-            m[nt] = mnew;
+            const bool grew = mnew > m[nt];
+            if (__any(grew)) {
+                const float alpha = grew ? __builtin_amdgcn_exp2f(m[nt] - mnew) : 1.0f;
+                l[nt] *= alpha;
 #pragma unroll
-            for (int t = 0; t < DT; ++t) { O[nt][t] *= alpha; }
+                for (int t = 0; t < DT; ++t) { O[nt][t] *= alpha; }
+            }
+            l[nt] += lsum;
+            m[nt] = mnew;
         }
 
         // ---- O^T += V^T P^T. V' = FP16(code * scale): codes convert exactly, one packed multiply
-        // rounds the product once.
+        // rounds the product once. Keys past the range end get a zero scale (their rows may be
+        // uninitialized).
         h2 vsp[4];
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
 #pragma unroll
             for (int h1 = 0; h1 < 2; ++h1) {
                 const int j = 2 * w + h1;
-                vsp[w][h1] = half_bits_at(vr.sc[j >> 2], G * (j & 3) + vgroup);
+                vsp[w][h1] = half_bits_at(j < 4 ? vsw0 : vsw1, 2 * (j & 3) + vgroup);
             }
         }
         if (!full) {
@@ -353,12 +427,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 if (key >= k1) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
             }
         }
-        static_assert(DT == 8, "V transpose is written for 8 tiles");
 #define NMI_PV_TILE(TT)                                                                            \
     {                                                                                              \
         h2 pr[4];                                                                                  \
         _Pragma("unroll") for (int w = 0; w < 4; ++w) {                                            \
-            pr[w] = __builtin_bit_cast(h2, v_pair<TT>(vr.v[2 * w], vr.v[2 * w + 1])) * vsp[w];     \
+            pr[w] = __builtin_bit_cast(h2, v_pair<TT>(vr[2 * w], vr[2 * w + 1])) * vsp[w];         \
         }                                                                                          \
         const h8 va = __builtin_bit_cast(h8, pr);                                                  \
         _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                        \
@@ -374,35 +447,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         NMI_PV_TILE(6)
         NMI_PV_TILE(7)
 #undef NMI_PV_TILE
-        if (more) { load_v<D>(vr, vbase, vsbase, c1, c, g); }
-        c0 = c1;
     }
 
-    // ---- merge the four waves through LDS, then write this split's partial.
-    __shared__ float sm_o[kWaves][32][D + 1];
-    __shared__ float sm_m[kWaves][32];
-    __shared__ float sm_l[kWaves][32];
+    // ---- merge the four waves through LDS (reusing the staging ring), then write the partial.
+    __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
+    __syncthreads();
+    float* sm_o = reinterpret_cast<float*>(smem);      // [kWaves][32][D + 1]
+    float* sm_m = sm_o + kWaves * 32 * (D + 1);        // [kWaves][32]
+    float* sm_l = sm_m + kWaves * 32;                  // [kWaves][32]
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const float lt = group4_sum(l[nt]);
         const int r = 16 * nt + c;
         if (g == 0) {
-            sm_m[wave][r] = m[nt];
-            sm_l[wave][r] = lt;
+            sm_m[wave * 32 + r] = m[nt];
+            sm_l[wave * 32 + r] = lt;
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 // O^T tile t row (4g + e) is dim 8*(4g + e) + t.
-                sm_o[wave][r][8 * (4 * g + e) + t] = O[nt][t][e];
+                sm_o[(wave * 32 + r) * (D + 1) + 8 * (4 * g + e) + t] = O[nt][t][e];
             }
-        }
-    }
-    for (int r = NT * 16 + threadIdx.x; r < 32; r += blockDim.x) {
-        for (int w = 0; w < kWaves; ++w) {
-            sm_m[w][r] = -INFINITY;
-            sm_l[w][r] = 0.0f;
         }
     }
     __syncthreads();
@@ -411,17 +478,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int d = idx - r * D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w][r]); }
+        for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
         float o = 0.0f;
         float lsum = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const float mw = sm_m[w][r];
+                const float mw = sm_m[w * 32 + r];
                 if (mw == -INFINITY) { continue; }
                 const float wgt = __builtin_amdgcn_exp2f(mw - M);
-                o = fmaf(sm_o[w][r][d], wgt, o);
-                lsum = fmaf(sm_l[w][r], wgt, lsum);
+                o = fmaf(sm_o[(w * 32 + r) * (D + 1) + d], wgt, o);
+                lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
             }
         }
         out_o[r * D + d] = o;
@@ -443,14 +510,22 @@ struct MergeArgs {
     int32_t tokens_per_chunk;
     int32_t row_chunks;
     int32_t nsplit;
-    float out_scale; // undoes the 2^15 probability scaling of the PV operand
     int32_t out_f32;
 };
 
+constexpr int kMergeThreads = 256;
+constexpr int kMergeMaxSplits = 2048;
+
 // Log-sum-exp merge over splits (reference src/ops/kernel/gqa_attention_decode.cuh:144-227,
-// including "every split empty => 0").
+// including "every split empty => 0"). One block per output row (b, t, qh): the first 32 splits'
+// partial rows are requested up front, every split's (m, l) becomes a weight in LDS through block
+// reductions, then two thread halves accumulate alternate splits.
 template <int D>
-__global__ __launch_bounds__(D) void verify_attn_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
+    __shared__ float wts[kMergeMaxSplits];
+    __shared__ float lw[kMergeMaxSplits];
+    __shared__ float red[kMergeThreads / 64];
+    __shared__ float half_o[D];
     const int row_id = blockIdx.x; // (b, t, qh)
     const int qh = row_id % a.Hq;
     const int t = (row_id / a.Hq) % a.T;
@@ -462,35 +537,75 @@ __global__ __launch_bounds__(D) void verify_attn_merge_kernel(MergeArgs a) {
     const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
     const float* ml = a.part_ml + unit * a.nsplit * 64;
     const float* po = a.part_o + unit * a.nsplit * (32 * D);
-    const int d = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
 
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; ++s) {
-        if (ml[s * 64 + 2 * r + 1] > 0.0f) { M = fmaxf(M, ml[s * 64 + 2 * r]); }
+    // Issue the first partial-row loads before any reduction: thread (half, d) owns splits
+    // s = half + 2k.
+    constexpr int kPre = 16;
+    const int half = tid / D;
+    const int d = tid - half * D;
+    float pre[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+        const int s = half + 2 * k;
+        pre[k] = s < a.nsplit ? po[static_cast<int64_t>(s) * 32 * D + r * D + d] : 0.0f;
     }
-    float o = 0.0f;
+    float M = -INFINITY;
+    for (int s = tid; s < a.nsplit; s += kMergeThreads) {
+        const float ls = ml[s * 64 + 2 * r + 1];
+        const float ms = ml[s * 64 + 2 * r];
+        wts[s] = ls > 0.0f ? ms : -INFINITY;
+        lw[s] = ls;
+        M = fmaxf(M, wts[s]);
+    }
+    M = wave_max(M);
+    if (lane == 0) { red[wave] = M; }
+    __syncthreads();
+    M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
     float lsum = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < a.nsplit; ++s) {
-            const float ls = ml[s * 64 + 2 * r + 1];
-            if (!(ls > 0.0f)) { continue; }
-            const float w = __builtin_amdgcn_exp2f(ml[s * 64 + 2 * r] - M);
-            lsum = fmaf(ls, w, lsum);
-            o = fmaf(po[static_cast<int64_t>(s) * 32 * D + r * D + d], w, o);
+    for (int s = tid; s < a.nsplit; s += kMergeThreads) {
+        const float w = (M != -INFINITY && wts[s] != -INFINITY) ? __builtin_amdgcn_exp2f(wts[s] - M) : 0.0f;
+        wts[s] = w;
+        lsum = fmaf(lw[s], w, lsum);
+    }
+    lsum = wave_sum(lsum);
+    if (lane == 0) { red[wave] = lsum; }
+    __syncthreads();
+    lsum = (red[0] + red[1]) + (red[2] + red[3]);
+
+    float o = 0.0f;
+    if (lsum > 0.0f) {
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int s = half + 2 * k;
+            if (s < a.nsplit) { o = fmaf(pre[k], wts[s], o); }
+        }
+#pragma unroll 4
+        for (int s = half + 2 * kPre; s < a.nsplit; s += 2) {
+            o = fmaf(po[static_cast<int64_t>(s) * 32 * D + r * D + d], wts[s], o);
         }
     }
-    const float val = lsum > 0.0f ? (o / lsum) * a.out_scale : 0.0f;
-    const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
-    if (a.out_f32) {
-        static_cast<float*>(a.out)[oi] = val;
-    } else {
-        static_cast<uint16_t*>(a.out)[oi] = f32_to_bf16_bits(val);
+    if (half == 1) { half_o[d] = o; }
+    __syncthreads();
+    if (half == 0) {
+        o += half_o[d];
+        const float val = lsum > 0.0f ? o / lsum : 0.0f;
+        const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
+        if (a.out_f32) {
+            static_cast<float*>(a.out)[oi] = val;
+        } else {
+            static_cast<uint16_t*>(a.out)[oi] = f32_to_bf16_bits(val);
+        }
     }
 }
 
-// INT8-G64 encoder (reference contract include/ninfer/ops/gqa_attention.h:25-30; device encoder
-// src/ops/kernel/gqa_attention_decode_i8.cuh:168-209). One wave per (KV head, K|V, group): lane i
-// owns element i of the 64-element group.
+// INT8-G64 encoder for A2, the prefix commit and multi-row-chunk A1 (reference contract
+// include/ninfer/ops/gqa_attention.h:25-30; device encoder
+// src/ops/kernel/gqa_attention_decode_i8.cuh:168-209). Block (t, b, h): one wave per (K|V, group),
+// lane i owns element i of the 64-element group.
 template <int D>
 __global__ __launch_bounds__(256) void kv_quant_append_kernel(const uint16_t* k, const uint16_t* v,
                                                               const int32_t* positions,
@@ -502,17 +617,14 @@ __global__ __launch_bounds__(256) void kv_quant_append_kernel(const uint16_t* k,
     constexpr int G = D / 64;
     const int t = blockIdx.x;
     const int b = blockIdx.y;
+    const int h = blockIdx.z;
     if (count != nullptr && t >= count[b]) { return; }
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     const int pos = positions[static_cast<int64_t>(b) * T + t];
     if (pos < 0 || pos >= P) { return; }
-    const int units = Hkv * 2 * G;
-    for (int unit = wave; unit < units; unit += blockDim.x / 64) {
-        const int h = unit / (2 * G);
-        const int rem = unit - h * 2 * G;
-        const int which = rem / G;
-        const int grp = rem - which * G;
+    for (int unit = threadIdx.x >> 6; unit < 2 * G; unit += blockDim.x / 64) {
+        const int which = unit / G;
+        const int grp = unit - which * G;
         const uint16_t* src = (which ? v : k) + static_cast<int64_t>(D) * (h + static_cast<int64_t>(Hkv) * (t + static_cast<int64_t>(T) * b)) + grp * 64;
         const float x = bf16_to_f32(src[lane]);
         const float amax = wave_max(fabsf(x));
@@ -563,20 +675,30 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
                       const int32_t* count, int32_t T, const CacheRef& c, hipStream_t stream) {
     if (c.D != 128) { throw Unsupported("kv append: only head_dim 128 is built"); }
-    dim3 grid(T, c.B);
+    dim3 grid(T, c.B, c.Hkv);
     hipLaunchKernelGGL(kv_quant_append_kernel<128>, grid, dim3(256), 0, stream, k, v, positions,
                        count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
     check_launch("kv_quant_append_kernel");
 }
 
-void launch_verify_attention(const uint16_t* q, const int32_t* positions, const int32_t* parents,
-                             int32_t T, int32_t Hq, const CacheRef& c, float scale,
-                             uint32_t max_keys, void* workspace, const SplitPlan& plan, void* out,
-                             bool out_f32, hipStream_t stream) {
+void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uint16_t* v_new,
+                             const int32_t* positions, const int32_t* parents, int32_t T,
+                             int32_t Hq, const CacheRef& c, float scale, uint32_t max_keys,
+                             void* workspace, const SplitPlan& plan, void* out, bool out_f32,
+                             hipStream_t stream) {
     if (c.D != 128) { throw Unsupported("verify attention: only head_dim 128 is built"); }
+    if (plan.nsplit > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
+    if (k_new != nullptr && plan.row_chunks > 1) {
+        // Several row-chunk workgroups read the new rows: write them in a launch of their own.
+        launch_kv_append(k_new, v_new, positions, nullptr, T, c, stream);
+        k_new = nullptr;
+        v_new = nullptr;
+    }
     char* ws = static_cast<char*>(workspace);
     AttnArgs a{};
     a.q = q;
+    a.k_new = k_new;
+    a.v_new = v_new;
     a.positions = positions;
     a.parents = parents;
     a.kc = c.kc;
@@ -601,9 +723,9 @@ void launch_verify_attention(const uint16_t* q, const int32_t* positions, const 
     const int rows = plan.tokens_per_chunk * plan.G;
     dim3 grid(plan.nsplit, c.Hkv, c.B * plan.row_chunks);
     if (rows <= 16) {
-        hipLaunchKernelGGL((verify_attn_partial_kernel<128, 1>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(verify_attn_partial_kernel<1>, grid, dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL((verify_attn_partial_kernel<128, 2>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(verify_attn_partial_kernel<2>, grid, dim3(256), 0, stream, a);
     }
     check_launch("verify_attn_partial_kernel");
 
@@ -618,9 +740,8 @@ void launch_verify_attention(const uint16_t* q, const int32_t* positions, const 
     mg.tokens_per_chunk = plan.tokens_per_chunk;
     mg.row_chunks = plan.row_chunks;
     mg.nsplit = plan.nsplit;
-    mg.out_scale = 1.0f / 32768.0f;
     mg.out_f32 = out_f32 ? 1 : 0;
-    hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq), dim3(128), 0, stream, mg);
+    hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq), dim3(kMergeThreads), 0, stream, mg);
     check_launch("verify_attn_merge_kernel");
 }
 
