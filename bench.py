@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0
 HQ, HKV, D, T = 40, 8, 128, 4
 VOCAB = 248320
 BYTES_PER_TOKEN = 2 * HKV * (D + 2 * (D // 64))  # K+V codes + FP16 scales over 8 heads = 2,112
+C3_LAYERS = 8
 
 
 def attn_bytes(L: int) -> int:
@@ -54,19 +55,25 @@ def log(msg: str) -> None:
 class Layer:
     """One attention layer: its own cache planes, inputs, output and positions."""
 
-    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22):
+    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22, copy_from=None):
         import ninfer_amd as na
-        from ninfer_amd import ops, synthetic as syn
+        from ninfer_amd import device, ops, synthetic as syn
         from ninfer_amd.device import DeviceArray, synchronize
         from ninfer_amd.kv_cache import KVCacheLayer
 
         self.L = L
         self.cache = KVCacheLayer(max_context, HKV, D)
-        # History K/V: BF16 N(0,1) (optionally 1% outliers at +-20), quantized on the GPU in chunks.
         rng = np.random.default_rng(seed)
         per_tok = D * HKV
         chunk = max(1, gen_chunk // per_tok)
-        for start in range(0, L, chunk):
+        if copy_from is not None:
+            # Same history as another layer, in planes of its own (a device-to-device copy).
+            for dst, src in zip((self.cache.k, self.cache.v, self.cache.k_scale, self.cache.v_scale),
+                                (copy_from.cache.k, copy_from.cache.v, copy_from.cache.k_scale, copy_from.cache.v_scale)):
+                device.memcpy_dtod(dst.buf, src.buf, dst.nbytes)
+            synchronize()
+        # History K/V: BF16 N(0,1) (optionally 1% outliers at +-20), quantized on the GPU in chunks.
+        for start in range(0, L if copy_from is None else 0, chunk):
             n = min(chunk, L - start)
             kv = []
             for _ in range(2):
@@ -215,8 +222,9 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "sampler"], default=None,
-                    help="profile helper: run one workload's replays and exit (no JSON line)")
+    ap.add_argument("--only", choices=["c2", "c3", "sampler", "copy"], default=None,
+                    help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
+                         "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}). "
@@ -230,6 +238,21 @@ def main():
     log(f"device: {device.device_name()}")
     stream = Stream()
     result = {}
+
+    if args.only == "copy":
+        # A plain copy of known size: FETCH_SIZE / WRITE_SIZE of its dispatches calibrate the
+        # counters against bytes actually moved (256 MiB read + 256 MiB written per dispatch).
+        nbytes = 256 << 20
+        src, dst = DeviceBuffer(nbytes), DeviceBuffer(nbytes)
+        src.fill(1, stream)
+        from ninfer_amd.device import Event
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(5):
+            device.memcpy_dtod(dst, src, nbytes, stream)
+        e1.record(stream)
+        log(f"copy 256 MiB: {2 * nbytes * 5 / (e0.elapsed_ms(e1) * 1e-3) / 1e9:.0f} GB/s (read + write)")
+        return
 
     # ---- C2: 64 layers at context 7680 + greedy acceptance --------------------------------------
     if args.only in (None, "c2"):
@@ -274,11 +297,17 @@ def main():
     if (args.only in (None, "c3")) and not args.skip_long:
         L3 = 260096
         t0 = time.perf_counter()
-        layer = Layer(L3, L3 + T, seed=3, outliers=True)
-        log(f"C3: layer generated + quantized in {time.perf_counter() - t0:.1f}s")
+        first = Layer(L3, L3 + T, seed=3, outliers=True)
+        # C3_LAYERS layers with planes of their own (0.55 GB each, far beyond the 256 MB Infinity
+        # Cache) in one graph, as consecutive layers of a model run: per-layer time without the
+        # graph launch overhead of a one-kernel graph.
+        c3_layers = [first] + [Layer(L3, L3 + T, seed=4 + i, outliers=True, copy_from=first) for i in range(C3_LAYERS - 1)]
+        log(f"C3: {C3_LAYERS} layers generated + quantized in {time.perf_counter() - t0:.1f}s")
         ws3 = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L3 + T))
-        g3 = capture(stream, lambda: layer.launch(ws3, stream))
+        g3 = capture(stream, lambda: [ly.launch(ws3, stream) for ly in c3_layers])
         ms3, p95_3, _ = time_graph(g3, stream, max(args.steps, 20), args.warmup)
+        ms3 /= C3_LAYERS
+        p95_3 /= C3_LAYERS
         if args.only:
             log(f"C3 {ms3 * 1e3:.1f} us/layer")
             return
@@ -287,7 +316,7 @@ def main():
                             bytes_per_layer=attn_bytes(L3), frac_of_peak=gbs3 / HBM_PEAK_GBS,
                             target_us=attn_bytes(L3) / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6)
         log(f"C3: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
-        del layer, g3
+        del c3_layers, first, g3
         device.synchronize()
 
     # ---- sampler: top-20 stochastic acceptance at B=1 and B=16 --------------------------------------

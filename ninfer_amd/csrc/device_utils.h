@@ -45,16 +45,21 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Reduction across the four 16-lane groups that share one MFMA column (lanes c, c+16, c+32, c+48).
+// v_permlane32_swap / v_permlane16_swap exchange half-waves and odd/even 16-lane rows in the VALU,
+// so each step is a register swap plus one op (no LDS round trip as with ds_bpermute). Both lanes
+// of a pair add in the same order, so every lane ends with the same bits.
 __device__ __forceinline__ float group4_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float group4_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Two signed INT8 codes -> one packed FP16 pair, exactly: byte BYTE of `lo` -> low half, byte BYTE

@@ -2,28 +2,31 @@
 //
 // Semantics (reference include/ninfer/ops/gqa_attention.h:52-91): for sequence b, query token t
 // and query head qh (KV head h = qh / G), attend over cache rows [0, positions[0]) plus the new
-// rows positions[u] with u visible from t (u <= t causal; u an ancestor-or-self of t for trees),
-// reading INT8-G64 codes with FP16 scales. A1 first quantizes the new K/V columns into their rows
-// (the split owning a row writes it, as the reference's decode kernel does,
-// src/ops/kernel/gqa_attention_decode_i8.cuh:168-209). Split-K over keys with an online softmax
-// per split and a log-sum-exp merge (reference reducer src/ops/kernel/gqa_attention_decode.cuh:
-// 144-227).
+// rows positions[u] (positions are sequential) with u visible from t (u <= t causal; u an
+// ancestor-or-self of t for trees), reading INT8-G64 codes with FP16 scales. A1 first quantizes
+// the new K/V columns into their rows (the split owning them writes them, as the reference's
+// decode kernel does, src/ops/kernel/gqa_attention_decode_i8.cuh:168-209). Split-K over keys with
+// an online softmax per split and a log-sum-exp merge (reference reducer
+// src/ops/kernel/gqa_attention_decode.cuh:144-227).
 //
 // MI355X design:
 //  * One workgroup = 4 waves = one (sequence, row chunk, KV head, key split); 2 workgroups per CU.
-//    Each wave streams 32-key chunks (chunk w, w+4, ...). A chunk (K codes, V codes, FP16 scales:
-//    8,448 bytes) moves HBM -> LDS by asynchronous global_load_lds DMA into a per-wave two-stage
-//    ring with a lookahead of two chunks: 16.5 KB per wave, 132 KB per CU stay in flight while
-//    the current chunk is computed, at no VGPR cost.
-//  * QK^T runs as S^T = K * Q^T on v_mfma_f32_16x16x32_f16: K codes (exact in FP16) are the A
-//    operand, Q (BF16 -> FP16 exact after a per-row power-of-two rescale) the B operand. Each
-//    32-dim MFMA step stays inside one 64-wide quant group and each group accumulates separately,
-//    so the per-(key, group) FP16 scale is applied exactly in FP32. The K DMA writes LDS in MFMA
-//    operand order, so every lane reads its own 16 bytes (conflict-free ds_read_b128).
-//  * PV runs as O^T = V^T * P^T on the same instruction. The S^T accumulator layout (lane = query
+//    Each wave streams 32-key chunks (chunk w, w+4, ...). A chunk (K codes, V codes, FP16 scales)
+//    moves HBM -> LDS by asynchronous buffer_load ... lds DMA into a per-wave two-stage ring with
+//    a lookahead of two chunks; every code DMA instruction reads 1 KB of whole 128-byte rows.
+//    The loop is software-pipelined: chunk j+1 is read from LDS and its QK^T issued while chunk
+//    j's softmax and PV run.
+//  * QK^T runs as S^T = K' * Q^T on v_mfma_f32_16x16x32_f16: K' = FP16(code * scale) (one packed
+//    multiply per pair after an exact SDWA int8 -> FP16 convert) is the A operand, Q (BF16 -> FP16
+//    exact after a per-row power-of-two rescale) the B operand. K rows sit in LDS with their
+//    16-byte pieces XOR-swizzled by row, so the A-operand ds_read_b128 is conflict-free.
+//  * PV runs as O^T = V'^T * P^T on the same instruction. The S^T accumulator layout (lane = query
 //    row, 4 keys per 16-key tile) is exactly the B-operand layout of P^T, so probabilities never
 //    leave registers. V rows land in LDS in their natural layout; each lane reads 8 bytes of 8 keys
-//    (dims 8c..8c+7) and transposes in registers with SDWA converts.
+//    (dims 8c..8c+7) and transposes in registers with SDWA converts. Row sums come from one more
+//    MFMA with an all-ones A operand.
+//  * The softmax keeps a lazy reference maximum: probabilities are FP16 exp2(s - m + 8) and m
+//    moves (rescaling O) only when a score exceeds it by 2^7, so most chunks skip the rescale.
 //  * GQA x q_len rows (5 x 4 = 20 for the 40/8 geometry) are padded to two 16-row MFMA tiles.
 #include "common.h"
 #include "device_utils.h"
@@ -31,6 +34,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #define NMI_AS1 __attribute__((address_space(1)))
 #define NMI_AS3 __attribute__((address_space(3)))
@@ -40,11 +44,35 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kChunk = 32;
-constexpr int kStageK = 0;       // 4 x 1 KB, MFMA operand order
-constexpr int kStageV = 4096;    // 32 rows x 128 B, natural order
-constexpr int kStageS = 8192;    // 32 K scale words then 32 V scale words
-constexpr int kStageBytes = 8448;
-constexpr int kSmemBytes = kWaves * 2 * kStageBytes; // 67,584 B; the epilogue merge reuses it
+constexpr int kStride = kChunk * kWaves; // keys between one wave's consecutive chunks
+// One 32-key stage of one KV head in LDS.
+constexpr int kStageK = 0;      // K codes: 32 rows x 128 B; row r's 16-byte piece p at slot p ^ (r & 7)
+constexpr int kStageV = 4096;   // V codes: 32 rows x 128 B, natural order
+constexpr int kStageKS = 8192;  // K scales: 64 keys x (group 0, group 1) FP16; keys 32-63 unused
+constexpr int kStageVS = 8448;  // V scales, same shape
+constexpr int kStageBytes = 8704;
+constexpr int kRingBytes = kWaves * 2 * kStageBytes; // two stages per wave: 69,632 B
+constexpr int kNewStage = kRingBytes;                 // A1: new rows quantized in-kernel
+constexpr int kSmemBytes = kRingBytes + kStageBytes;  // 78,336 B: two workgroups per CU
+constexpr int kDmaPerChunk = 10;
+// Probabilities are FP16 exp2(score - m + 8); the reference maximum m moves only when a score
+// exceeds it by more than 2^7, so P <= 2^15 stays inside FP16 and most chunks skip the rescale.
+constexpr float kPOffset = 8.0f;
+constexpr float kLazyTau = 7.0f;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[15:14], expcnt[6:4], lgkmcnt[11:8]).
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+constexpr int kWaitLgkm0 = 0xc07f;
+
+// Wait until one chunk's DMA has landed; with `next_in_flight` the following chunk's stays
+// outstanding (DMAs of one wave complete in issue order).
+__device__ __forceinline__ void wait_chunk(bool next_in_flight) {
+    if (next_in_flight) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kDmaPerChunk));
+    } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
+}
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -99,44 +127,231 @@ __device__ __forceinline__ h8 cvt_codes8(int lo, int hi) {
     return __builtin_bit_cast(h8, w);
 }
 
+__device__ __forceinline__ h8 scale_h8(h8 x, h2 s) {
+    h2 p[4];
+    __builtin_memcpy(p, &x, sizeof(p));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { p[i] *= s; }
+    return __builtin_bit_cast(h8, p);
+}
+
 // Byte (T & 3) of word (T >> 2) from key slots 2w and 2w+1 -> packed FP16 pair (V transpose).
 template <int T>
 __device__ __forceinline__ uint32_t v_pair(const i2& a, const i2& b) {
     return i8x2_to_f16x2<T & 3>(static_cast<uint32_t>(a[T >> 2]), static_cast<uint32_t>(b[T >> 2]));
 }
 
-__device__ __forceinline__ _Float16 half_bits_at(const i4& v, int idx) {
-    const uint32_t word = static_cast<uint32_t>(v[idx >> 1]);
-    return __builtin_bit_cast(_Float16, static_cast<uint16_t>((idx & 1) ? (word >> 16) : (word & 0xffffu)));
+// Buffer resources of one (sequence, KV head): raw byte buffers, so DMA offsets are 32-bit.
+struct HeadBuffers {
+    __amdgpu_buffer_rsrc_t k, v, ks, vs;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-// Issue the DMA of one 32-key chunk (the caller guarantees c0 + 32 <= P) into `stage`.
-__device__ __forceinline__ void issue_chunk(NMI_AS3 char* stage, const int8_t* kbase, const int8_t* vbase,
-                                            const uint16_t* ksbase, const uint16_t* vsbase, int c0,
-                                            int lane) {
-    const int c = lane & 15;
-    const int g = lane >> 4;
+// Per-lane DMA source offsets, fixed for the whole kernel.
+struct DmaLanes {
+    int k;  // row lane >> 3, piece (lane & 7) ^ (lane >> 3): the swizzled K layout
+    int v;  // row lane >> 3, bytes 16 * (lane & 7)
+    int sc; // scale word lane
+};
+
+// Issue the DMA of one 32-key chunk (c0 + 32 <= P) into `st`: 4 K blocks, 4 V blocks and the K and
+// V scale words of keys c0..c0+63 (the upper 32 are not used; the chunk offset of the scales sits in
+// the range-checked voffset, so words past the head's last row read as zero). Block offsets of the
+// codes go through soffset, which moves only the source address; the LDS address is M0 + 16 * lane
+// (4 * lane for scales). Both scale loads run on the full wave: lane-divergent descriptors would
+// turn one DMA into a waterfall loop.
+__device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers& hb, const DmaLanes& dl,
+                                            int c0, int lane) {
+    const int so = c0 * 128;
+#pragma unroll
+    for (int r8 = 0; r8 < 4; ++r8) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.k, (NMI_AS3 void*)(st + kStageK + r8 * 1024), 16, dl.k, so + r8 * 1024, 0, 0);
+    }
+#pragma unroll
+    for (int r8 = 0; r8 < 4; ++r8) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.v, (NMI_AS3 void*)(st + kStageV + r8 * 1024), 16, dl.v, so + r8 * 1024, 0, 0);
+    }
+    const int vso = dl.sc + c0 * 4;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.ks, (NMI_AS3 void*)(st + kStageKS), 4, vso, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.vs, (NMI_AS3 void*)(st + kStageVS), 4, vso, 0, 0, 0);
+}
+
+// One chunk in registers: K codes in A-operand order, the K scale word of key 16kt + c, the V scale
+// words of keys 4g..4g+3 and 16+4g..16+4g+3, and 8 bytes (dims 8c..8c+7) of the lane's 8 V rows.
+struct ChunkRegs {
+    i4 kr[2][2];
+    uint32_t ksc[2];
+    i4 vsw[2];
+    i2 vr[8];
+};
+
+__device__ __forceinline__ void read_chunk(const NMI_AS3 char* st, ChunkRegs& r, int lane, int c, int g) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int gq = 0; gq < 2; ++gq) {
-            const int8_t* src = kbase + static_cast<int64_t>(c0 + 16 * kt + c) * 128 + 64 * gq + 16 * g;
-            __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(stage + kStageK + (2 * kt + gq) * 1024), 16, 0, 0);
+            // A operand: key 16kt + c, dims 64gq + 16g .. +15 = piece 4gq + g of row 16kt + c.
+            const int slot = (4 * gq + g) ^ (c & 7);
+            r.kr[kt][gq] = *(const NMI_AS3 i4*)(st + kStageK + (16 * kt + c) * 128 + 16 * slot);
         }
+        r.ksc[kt] = *(const NMI_AS3 uint32_t*)(st + kStageKS + 4 * (16 * kt + c));
     }
+    r.vsw[0] = *(const NMI_AS3 i4*)(st + kStageVS + 16 * g);
+    r.vsw[1] = *(const NMI_AS3 i4*)(st + kStageVS + 64 + 16 * g);
 #pragma unroll
-    for (int r8 = 0; r8 < 4; ++r8) {
-        const int8_t* src = vbase + static_cast<int64_t>(c0 + 8 * r8 + (lane >> 3)) * 128 + 16 * (lane & 7);
-        __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(stage + kStageV + r8 * 1024), 16, 0, 0);
+    for (int j = 0; j < 8; ++j) {
+        const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+        r.vr[j] = *(const NMI_AS3 i2*)(st + kStageV + row * 128 + 8 * c);
     }
-    const uint16_t* ssrc = (lane < 32 ? ksbase + static_cast<int64_t>(c0 + lane) * 2 : vsbase + static_cast<int64_t>(c0 + lane - 32) * 2);
-    __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)ssrc, (NMI_AS3 void*)(stage + kStageS), 4, 0, 0);
 }
 
-// Quantize-append one new token row of one KV head (one wave: lane owns dims lane and lane + 64 of
-// K and V), reference contract include/ninfer/ops/gqa_attention.h:25-30.
+// Which keys of a chunk a row may see: keys below vis_all are visible to every row; key
+// new_base + u (u < 32, key < key_end) is visible to the row's token if bit u of its mask is set.
+// V scales of keys at or past key_end count as zero (those rows may hold stale bytes).
+struct KeyRange {
+    int vis_all;
+    int new_base;
+    int key_end;
+};
+
+// Online-softmax state of one wave: NT tiles of 16 rows.
+template <int NT>
+struct RowState {
+    h8 q[NT][2][2];   // B operand of Q^T: rows 16nt + c, dims 64gq + 16g + 8s + e
+    float rowmul[NT]; // softmax scale * log2(e) / Q power-of-two factor
+    float rowthr[NT]; // kLazyTau / rowmul: the lazy-rescale threshold in raw score units
+    uint32_t nmask[NT];
+    float m[NT];      // reference maximum in raw score units
+    f4 O[NT][8];      // O^T tiles: tile t row 4g+e is dim 8(4g+e) + t
+    f4 l[NT];         // row sums, equal in all four entries (ones x P^T)
+};
+
+// S^T = K' Q^T with K' = FP16(code * scale) as the A operand (key 16kt + c).
+template <int NT>
+__device__ __forceinline__ void qk_chunk(const ChunkRegs& r, const RowState<NT>& s, f4 (&sacc)[2][NT]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int gq = 0; gq < 2; ++gq) {
+            const uint32_t sp = __builtin_amdgcn_perm(r.ksc[kt], r.ksc[kt], gq ? 0x03020302u : 0x01000100u);
+            const h2 s2 = __builtin_bit_cast(h2, sp);
+            const h8 a0 = scale_h8(cvt_codes8(r.kr[kt][gq][0], r.kr[kt][gq][1]), s2);
+            const h8 a1 = scale_h8(cvt_codes8(r.kr[kt][gq][2], r.kr[kt][gq][3]), s2);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f4 acc = gq == 0 ? f4{0.f, 0.f, 0.f, 0.f} : sacc[kt][nt];
+                sacc[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, s.q[nt][gq][0], acc, 0, 0, 0);
+                sacc[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, s.q[nt][gq][1], sacc[kt][nt], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Online softmax of one chunk; the S^T accumulator layout is the B-operand layout of P^T. `masked`
+// is uniform across the wave.
+template <int NT>
+__device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, bool masked, RowState<NT>& s,
+                                              const KeyRange& kr, int g, h8 (&pop)[NT]) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        float sv[8];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { sv[4 * kt + e] = sacc[kt][nt][e]; }
+        }
+        if (masked) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                // Branch-free: bitwise operators, and a shift count that is always in range.
+                const int key = c0 + 16 * (i >> 2) + 4 * g + (i & 3);
+                const int u = key - kr.new_base;
+                const bool bit = ((s.nmask[nt] >> (u & 31)) & 1u) != 0u;
+                const bool vis = (key < kr.vis_all) | ((key < kr.key_end) & (static_cast<unsigned>(u) < 32u) & bit);
+                sv[i] = vis ? sv[i] : -INFINITY;
+            }
+        }
+        float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+        cmax = group4_max(cmax);
+        const bool need = cmax > s.m[nt] + s.rowthr[nt];
+        if (__any(need)) {
+            const float mn = need ? cmax : s.m[nt];
+            const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) { s.O[nt][t] *= alpha; }
+            s.l[nt] *= alpha;
+            s.m[nt] = mn;
+        }
+        const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pop[nt][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)));
+        }
+    }
+}
+
+// O^T += V'^T P^T with V' = FP16(code * scale); l += ones x P^T. Keys at or past key_end of a
+// masked chunk get a zero V scale.
+template <int NT>
+__device__ __forceinline__ void pv_chunk(const h8 (&pop)[NT], const i2 (&vr)[8], const i4 (&vsw)[2], int c0,
+                                         bool masked, RowState<NT>& s, const KeyRange& kr, int c, int g) {
+    const uint32_t vsel = (c >> 3) ? 0x07060302u : 0x05040100u; // FP16 half of this lane's group
+    h2 vsp[4];
+    vsp[0] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[0][1]), static_cast<uint32_t>(vsw[0][0]), vsel));
+    vsp[1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[0][3]), static_cast<uint32_t>(vsw[0][2]), vsel));
+    vsp[2] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[1][1]), static_cast<uint32_t>(vsw[1][0]), vsel));
+    vsp[3] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[1][3]), static_cast<uint32_t>(vsw[1][2]), vsel));
+    if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+            if (key >= kr.key_end) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
+        }
+    }
+#define NMI_PV_TILE(TT)                                                                            \
+    {                                                                                              \
+        h2 pr[4];                                                                                  \
+        _Pragma("unroll") for (int w = 0; w < 4; ++w) {                                            \
+            pr[w] = __builtin_bit_cast(h2, v_pair<TT>(vr[2 * w], vr[2 * w + 1])) * vsp[w];         \
+        }                                                                                          \
+        const h8 va = __builtin_bit_cast(h8, pr);                                                  \
+        _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                        \
+            s.O[nt][TT] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pop[nt], s.O[nt][TT], 0, 0, 0); \
+        }                                                                                          \
+    }
+    NMI_PV_TILE(0)
+    NMI_PV_TILE(1)
+    NMI_PV_TILE(2)
+    NMI_PV_TILE(3)
+    NMI_PV_TILE(4)
+    NMI_PV_TILE(5)
+    NMI_PV_TILE(6)
+    NMI_PV_TILE(7)
+#undef NMI_PV_TILE
+    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) { s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[nt], s.l[nt], 0, 0, 0); }
+}
+
+template <int NT>
+__device__ __forceinline__ void compute_chunk(const ChunkRegs& r, int c0, bool masked, RowState<NT>& s,
+                                              const KeyRange& kr, int c, int g) {
+    f4 sacc[2][NT];
+    qk_chunk<NT>(r, s, sacc);
+    h8 pop[NT];
+    softmax_chunk<NT>(sacc, c0, masked, s, kr, g, pop);
+    pv_chunk<NT>(pop, r.vr, r.vsw, c0, masked, s, kr, c, g);
+}
+
+// Quantize one new token row of one KV head (one wave: lane owns dims lane and lane + 64 of K and
+// V; reference contract include/ninfer/ops/gqa_attention.h:25-30) into the cache and into key slot
+// u of the LDS stage `st`, in the layout the chunk DMA produces.
 __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t* vsrc, int8_t* kdst,
-                                           int8_t* vdst, uint16_t* ksdst, uint16_t* vsdst, int lane) {
+                                           int8_t* vdst, uint16_t* ksdst, uint16_t* vsdst,
+                                           NMI_AS3 char* st, int u, int lane) {
     const float x[4] = {bf16_to_f32(ksrc[lane]), bf16_to_f32(ksrc[64 + lane]), bf16_to_f32(vsrc[lane]),
                         bf16_to_f32(vsrc[64 + lane])};
     uint16_t sbits[4];
@@ -145,27 +360,36 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
     for (int i = 0; i < 4; ++i) {
         const float amax = wave_max(fabsf(x[i]));
         sbits[i] = f32_to_f16_bits(amax > 0.0f ? amax / 127.0f : 0.0f);
-        const float s = f16_bits_to_f32(sbits[i]);
-        const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-        float r = inv != 0.0f ? rintf(x[i] * inv) : 0.0f;
-        r = fminf(127.0f, fmaxf(-127.0f, r));
-        code[i] = static_cast<int8_t>(r);
+        const float sc = f16_bits_to_f32(sbits[i]);
+        const float inv = sc > 0.0f ? 1.0f / sc : 0.0f;
+        float rr = inv != 0.0f ? rintf(x[i] * inv) : 0.0f;
+        rr = fminf(127.0f, fmaxf(-127.0f, rr));
+        code[i] = static_cast<int8_t>(rr);
     }
     kdst[lane] = code[0];
     kdst[64 + lane] = code[1];
     vdst[lane] = code[2];
     vdst[64 + lane] = code[3];
+    const uint32_t kw = static_cast<uint32_t>(sbits[0]) | (static_cast<uint32_t>(sbits[1]) << 16);
+    const uint32_t vw = static_cast<uint32_t>(sbits[2]) | (static_cast<uint32_t>(sbits[3]) << 16);
     if (lane == 0) {
-        *reinterpret_cast<uint32_t*>(ksdst) = static_cast<uint32_t>(sbits[0]) | (static_cast<uint32_t>(sbits[1]) << 16);
-        *reinterpret_cast<uint32_t*>(vsdst) = static_cast<uint32_t>(sbits[2]) | (static_cast<uint32_t>(sbits[3]) << 16);
+        *reinterpret_cast<uint32_t*>(ksdst) = kw;
+        *reinterpret_cast<uint32_t*>(vsdst) = vw;
+        *(NMI_AS3 uint32_t*)(st + kStageKS + 4 * u) = kw;
+        *(NMI_AS3 uint32_t*)(st + kStageVS + 4 * u) = vw;
     }
+    // Swizzled K row u: dim d sits in piece d >> 4 at slot (d >> 4) ^ (u & 7).
+    const int krow = kStageK + u * 128 + (lane & 15);
+    st[krow + 16 * ((lane >> 4) ^ (u & 7))] = static_cast<char>(code[0]);
+    st[krow + 16 * ((4 + (lane >> 4)) ^ (u & 7))] = static_cast<char>(code[1]);
+    st[kStageV + u * 128 + lane] = static_cast<char>(code[2]);
+    st[kStageV + u * 128 + 64 + lane] = static_cast<char>(code[3]);
 }
 
 template <int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void verify_attn_partial_kernel(AttnArgs a) {
     constexpr int D = 128;
-    constexpr int G = 2;       // quant groups per row
-    constexpr int DT = D / 16; // O^T tiles of 16 dims
+    constexpr int G = 2; // quant groups per row
     __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
 
     const int lane = threadIdx.x & 63;
@@ -184,63 +408,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     int8_t* vbase = a.vc + head_code;
     uint16_t* ksbase = a.ks + head_scale;
     uint16_t* vsbase = a.vs + head_scale;
-    NMI_AS3 char* my_stage0 = (NMI_AS3 char*)smem + wave * 2 * kStageBytes;
+    const HeadBuffers hb{raw_buffer(kbase, static_cast<int64_t>(a.P) * D), raw_buffer(vbase, static_cast<int64_t>(a.P) * D),
+                         raw_buffer(ksbase, static_cast<int64_t>(a.P) * 4), raw_buffer(vsbase, static_cast<int64_t>(a.P) * 4)};
+    const DmaLanes dl{(lane >> 3) * 128 + 16 * ((lane & 7) ^ (lane >> 3)), (lane >> 3) * 128 + 16 * (lane & 7), lane * 4};
+    NMI_AS3 char* ring = (NMI_AS3 char*)smem + wave * 2 * kStageBytes;
 
     // The first chunk does not depend on the positions: start its DMA right away.
     const int first = k0 + kChunk * wave;
-    if (first + kChunk <= a.P) { issue_chunk(my_stage0, kbase, vbase, ksbase, vsbase, first, lane); }
+    if (first + kChunk <= a.P) { issue_chunk(ring, hb, dl, first, lane); }
 
     const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
     const int32_t* par = a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr;
-    const int window = min(pos[a.T - 1] + 1, a.max_keys);
-    const int L = max(0, min(pos[0], window));
+    // Positions load while Q is converted: nothing in the Q operand depends on them.
+    const int pos_first = pos[0];
+    const int pos_last = pos[a.T - 1];
     const int t0 = rc * a.tokens_per_chunk;
     const int Tc = min(a.tokens_per_chunk, a.T - t0);
     const int R = Tc * a.G;
-    const int k1 = min(k0 + a.kps, window);
-    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
-    const int64_t pidx = unit * a.nsplit + split;
-    float* out_o = a.part_o + pidx * (32 * D);
-    float* out_ml = a.part_ml + pidx * 64;
-
-    // ---- fused A1 append: this split writes the new rows inside [k0, k0 + kps). Only launched
-    // with a single row chunk, so no other workgroup reads these rows concurrently.
-    if (a.k_new != nullptr) {
-        bool owner = false;
-        for (int t = 0; t < a.T; ++t) {
-            const int p = pos[t];
-            const bool mine = p >= k0 && p < k0 + a.kps && p >= 0 && p < a.P;
-            owner |= mine;
-            if (mine && (t & (kWaves - 1)) == wave) {
-                const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (t + static_cast<int64_t>(a.T) * b));
-                append_row(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D,
-                           vbase + static_cast<int64_t>(p) * D, ksbase + static_cast<int64_t>(p) * G,
-                           vsbase + static_cast<int64_t>(p) * G, lane);
-            }
-        }
-        if (owner) {
-            // Stores visible (and this CU's L1 invalidated) before any DMA of the new rows.
-            __threadfence();
-            __syncthreads();
-            if (first + kChunk <= a.P && first < pos[a.T - 1] + 1 && first + kChunk > pos[0]) {
-                issue_chunk(my_stage0, kbase, vbase, ksbase, vsbase, first, lane); // re-fetch
-            }
-        }
-    }
-
-    if (k0 >= k1) {
-        __builtin_amdgcn_s_waitcnt(0);
-        if (threadIdx.x < 32) {
-            out_ml[2 * threadIdx.x] = -INFINITY;
-            out_ml[2 * threadIdx.x + 1] = 0.0f;
-        }
-        return;
-    }
 
     // ---- Q operand: rows r = 16*nt + c; dims d = 64*gq + 16*g + 8*s + e.
-    h8 qop[NT][G][2];
-    float rowmul[NT];
-    uint32_t nmask[NT];
+    RowState<NT> s;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int r = 16 * nt + c;
@@ -255,231 +442,174 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int gq = 0; gq < G; ++gq) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const i4 raw = valid ? *reinterpret_cast<const i4*>(qrow + 64 * gq + 16 * g + 8 * s) : i4{0, 0, 0, 0};
+            for (int hs = 0; hs < 2; ++hs) {
+                const i4 raw = valid ? *reinterpret_cast<const i4*>(qrow + 64 * gq + 16 * g + 8 * hs) : i4{0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int w = raw[e >> 1];
                     const uint16_t bits = static_cast<uint16_t>((e & 1) ? (static_cast<uint32_t>(w) >> 16) : (static_cast<uint32_t>(w) & 0xffffu));
-                    x[gq][s][e] = bf16_to_f32(bits);
-                    amax = fmaxf(amax, fabsf(x[gq][s][e]));
+                    x[gq][hs][e] = bf16_to_f32(bits);
+                    amax = fmaxf(amax, fabsf(x[gq][hs][e]));
                 }
             }
         }
         amax = group4_max(amax);
         // factor = 2^(14 - floor(log2(amax))) puts max|q| in [2^14, 2^15): FP16 holds every BF16
-        // value of the row exactly down to 2^-28 of its maximum.
+        // value of the row exactly down to 2^-28 of its maximum. The exponent is clamped so the
+        // factor and the lazy threshold stay finite for rows of tiny values.
         float factor = 1.0f;
         if (amax > 0.0f && amax < INFINITY) {
-            const int ex = static_cast<int>((__float_as_uint(amax) >> 23) & 0xff) - 127;
+            const int ex = max(static_cast<int>((__float_as_uint(amax) >> 23) & 0xff) - 127, -100);
             factor = ldexpf(1.0f, 14 - ex);
         }
 #pragma unroll
         for (int gq = 0; gq < G; ++gq) {
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
+            for (int hs = 0; hs < 2; ++hs) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) { qop[nt][gq][s][e] = static_cast<_Float16>(x[gq][s][e] * factor); }
+                for (int e = 0; e < 8; ++e) { s.q[nt][gq][hs][e] = static_cast<_Float16>(x[gq][hs][e] * factor); }
             }
         }
-        rowmul[nt] = a.scale_log2 / factor;
-        nmask[nt] = valid ? new_key_mask(par, t) : 0u;
+        s.rowmul[nt] = a.scale_log2 / factor;
+        s.rowthr[nt] = kLazyTau / s.rowmul[nt];
+        s.nmask[nt] = valid ? new_key_mask(par, t) : 0u;
+        s.m[nt] = -INFINITY;
+        s.l[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t8 = 0; t8 < 8; ++t8) { s.O[nt][t8] = f4{0.f, 0.f, 0.f, 0.f}; }
     }
 
-    float m[NT];
-    float l[NT];
-    f4 O[NT][DT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        m[nt] = -INFINITY;
-        l[nt] = 0.0f;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) { O[nt][t] = f4{0.f, 0.f, 0.f, 0.f}; }
+
+    const int window = min(pos_last + 1, a.max_keys);
+    const int L = max(0, min(pos_first, window));
+    const int k1 = min(k0 + a.kps, window);
+    const bool fused = a.k_new != nullptr;
+    // With the fused append the cache rows >= L are written by this launch: splits stream only the
+    // history below L, and the split holding L attends to the new rows from its own registers.
+    const int hend = fused ? min(k1, L) : k1;
+    const bool owner = fused && L >= k0 && L < k0 + a.kps && L < window;
+    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
+    const int64_t pidx = unit * a.nsplit + split;
+    float* out_o = a.part_o + pidx * (32 * D);
+    float* out_ml = a.part_ml + pidx * 64;
+
+    if (first + kStride < hend) { issue_chunk(ring + kStageBytes, hb, dl, first + kStride, lane); }
+
+    if (k0 >= hend && !owner) {
+        __builtin_amdgcn_s_waitcnt(0);
+        if (threadIdx.x < 32) {
+            out_ml[2 * threadIdx.x] = -INFINITY;
+            out_ml[2 * threadIdx.x + 1] = 0.0f;
+        }
+        return;
     }
 
-    const int hist_end = min(L, k1); // keys below this are visible to every row
-    const int vgroup = c >> 3;       // quant group of this lane's V dims 8c..8c+7
+    // ---- fused A1 append: the owner quantizes the T new rows into the cache and into its new-row
+    // stage; wave 0 attends to them before its history chunks.
+    if (owner) {
+        NMI_AS3 char* ns = (NMI_AS3 char*)smem + kNewStage;
+        for (int i = threadIdx.x; i < kStageBytes / 16; i += blockDim.x) { *(NMI_AS3 i4*)(ns + 16 * i) = i4{0, 0, 0, 0}; }
+        __syncthreads();
+        for (int t = wave; t < a.T; t += kWaves) {
+            const int p = pos[t];
+            if (p < 0 || p >= a.P) { continue; }
+            const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (t + static_cast<int64_t>(a.T) * b));
+            append_row(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D, vbase + static_cast<int64_t>(p) * D,
+                       ksbase + static_cast<int64_t>(p) * G, vsbase + static_cast<int64_t>(p) * G, ns, t, lane);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            ChunkRegs r;
+            read_chunk(ns, r, lane, c, g);
+            const KeyRange nk{L, L, min(window, L + a.T)};
+            compute_chunk<NT>(r, L, true, s, nk, c, g);
+        }
+    }
 
-    // Lookahead of two chunks: while chunk i is computed, chunks i+1 and i+2 are in flight. Chunk
-    // i+2 reuses chunk i's stage once chunk i sits in registers.
-    constexpr int kStride = kChunk * kWaves;
-    if (first + kStride < k1) { issue_chunk(my_stage0 + kStageBytes, kbase, vbase, ksbase, vsbase, first + kStride, lane); }
-    int stage = 0;
+    // ---- history chunks, software-pipelined: while chunk j's softmax and PV run, chunk j+1 is
+    // read from LDS and its QK^T issued, and chunks j+2, j+3 are in flight as DMA.
+    const KeyRange hk{min(L, k1), L, hend};
+    if (first < hend) {
+        int stage = 0;
+        int cj = first;
+        ChunkRegs r;
+        wait_chunk(first + kStride < hend);
+        read_chunk(ring, r, lane, c, g);
+        if (first + 2 * kStride < hend) {
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            issue_chunk(ring, hb, dl, first + 2 * kStride, lane);
+        }
+        f4 sacc[2][NT];
+        qk_chunk<NT>(r, s, sacc);
+        i2 vcur[8];
+        i4 vswcur[2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { vcur[j] = r.vr[j]; }
+        vswcur[0] = r.vsw[0];
+        vswcur[1] = r.vsw[1];
+        stage = 1;
 #pragma unroll 1
-    for (int c0 = first; c0 < k1; c0 += kStride) {
-        NMI_AS3 char* st = my_stage0 + stage * kStageBytes;
-        // Wait for this chunk's 9 DMA instructions; the next chunk's 9 may stay outstanding.
-        if (c0 + kStride < k1) {
-            __builtin_amdgcn_s_waitcnt(0x0f79); // vmcnt(9)
-        } else {
-            __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
-        }
-        i4 kr[2][G];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int gq = 0; gq < G; ++gq) { kr[kt][gq] = *(NMI_AS3 const i4*)(st + kStageK + (2 * kt + gq) * 1024 + 16 * lane); }
-        }
-        const i4 ksw0 = *(NMI_AS3 const i4*)(st + kStageS + (4 * g) * 4);
-        const i4 ksw1 = *(NMI_AS3 const i4*)(st + kStageS + (16 + 4 * g) * 4);
-        const i4 vsw0 = *(NMI_AS3 const i4*)(st + kStageS + 128 + (4 * g) * 4);
-        const i4 vsw1 = *(NMI_AS3 const i4*)(st + kStageS + 128 + (16 + 4 * g) * 4);
-        i2 vr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-            vr[j] = *(NMI_AS3 const i2*)(st + kStageV + row * 128 + 8 * c);
-        }
-        // Chunk i is in registers once these reads retire; then its stage takes chunk i+2.
-        const int c2 = c0 + 2 * kStride;
-        if (c2 < k1) {
-            __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0)
-            issue_chunk(st, kbase, vbase, ksbase, vsbase, c2, lane);
-        }
-        stage ^= 1;
-
-        // ---- S^T = K Q^T per quant group
-        f4 sacc[2][NT][G];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-            for (int gq = 0; gq < G; ++gq) {
-                const h8 ka0 = cvt_codes8(kr[kt][gq][0], kr[kt][gq][1]);
-                const h8 ka1 = cvt_codes8(kr[kt][gq][2], kr[kt][gq][3]);
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) {
-                    f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka0, qop[nt][gq][0], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    sacc[kt][nt][gq] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka1, qop[nt][gq][1], acc, 0, 0, 0);
-                }
+        for (; cj < hend; cj += kStride) {
+            const int cn = cj + kStride; // next chunk (if < hend, its DMA was issued two steps ago)
+            NMI_AS3 char* stn = ring + stage * kStageBytes;
+            // Chunk j+1's DMA done (j+2's may stay outstanding). Reading a stage past the end is
+            // harmless: those registers are never used.
+            wait_chunk(cn + kStride < hend);
+            ChunkRegs rn;
+            read_chunk(stn, rn, lane, c, g);
+            h8 pop[NT];
+            softmax_chunk<NT>(sacc, cj, cj + kChunk > hk.vis_all, s, hk, g, pop);
+            if (cn + 2 * kStride < hend) {
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk j+1 sits in registers: reuse its stage
+                issue_chunk(stn, hb, dl, cn + 2 * kStride, lane);
             }
-        }
-
-        const bool full = (c0 + kChunk) <= hist_end;
-        h8 pop[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            float sv[2][4];
-            float cmax = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const i4& ksw = kt ? ksw1 : ksw0;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    float s = static_cast<float>(half_bits_at(ksw, 2 * e)) * sacc[kt][nt][0][e];
-                    s = fmaf(static_cast<float>(half_bits_at(ksw, 2 * e + 1)), sacc[kt][nt][1][e], s);
-                    s *= rowmul[nt];
-                    if (!full) {
-                        const int key = c0 + 16 * kt + 4 * g + e;
-                        bool vis = key < hist_end;
-                        if (!vis && key >= L && key < k1) {
-                            const int u = key - L;
-                            vis = u < 32 && ((nmask[nt] >> u) & 1u);
-                        }
-                        s = vis ? s : -INFINITY;
-                    }
-                    sv[kt][e] = s;
-                    cmax = fmaxf(cmax, s);
-                }
-            }
-            cmax = group4_max(cmax);
-            const float mnew = fmaxf(m[nt], cmax);
-            const bool live = mnew != -INFINITY;
-            // Probabilities carry a 2^15 factor (exact in FP16, cancels in O / l) so the PV operand
-            // stays in FP16's normal range down to 2^-29 of the row maximum.
-            const float mref = mnew - 15.0f;
-            float lsum = 0.0f;
+            stage ^= 1;
+            f4 sn[2][NT];
+            qk_chunk<NT>(rn, s, sn);
+            pv_chunk<NT>(pop, vcur, vswcur, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float pe = live ? __builtin_amdgcn_exp2f(sv[kt][e] - mref) : 0.0f;
-                    lsum += pe;
-                    pop[nt][4 * kt + e] = static_cast<_Float16>(pe);
-                }
+                for (int nt = 0; nt < NT; ++nt) { sacc[kt][nt] = sn[kt][nt]; }
             }
-            const bool grew = mnew > m[nt];
-            if (__any(grew)) {
-                const float alpha = grew ? __builtin_amdgcn_exp2f(m[nt] - mnew) : 1.0f;
-                l[nt] *= alpha;
 #pragma unroll
-                for (int t = 0; t < DT; ++t) { O[nt][t] *= alpha; }
-            }
-            l[nt] += lsum;
-            m[nt] = mnew;
+            for (int j = 0; j < 8; ++j) { vcur[j] = rn.vr[j]; }
+            vswcur[0] = rn.vsw[0];
+            vswcur[1] = rn.vsw[1];
         }
-
-        // ---- O^T += V^T P^T. V' = FP16(code * scale): codes convert exactly, one packed multiply
-        // rounds the product once. Keys past the range end get a zero scale (their rows may be
-        // uninitialized).
-        h2 vsp[4];
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int h1 = 0; h1 < 2; ++h1) {
-                const int j = 2 * w + h1;
-                vsp[w][h1] = half_bits_at(j < 4 ? vsw0 : vsw1, 2 * (j & 3) + vgroup);
-            }
-        }
-        if (!full) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
-                if (key >= k1) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
-            }
-        }
-#define NMI_PV_TILE(TT)                                                                            \
-    {                                                                                              \
-        h2 pr[4];                                                                                  \
-        _Pragma("unroll") for (int w = 0; w < 4; ++w) {                                            \
-            pr[w] = __builtin_bit_cast(h2, v_pair<TT>(vr[2 * w], vr[2 * w + 1])) * vsp[w];         \
-        }                                                                                          \
-        const h8 va = __builtin_bit_cast(h8, pr);                                                  \
-        _Pragma("unroll") for (int nt = 0; nt < NT; ++nt) {                                        \
-            O[nt][TT] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pop[nt], O[nt][TT], 0, 0, 0);   \
-        }                                                                                          \
-    }
-        NMI_PV_TILE(0)
-        NMI_PV_TILE(1)
-        NMI_PV_TILE(2)
-        NMI_PV_TILE(3)
-        NMI_PV_TILE(4)
-        NMI_PV_TILE(5)
-        NMI_PV_TILE(6)
-        NMI_PV_TILE(7)
-#undef NMI_PV_TILE
     }
 
     // ---- merge the four waves through LDS (reusing the staging ring), then write the partial.
     __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
     __syncthreads();
-    float* sm_o = reinterpret_cast<float*>(smem);      // [kWaves][32][D + 1]
-    float* sm_m = sm_o + kWaves * 32 * (D + 1);        // [kWaves][32]
-    float* sm_l = sm_m + kWaves * 32;                  // [kWaves][32]
+    constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
+    float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
+    float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
+    float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        const float lt = group4_sum(l[nt]);
         const int r = 16 * nt + c;
         if (g == 0) {
-            sm_m[wave * 32 + r] = m[nt];
-            sm_l[wave * 32 + r] = lt;
+            // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
+            sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
+            sm_l[wave * 32 + r] = s.l[nt][0];
         }
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // O^T tile t row (4g + e) is dim 8*(4g + e) + t.
-                sm_o[(wave * 32 + r) * (D + 1) + 8 * (4 * g + e) + t] = O[nt][t][e];
-            }
+        for (int e = 0; e < 4; ++e) {
+            // O^T tile t row (4g + e) is dim 8*(4g + e) + t: eight consecutive dims per (lane, e).
+            float* dst = sm_o + (wave * 32 + r) * kRowStride + 8 * (4 * g + e);
+            *reinterpret_cast<f4*>(dst) = f4{s.O[nt][0][e], s.O[nt][1][e], s.O[nt][2][e], s.O[nt][3][e]};
+            *reinterpret_cast<f4*>(dst + 4) = f4{s.O[nt][4][e], s.O[nt][5][e], s.O[nt][6][e], s.O[nt][7][e]};
         }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < R * D; idx += blockDim.x) {
-        const int r = idx / D;
-        const int d = idx - r * D;
+    for (int idx = threadIdx.x; idx < R * (D / 4); idx += blockDim.x) {
+        const int r = idx / (D / 4);
+        const int d4 = 4 * (idx - r * (D / 4));
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
-        float o = 0.0f;
+        f4 o = {0.f, 0.f, 0.f, 0.f};
         float lsum = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
@@ -487,12 +617,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 const float mw = sm_m[w * 32 + r];
                 if (mw == -INFINITY) { continue; }
                 const float wgt = __builtin_amdgcn_exp2f(mw - M);
-                o = fmaf(sm_o[(w * 32 + r) * (D + 1) + d], wgt, o);
+                o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
                 lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
             }
         }
-        out_o[r * D + d] = o;
-        if (d == 0) {
+        *reinterpret_cast<f4*>(out_o + r * D + d4) = o;
+        if (d4 == 0) {
             out_ml[2 * r] = M;
             out_ml[2 * r + 1] = lsum;
         }
@@ -514,18 +644,21 @@ struct MergeArgs {
 };
 
 constexpr int kMergeThreads = 256;
+constexpr int kMergeDims = 32;                               // output dims per block
+constexpr int kMergeGroups = kMergeThreads / kMergeDims;     // split groups per block
+constexpr int kMergePre = 8;                                 // 64 splits loaded up front
 constexpr int kMergeMaxSplits = 2048;
 
 // Log-sum-exp merge over splits (reference src/ops/kernel/gqa_attention_decode.cuh:144-227,
-// including "every split empty => 0"). One block per output row (b, t, qh): the first 32 splits'
-// partial rows are requested up front, every split's (m, l) becomes a weight in LDS through block
-// reductions, then two thread halves accumulate alternate splits.
+// including "every split empty => 0"). Block (row, dim slice): (b, t, qh) x 32 dims. Thread
+// (group sg, dim) owns splits sg, sg + 8, ...; the first 64 splits' partial values and every
+// split's (m, l) are requested before any reduction, so the block waits for memory about once.
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
     __shared__ float wts[kMergeMaxSplits];
     __shared__ float lw[kMergeMaxSplits];
     __shared__ float red[kMergeThreads / 64];
-    __shared__ float half_o[D];
+    __shared__ float part[kMergeGroups][kMergeDims];
     const int row_id = blockIdx.x; // (b, t, qh)
     const int qh = row_id % a.Hq;
     const int t = (row_id / a.Hq) % a.T;
@@ -540,16 +673,13 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int sg = tid / kMergeDims;
+    const int d = blockIdx.y * kMergeDims + (tid - sg * kMergeDims);
 
-    // Issue the first partial-row loads before any reduction: thread (half, d) owns splits
-    // s = half + 2k.
-    constexpr int kPre = 16;
-    const int half = tid / D;
-    const int d = tid - half * D;
-    float pre[kPre];
+    float pre[kMergePre];
 #pragma unroll
-    for (int k = 0; k < kPre; ++k) {
-        const int s = half + 2 * k;
+    for (int k = 0; k < kMergePre; ++k) {
+        const int s = sg + kMergeGroups * k;
         pre[k] = s < a.nsplit ? po[static_cast<int64_t>(s) * 32 * D + r * D + d] : 0.0f;
     }
     float M = -INFINITY;
@@ -576,23 +706,28 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     __syncthreads();
     lsum = (red[0] + red[1]) + (red[2] + red[3]);
 
+    // A split with zero weight (no visible key) never wrote its partial rows: skip it rather than
+    // multiply whatever the workspace holds by zero.
     float o = 0.0f;
     if (lsum > 0.0f) {
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) {
-            const int s = half + 2 * k;
-            if (s < a.nsplit) { o = fmaf(pre[k], wts[s], o); }
+        for (int k = 0; k < kMergePre; ++k) {
+            const int s = sg + kMergeGroups * k;
+            if (s < a.nsplit) { o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o; }
         }
 #pragma unroll 4
-        for (int s = half + 2 * kPre; s < a.nsplit; s += 2) {
-            o = fmaf(po[static_cast<int64_t>(s) * 32 * D + r * D + d], wts[s], o);
+        for (int s = sg + kMergeGroups * kMergePre; s < a.nsplit; s += kMergeGroups) {
+            const float v = po[static_cast<int64_t>(s) * 32 * D + r * D + d];
+            o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
     }
-    if (half == 1) { half_o[d] = o; }
+    part[sg][tid - sg * kMergeDims] = o;
     __syncthreads();
-    if (half == 0) {
-        o += half_o[d];
-        const float val = lsum > 0.0f ? o / lsum : 0.0f;
+    if (tid < kMergeDims) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kMergeGroups; ++k) { acc += part[k][tid]; }
+        const float val = lsum > 0.0f ? acc / lsum : 0.0f;
         const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
         if (a.out_f32) {
             static_cast<float*>(a.out)[oi] = val;
@@ -741,7 +876,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.row_chunks = plan.row_chunks;
     mg.nsplit = plan.nsplit;
     mg.out_f32 = out_f32 ? 1 : 0;
-    hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq), dim3(kMergeThreads), 0, stream, mg);
+    hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     check_launch("verify_attn_merge_kernel");
 }
 

@@ -180,3 +180,10 @@ class Graph:
 
 def synchronize() -> None:
     check(lib().nmi_rt_device_synchronize())
+
+
+def memcpy_dtod(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int, stream: Stream | None = None) -> None:
+    """Stream-ordered device-to-device copy of `nbytes` (hipMemcpyAsync)."""
+    assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+    check(lib().nmi_rt_memcpy_dtod(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), nbytes,
+                                   stream.handle if stream else None))

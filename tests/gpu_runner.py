@@ -26,6 +26,7 @@ def run_attention(case, out_f32=False, mode="A1", cache=None, stream=None, envel
     out = DeviceArray(na.FP32 if out_f32 else na.BF16, (D, Hq, T, B))
     env = envelope or (1, case.max_context)
     ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(Hq, Hkv, D, T, B, env[1]))
+    ws.fill(0xFF)  # NaN bit patterns: the op may not depend on what scratch held before
     view = cache.view()
     if mode == "A1":
         ops.gqa_attention(q.tensor(), k.tensor(), v.tensor(), pos.tensor(), case.scale, view, env, ws,

@@ -66,15 +66,22 @@ def test_outliers_long(gpu):
 
 
 def test_a2_then_a3_equals_a1(gpu):
+    """A2 then A3 against A1: identical cache bytes, and outputs within the reference's A1/A3 parity
+    criterion (attention_bf16 composite, tests/ops/test_gqa_attention.cpp:1077-1078). A1 attends to
+    the new rows from registers, A3 reads them back, so the sums are ordered differently."""
     case = AttnCase([3000], T=4, seed=11)
     expected_cache, ref = case.oracle_after_append()
     cache = gpu_runner.upload_cache(case)
     gpu_runner.append(case, cache)
     _check_cache(cache, expected_cache)
     out3, _ = gpu_runner.run_attention(case, out_f32=True, mode="A3", cache=cache)
-    out1, _ = gpu_runner.run_attention(case, out_f32=True, mode="A1")
-    assert np.array_equal(out1, out3), "A1 and A2+A3 differ"
+    out1, cache1 = gpu_runner.run_attention(case, out_f32=True, mode="A1")
+    _check_cache(cache1, expected_cache)
+    ok, msg = reference_composite_ok(out1, out3)
+    assert ok, f"A1/A3 parity: {msg}"
+    assert rel_l2(out1, out3) <= 5e-4
     _check_out(out3, ref, REL_L2_F32)
+    _check_out(out1, ref, REL_L2_F32)
 
 
 def test_future_token_isolation(gpu):
