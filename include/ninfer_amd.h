@@ -37,14 +37,15 @@ typedef enum nmi_status {
     NMI_UNSUPPORTED = 4       /* valid request outside the built kernel set */
 } nmi_status;
 
-/* src/core/dtype.h */
+/* src/core/dtype.h:8-16 — same values as ninfer::DType, so a binding converts with a cast. */
 typedef enum nmi_dtype {
     NMI_BF16 = 0,
-    NMI_FP16 = 1,
-    NMI_FP32 = 2,
-    NMI_I8 = 3,
-    NMI_I32 = 4,
-    NMI_I64 = 5
+    NMI_FP32 = 1,
+    NMI_I32 = 2,
+    NMI_U8 = 3,
+    NMI_I64 = 4,
+    NMI_I8 = 5,
+    NMI_FP16 = 6
 } nmi_dtype;
 
 /* src/core/tensor.h:11-15 */

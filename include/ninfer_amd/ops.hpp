@@ -18,7 +18,7 @@
 
 namespace ninfer_amd {
 
-enum class DType : int32_t { BF16 = NMI_BF16, FP16 = NMI_FP16, FP32 = NMI_FP32, I8 = NMI_I8, I32 = NMI_I32, I64 = NMI_I64 };
+enum class DType : int32_t { BF16 = NMI_BF16, FP32 = NMI_FP32, I32 = NMI_I32, U8 = NMI_U8, I64 = NMI_I64, I8 = NMI_I8, FP16 = NMI_FP16 };
 
 inline std::size_t dtype_size(DType d) {
     switch (d) {
@@ -26,7 +26,8 @@ inline std::size_t dtype_size(DType d) {
     case DType::FP16: return 2;
     case DType::FP32:
     case DType::I32: return 4;
-    case DType::I8: return 1;
+    case DType::I8:
+    case DType::U8: return 1;
     case DType::I64: return 8;
     }
     return 0;

@@ -9,7 +9,7 @@ Layers:
 from __future__ import annotations
 
 from . import _capi
-from ._capi import (BF16, FP16, FP32, I8, I32, I64, CommitEnvelope, GeneralConfig, GqaEnvelope,
+from ._capi import (BF16, FP16, FP32, I8, I32, I64, U8, CommitEnvelope, GeneralConfig, GqaEnvelope,
                     KVLayerView, SamplingConfig, Tensor, lib)
 
 __all__ = [

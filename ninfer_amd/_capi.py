@@ -14,8 +14,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libninfer_amd.so"
 # nmi_status
 OK, INVALID_ARGUMENT, OVERFLOW, HIP_ERROR, UNSUPPORTED = 0, 1, 2, 3, 4
 # nmi_dtype
-BF16, FP16, FP32, I8, I32, I64 = 0, 1, 2, 3, 4, 5
-DTYPE_SIZE = {BF16: 2, FP16: 2, FP32: 4, I8: 1, I32: 4, I64: 8}
+# ninfer::DType values (src/core/dtype.h:8-16)
+BF16, FP32, I32, U8, I64, I8, FP16 = 0, 1, 2, 3, 4, 5, 6
+DTYPE_SIZE = {BF16: 2, FP16: 2, FP32: 4, I8: 1, U8: 1, I32: 4, I64: 8}
 
 
 class Tensor(C.Structure):

@@ -79,7 +79,8 @@ inline size_t dtype_size(int32_t dt) {
     case NMI_FP16: return 2;
     case NMI_FP32:
     case NMI_I32: return 4;
-    case NMI_I8: return 1;
+    case NMI_I8:
+    case NMI_U8: return 1;
     case NMI_I64: return 8;
     default: throw InvalidArgument("unknown dtype");
     }

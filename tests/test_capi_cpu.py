@@ -176,3 +176,13 @@ def test_sampling_config_layout_matches_reference():
     (include/ninfer/ops/sampling.h:24-33)."""
     assert C.sizeof(na.SamplingConfig) == 40
     assert na.SamplingConfig.seed.offset == 24 and na.SamplingConfig.token_counts.offset == 32
+
+
+def test_dtype_values_match_reference_enum():
+    """nmi_dtype carries ninfer::DType's values (src/core/dtype.h:8-16), so a reference-side
+    binding converts a Tensor's dtype with a cast."""
+    assert (na.BF16, na.FP32, na.I32, na.U8, na.I64, na.I8, na.FP16) == (0, 1, 2, 3, 4, 5, 6)
+    hdr = (ROOT / "include" / "ninfer_amd.h").read_text()
+    for name, val in (("NMI_BF16", 0), ("NMI_FP32", 1), ("NMI_I32", 2), ("NMI_U8", 3), ("NMI_I64", 4),
+                      ("NMI_I8", 5), ("NMI_FP16", 6)):
+        assert re.search(rf"\b{name} = {val}\b", hdr), name
