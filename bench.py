@@ -181,6 +181,43 @@ def accept_launch(dev, stream, greedy_argmax):
                                          dev["cfg"].ptr, dev["ws"], stream)
 
 
+def make_general_inputs(B, K, seed):
+    """Mode F inputs: target logits N(0,3) BF16 [V, K+1, B], draft logits correlated 0.9
+    with the target, drafts = each draft column's top token, seeded uniforms, T=0.7, top-p 0.95."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    rng = np.random.default_rng(seed)
+    std = np.sqrt(3.0)
+    t = rng.standard_normal((B, K + 1, VOCAB), dtype=np.float32) * std
+    d = 0.9 * t[:, :K, :] + np.sqrt(1 - 0.81) * rng.standard_normal((B, K, VOCAB), dtype=np.float32) * std
+    tb, db = syn.f32_to_bf16_bits(t), syn.f32_to_bf16_bits(d.astype(np.float32))
+    drafts = np.argmax(syn.bf16_bits_to_f32(db), axis=2).astype(np.int32)
+    cfg = na.GeneralConfig()
+    cfg.temperature, cfg.top_p = 0.7, 0.95
+    cbuf = DeviceBuffer(8)
+    cbuf.upload(np.frombuffer(bytes(memoryview(cfg)), np.uint8))
+    dev = dict(t=DeviceArray.from_numpy(na.BF16, tb, (VOCAB, K + 1, B)),
+               d=DeviceArray.from_numpy(na.BF16, db, (VOCAB, K, B)),
+               drafts=DeviceArray.from_numpy(na.I32, drafts, (K, B)),
+               ua=DeviceArray.from_numpy(na.FP32, rng.random((B, K + 1), dtype=np.float32), (K + 1, B)),
+               ur=DeviceArray.from_numpy(na.FP32, rng.random(B, dtype=np.float32), (1, B)),
+               length=DeviceArray.from_numpy(na.I32, np.full(B, 4096, np.int32), (B,)),
+               token=DeviceArray(na.I32, (B,)), so=DeviceArray(na.I32, (K + 1, B)), ns=DeviceArray(na.I32, (B,)),
+               acc=DeviceArray(na.I32, (B,)),
+               stats=DeviceArray.from_numpy(na.I64, np.zeros((B, 4 + K), np.int64), (4 + K, B)), cfg=cbuf,
+               ws=DeviceBuffer(ops.general_accept_workspace_bytes(VOCAB, K, B)))
+    return dev
+
+
+def general_launch(dev, stream):
+    from ninfer_amd import ops
+    ops.speculative_accept_general(dev["t"].tensor(), dev["d"].tensor(), dev["drafts"].tensor(), dev["ua"].tensor(),
+                                   dev["ur"].tensor(), dev["length"].tensor(), dev["token"].tensor(),
+                                   dev["so"].tensor(), dev["ns"].tensor(), dev["acc"].tensor(), dev["stats"].tensor(),
+                                   VOCAB, dev["cfg"].ptr, dev["ws"], stream)
+
+
 def cpu_baseline(sample_layers: int):
     """Oracle attention on the host for `sample_layers` C2 layers (reported only)."""
     from oracle import pyoracle
@@ -254,6 +291,32 @@ def main():
         log(f"copy 256 MiB: {2 * nbytes * 5 / (e0.elapsed_ms(e1) * 1e-3) / 1e9:.0f} GB/s (read + write)")
         return
 
+    # ---- C3: layers at context 260,096, allocated first (as a server allocates its KV planes) -----------------------------------------------------------
+    if (args.only in (None, "c3")) and not args.skip_long:
+        L3 = 260096
+        t0 = time.perf_counter()
+        first = Layer(L3, L3 + T, seed=3, outliers=True)
+        # C3_LAYERS layers with planes of their own (0.55 GB each, far beyond the 256 MB Infinity
+        # Cache) in one graph, as consecutive layers of a model run: per-layer time without the
+        # graph launch overhead of a one-kernel graph.
+        c3_layers = [first] + [Layer(L3, L3 + T, seed=4 + i, outliers=True, copy_from=first) for i in range(C3_LAYERS - 1)]
+        log(f"C3: {C3_LAYERS} layers generated + quantized in {time.perf_counter() - t0:.1f}s")
+        ws3 = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L3 + T))
+        g3 = capture(stream, lambda: [ly.launch(ws3, stream) for ly in c3_layers])
+        ms3, p95_3, _ = time_graph(g3, stream, max(args.steps, 20), args.warmup)
+        ms3 /= C3_LAYERS
+        p95_3 /= C3_LAYERS
+        if args.only:
+            log(f"C3 {ms3 * 1e3:.1f} us/layer")
+            return
+        gbs3 = attn_bytes(L3) / (ms3 * 1e-3) / 1e9
+        result["c3"] = dict(us_per_layer=ms3 * 1e3, us_per_layer_p95=p95_3 * 1e3, gbs=gbs3,
+                            bytes_per_layer=attn_bytes(L3), frac_of_peak=gbs3 / HBM_PEAK_GBS,
+                            target_us=attn_bytes(L3) / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6)
+        log(f"C3: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+        del c3_layers, first, g3
+        device.synchronize()
+
     # ---- C2: 64 layers at context 7680 + greedy acceptance --------------------------------------
     if args.only in (None, "c2"):
         L2 = 7680
@@ -293,32 +356,6 @@ def main():
         del layers, g_attn, g_step
         device.synchronize()
 
-    # ---- C3: one layer at context 260,096 -----------------------------------------------------------
-    if (args.only in (None, "c3")) and not args.skip_long:
-        L3 = 260096
-        t0 = time.perf_counter()
-        first = Layer(L3, L3 + T, seed=3, outliers=True)
-        # C3_LAYERS layers with planes of their own (0.55 GB each, far beyond the 256 MB Infinity
-        # Cache) in one graph, as consecutive layers of a model run: per-layer time without the
-        # graph launch overhead of a one-kernel graph.
-        c3_layers = [first] + [Layer(L3, L3 + T, seed=4 + i, outliers=True, copy_from=first) for i in range(C3_LAYERS - 1)]
-        log(f"C3: {C3_LAYERS} layers generated + quantized in {time.perf_counter() - t0:.1f}s")
-        ws3 = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L3 + T))
-        g3 = capture(stream, lambda: [ly.launch(ws3, stream) for ly in c3_layers])
-        ms3, p95_3, _ = time_graph(g3, stream, max(args.steps, 20), args.warmup)
-        ms3 /= C3_LAYERS
-        p95_3 /= C3_LAYERS
-        if args.only:
-            log(f"C3 {ms3 * 1e3:.1f} us/layer")
-            return
-        gbs3 = attn_bytes(L3) / (ms3 * 1e-3) / 1e9
-        result["c3"] = dict(us_per_layer=ms3 * 1e3, us_per_layer_p95=p95_3 * 1e3, gbs=gbs3,
-                            bytes_per_layer=attn_bytes(L3), frac_of_peak=gbs3 / HBM_PEAK_GBS,
-                            target_us=attn_bytes(L3) / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6)
-        log(f"C3: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
-        del c3_layers, first, g3
-        device.synchronize()
-
     # ---- sampler: top-20 stochastic acceptance at B=1 and B=16 --------------------------------------
     if args.only in (None, "sampler"):
         sres = {}
@@ -329,11 +366,18 @@ def main():
             sres[f"b{B}_us"] = ms * 1e3
             sres[f"b{B}_us_per_seq"] = ms * 1e3 / B
             sres[f"b{B}_p95_us"] = p95 * 1e3
+        for B in (1, 16):
+            gdev = make_general_inputs(B, 3, seed=60 + B)
+            g = capture(stream, lambda: general_launch(gdev, stream))
+            ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)
+            sres[f"mode_f_b{B}_us"] = ms * 1e3
+            sres[f"mode_f_b{B}_us_per_seq"] = ms * 1e3 / B
         if args.only:
             log(f"sampler {sres}")
             return
         result["sampler"] = sres
-        log(f"sampler: B=1 {sres['b1_us']:.1f} us, B=16 {sres['b16_us_per_seq']:.2f} us/seq")
+        log(f"sampler: B=1 {sres['b1_us']:.1f} us, B=16 {sres['b16_us_per_seq']:.2f} us/seq; "
+            f"Mode F B=1 {sres['mode_f_b1_us']:.1f} us, B=16 {sres['mode_f_b16_us_per_seq']:.2f} us/seq")
 
     cpu = None
     if not args.skip_cpu:
@@ -370,7 +414,8 @@ def main():
         line["long_context"] = {"workload": "C3: context 260096, 1% outliers +-20, one layer",
                                 **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3"].items()}}
     if "sampler" in result:
-        line["sampler"] = {"workload": "top-20 stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95",
+        line["sampler"] = {"workload": "stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95: Mode R (top-20 cap) "
+                                       "and Mode F (full vocabulary, draft logits correlated 0.9)",
                            **{k: round(v, 2) for k, v in result["sampler"].items()}}
     line["roofline"] = {
         "bound": "hbm",

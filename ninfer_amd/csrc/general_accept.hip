@@ -1,2 +1,587 @@
-// General speculative acceptance ("Mode F") on gfx950 — see capi_general.cpp.
+// General speculative acceptance ("Mode F", no reference counterpart) on gfx950.
+//
+// Semantics (bit-exact with the CPU oracle's orc_general_accept): for every target column i
+// (0..K) and draft column i (0..K-1) the distribution is the full-vocabulary softmax at the
+// configured temperature in 2^40 fixed point, W_v = rint(det_expf(fma(x_v, 1/T, -xmax/T)) * 2^40),
+// truncated by top-p to the shortest prefix in (value desc, id asc) order whose mass reaches
+// floor(z * p24 / 2^24) (p24 = rint(top_p * 2^24)). Draft i is accepted iff
+// u24(u_accept[i]) * q_i(d_i) < p_i(d_i), compared exactly in 128 bits over the common denominator.
+// At the first rejection the token is drawn from the normalized residual max(0, p_i - q_i)
+// (weights (W^p_v z_q - W^q_v z_p) >> 40, falling back to p_i when the residual is empty) with
+// u_residual; after K acceptances it is drawn from p_K with u_accept[K]. Draws are inverse-CDF over
+// token ids in ascending order.
+//
+// Every quantity is an integer except W, which depends only on a token's BF16 value, so the
+// nucleus is found without sorting: a coarse histogram (high byte of the 16-bit ordered value) of
+// counts and masses, then a fine histogram inside the crossing coarse bin, then the rank of the
+// last included token among equal values (ids ascending). The nucleus collapses to one 64-bit
+// key threshold: token v is a member iff sort_key(x_v, v) >= kstar.
+//
+// Launches (tiles of 4096 tokens, all columns and sequences in one grid each):
+//   1 gen_max      tile maxima; zero the coarse histograms
+//   2 gen_coarse   per-token weights -> coarse counts and masses (LDS, then global atomics)
+//   3 gen_cross    per column: total mass, top-p target, crossing coarse bin
+//   4 gen_fine     per tile: counts of the 256 values inside the crossing bin
+//   5 gen_nucleus  per column: crossing value, rank cut, kstar and nucleus mass
+//   6 gen_totals   per tile: accept decision (recomputed per block), masses of the draw
+//   7 gen_pick     per sequence: locate the draw, commit the round
 #include "common.h"
+#include "device_utils.h"
+#include "general_internal.h"
+#include "sampler_common.h"
+
+#pragma clang fp contract(off)
+
+namespace nmi {
+namespace {
+
+typedef unsigned __int128 u128;
+
+constexpr int kThreads = 256;
+constexpr int kPerThread = kGenTile / kThreads; // 16 consecutive tokens per thread in rescans
+
+struct ColDesc {
+    float m;          // xmax / T
+    float inv_temp;   // 1 / T
+    int32_t c1;       // crossing coarse bin
+    int32_t nucleus;  // top-p truncates
+    uint64_t cum1;    // mass above the crossing coarse bin
+    uint64_t target;  // floor(z * p24 / 2^24)
+    uint64_t z;       // full mass
+    uint64_t zs;      // nucleus mass
+    uint64_t kstar;   // members: sort_key(x_v, v) >= kstar
+    uint64_t pad;
+};
+static_assert(sizeof(ColDesc) == kGenDescBytes, "descriptor size");
+
+struct GenArgs {
+    const uint16_t* logits;
+    const uint16_t* draft_logits;
+    const int32_t* drafts;
+    const float* u_accept;
+    const float* u_residual;
+    int32_t* length;
+    int32_t* token;
+    int32_t* sampled_out;
+    int32_t* num_sampled;
+    int32_t* accepted;
+    int64_t* stats;
+    const nmi_general_config* config;
+    int64_t logit_col;   // elements between target columns
+    int64_t logit_seq;   // elements between sequences
+    int64_t draft_col;
+    int64_t draft_seq;
+    int32_t stats_stride;
+    int32_t V;
+    int32_t K;
+    int32_t ncols;
+    int32_t ntiles;
+    float* tile_max;
+    uint64_t* cmass;
+    uint32_t* ccount;
+    ColDesc* desc;
+    uint32_t* fine;
+    uint64_t* tile_res;
+    uint64_t* tile_p;
+};
+
+__device__ __forceinline__ const uint16_t* column_ptr(const GenArgs& a, int b, int c) {
+    if (c <= a.K) { return a.logits + b * a.logit_seq + c * a.logit_col; }
+    return a.draft_logits + b * a.draft_seq + (c - a.K - 1) * a.draft_col;
+}
+
+__device__ __forceinline__ uint32_t fixed_u24(float u) {
+    float s = __builtin_rintf(u * 16777216.0f);
+    s = fmaxf(0.0f, fminf(16777216.0f, s));
+    return static_cast<uint32_t>(s);
+}
+
+__device__ __forceinline__ uint64_t gen_weight(float x, float inv_temp, float m) {
+    const float w = det_expf(__builtin_fmaf(x, inv_temp, -m));
+    return static_cast<uint64_t>(__builtin_rintf(w * 1099511627776.0f)); // 2^40
+}
+
+// 16-bit ordered value of a BF16 token (the high half of the ordered-float key).
+__device__ __forceinline__ uint32_t ordered16(float x) { return ordered_float(x) >> 16; }
+
+__device__ __forceinline__ float value_of_ordered16(uint32_t o) {
+    const uint32_t bits = (o & 0x8000u) ? (o ^ 0x8000u) : (~o & 0xffffu);
+    return bf16_to_f32(static_cast<uint16_t>(bits));
+}
+
+// Block-wide inclusive scan over 256 threads (Hillis-Steele in LDS).
+template <typename T>
+__device__ T block_scan(T v, T* sh) {
+    const int tid = threadIdx.x;
+    sh[tid] = v;
+    __syncthreads();
+#pragma unroll 1
+    for (int off = 1; off < kThreads; off <<= 1) {
+        const T add = tid >= off ? sh[tid - off] : T(0);
+        __syncthreads();
+        sh[tid] += add;
+        __syncthreads();
+    }
+    const T r = sh[tid];
+    __syncthreads();
+    return r;
+}
+
+// Smallest thread index with `pred`, or kThreads.
+__device__ int block_first(bool pred, int* sh) {
+    if (threadIdx.x == 0) { *sh = kThreads; }
+    __syncthreads();
+    if (pred) { atomicMin(sh, static_cast<int>(threadIdx.x)); }
+    __syncthreads();
+    const int r = *sh;
+    __syncthreads();
+    return r;
+}
+
+__device__ float block_max(float v, float* sh) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) { sh[threadIdx.x >> 6] = v; }
+    __syncthreads();
+    const float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ bool member(const ColDesc& d, float x, int v) {
+    return sort_key(x, v) >= d.kstar;
+}
+
+__device__ __forceinline__ uint64_t member_weight(const ColDesc& d, float x, int v) {
+    return member(d, x, v) ? gen_weight(x, d.inv_temp, d.m) : 0ull;
+}
+
+// ---- 1: tile maxima ----------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_max_kernel(GenArgs a) {
+    __shared__ float red[kThreads / 64];
+    const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const uint16_t* col = column_ptr(a, b, c);
+    const int v0 = t * kGenTile;
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
+        const int v = v0 + i;
+        if (v < a.V) { mx = fmaxf(mx, bf16_to_f32(col[v])); }
+    }
+    mx = block_max(mx, red);
+    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    if (threadIdx.x == 0) { a.tile_max[cb * a.ntiles + t] = mx; }
+    if (t == 0) {
+        a.cmass[cb * kGenBins + threadIdx.x] = 0;
+        a.ccount[cb * kGenBins + threadIdx.x] = 0;
+    }
+}
+
+__device__ void column_scale(const GenArgs& a, int64_t cb, float* red, float* m, float* inv_temp) {
+    float mx = -INFINITY;
+    for (int i = threadIdx.x; i < a.ntiles; i += kThreads) { mx = fmaxf(mx, a.tile_max[cb * a.ntiles + i]); }
+    mx = block_max(mx, red);
+    *inv_temp = 1.0f / a.config->temperature;
+    *m = mx * *inv_temp;
+}
+
+// ---- 2: coarse histogram of counts and masses ----------------------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
+    __shared__ uint32_t cnt[kGenBins];
+    __shared__ uint64_t mass[kGenBins];
+    __shared__ float red[kThreads / 64];
+    const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    cnt[threadIdx.x] = 0;
+    mass[threadIdx.x] = 0;
+    float m, inv_temp;
+    column_scale(a, cb, red, &m, &inv_temp); // synchronizes the block
+    const uint16_t* col = column_ptr(a, b, c);
+    const int v0 = t * kGenTile;
+    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
+        const int v = v0 + i;
+        if (v >= a.V) { break; }
+        const float x = bf16_to_f32(col[v]);
+        const uint32_t bin = ordered16(x) >> 8;
+        atomicAdd(&cnt[bin], 1u);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x, inv_temp, m)));
+    }
+    __syncthreads();
+    if (cnt[threadIdx.x] != 0) {
+        atomicAdd(&a.ccount[cb * kGenBins + threadIdx.x], cnt[threadIdx.x]);
+        atomicAdd(reinterpret_cast<unsigned long long*>(&a.cmass[cb * kGenBins + threadIdx.x]),
+                  static_cast<unsigned long long>(mass[threadIdx.x]));
+    }
+}
+
+// ---- 3: total mass, top-p target, crossing coarse bin ------------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_cross_kernel(GenArgs a) {
+    __shared__ uint64_t sh[kThreads];
+    __shared__ float red[kThreads / 64];
+    __shared__ int first;
+    const int c = blockIdx.x, b = blockIdx.y;
+    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    float m, inv_temp;
+    column_scale(a, cb, red, &m, &inv_temp);
+    const int bin = kGenBins - 1 - static_cast<int>(threadIdx.x); // descending value order
+    const uint32_t count = a.ccount[cb * kGenBins + bin];
+    const uint64_t mass = a.cmass[cb * kGenBins + bin];
+    const uint64_t incl = block_scan<uint64_t>(mass, sh);
+    __shared__ uint64_t total;
+    if (threadIdx.x == kThreads - 1) { total = incl; }
+    __syncthreads();
+    const uint64_t Z = total;
+    const float top_p = a.config->top_p;
+    ColDesc d{};
+    d.m = m;
+    d.inv_temp = inv_temp;
+    d.z = Z;
+    if (!(top_p < 1.0f)) {
+        if (threadIdx.x == 0) {
+            d.c1 = -1;
+            d.nucleus = 0;
+            d.zs = Z;
+            d.kstar = 0;
+            a.desc[cb] = d;
+        }
+        return;
+    }
+    const uint64_t target = static_cast<uint64_t>((static_cast<u128>(Z) * fixed_u24(top_p)) >> 24);
+    const int f = block_first(count != 0 && incl >= target, &first);
+    if (static_cast<int>(threadIdx.x) == f) {
+        d.c1 = bin;
+        d.nucleus = 1;
+        d.cum1 = incl - mass;
+        d.target = target;
+        a.desc[cb] = d;
+    }
+}
+
+// ---- 4: fine counts inside the crossing coarse bin, per tile -----------------------------------
+__global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
+    __shared__ uint32_t cnt[kGenBins];
+    const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
+    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    const ColDesc d = a.desc[cb];
+    if (!d.nucleus) { return; }
+    cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const uint16_t* col = column_ptr(a, b, c);
+    const int v0 = t * kGenTile;
+    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
+        const int v = v0 + i;
+        if (v >= a.V) { break; }
+        const uint32_t o = ordered16(bf16_to_f32(col[v]));
+        if (static_cast<int>(o >> 8) == d.c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
+    }
+    __syncthreads();
+    a.fine[(cb * a.ntiles + t) * kGenBins + threadIdx.x] = cnt[threadIdx.x];
+}
+
+// ---- 5: crossing value, rank cut among equal values, kstar --------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
+    __shared__ uint64_t sh[kThreads];
+    __shared__ int first;
+    __shared__ uint64_t bcast[4];
+    const int c = blockIdx.x, b = blockIdx.y;
+    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    ColDesc d = a.desc[cb];
+    if (!d.nucleus) { return; }
+    if (threadIdx.x == 0) { bcast[0] = 1; bcast[1] = d.z; bcast[2] = static_cast<uint64_t>(d.c1) << 8; bcast[3] = 1; }
+    __syncthreads();
+    // Fine bin f = 255 - tid (descending value order).
+    const uint32_t f = kGenBins - 1 - threadIdx.x;
+    uint64_t count = 0;
+    for (int t = 0; t < a.ntiles; ++t) { count += a.fine[(cb * a.ntiles + t) * kGenBins + f]; }
+    const uint32_t o16 = (static_cast<uint32_t>(d.c1) << 8) | f;
+    const float x = value_of_ordered16(o16);
+    const uint64_t w = gen_weight(x, d.inv_temp, d.m);
+    const uint64_t mass = count * w;
+    const uint64_t incl = block_scan<uint64_t>(mass, sh);
+    const int fs = block_first(count != 0 && d.cum1 + incl >= d.target, &first);
+    if (static_cast<int>(threadIdx.x) == fs) {
+        const uint64_t before = d.cum1 + incl - mass;
+        // smallest j >= 1 with before + j * w >= target (w > 0 at the crossing)
+        uint64_t j = d.target > before ? (d.target - before + w - 1) / w : 0;
+        j = j < 1 ? 1 : (j > count ? count : j);
+        bcast[0] = j;
+        bcast[1] = before + j * w;
+        bcast[2] = o16;
+    }
+    __syncthreads();
+    const uint64_t j = bcast[0];
+    const uint32_t vstar = static_cast<uint32_t>(bcast[2]);
+    // Tile holding the j-th token of value vstar (ids ascending).
+    const uint32_t fstar = vstar & 0xffu;
+    uint64_t tc = 0;
+    if (static_cast<int>(threadIdx.x) < a.ntiles) { tc = a.fine[(cb * a.ntiles + threadIdx.x) * kGenBins + fstar]; }
+    const uint64_t tincl = block_scan<uint64_t>(tc, sh);
+    const int ts = block_first(static_cast<int>(threadIdx.x) < a.ntiles && tincl >= j, &first);
+    if (static_cast<int>(threadIdx.x) == ts) { bcast[3] = j - (tincl - tc); } // 1-based rank in tile
+    __syncthreads();
+    const uint64_t rank = bcast[3];
+    // Rescan that tile: thread i owns tokens [16 i, 16 i + 16) of it.
+    const uint16_t* col = column_ptr(a, b, c);
+    const int v0 = ts * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    uint64_t mine = 0;
+    for (int k = 0; k < kPerThread; ++k) {
+        const int v = v0 + k;
+        if (v < a.V && ordered16(bf16_to_f32(col[v])) == vstar) { ++mine; }
+    }
+    const uint64_t mincl = block_scan<uint64_t>(mine, sh);
+    if (mine != 0 && mincl >= rank && mincl - mine < rank) {
+        uint64_t need = rank - (mincl - mine);
+        for (int k = 0; k < kPerThread; ++k) {
+            const int v = v0 + k;
+            if (v < a.V && ordered16(bf16_to_f32(col[v])) == vstar && --need == 0) {
+                d.kstar = sort_key(value_of_ordered16(vstar), v);
+                d.zs = bcast[1];
+                a.desc[cb] = d;
+                break;
+            }
+        }
+    }
+}
+
+// Accept decisions of sequence b (identical in every block that evaluates them). Returns a; sets
+// *rejected to the rejected column (or -1 when all K drafts are accepted).
+__device__ int decide(const GenArgs& a, int b, int* rejected) {
+    for (int i = 0; i < a.K; ++i) {
+        const int d = a.drafts[b * a.K + i];
+        const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + i];
+        const ColDesc q = a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + i];
+        // A draft id outside the token domain has no mass under either distribution: rejected.
+        const bool in_domain = d >= 0 && d < a.V;
+        const float xp = in_domain ? bf16_to_f32(column_ptr(a, b, i)[d]) : 0.0f;
+        const float xq = in_domain ? bf16_to_f32(column_ptr(a, b, a.K + 1 + i)[d]) : 0.0f;
+        const uint64_t wp = in_domain ? member_weight(p, xp, d) : 0ull;
+        const uint64_t wq = in_domain ? member_weight(q, xq, d) : 0ull;
+        const u128 lhs = static_cast<u128>(fixed_u24(a.u_accept[b * (a.K + 1) + i])) * wq * p.zs;
+        const u128 rhs = (static_cast<u128>(wp) * q.zs) << 24;
+        if (!(lhs < rhs)) {
+            *rejected = i;
+            return i;
+        }
+    }
+    *rejected = -1;
+    return a.K;
+}
+
+// Draw weights of token v: residual (column pair i) or p (column i); both from one read.
+struct DrawMass {
+    uint64_t res;
+    uint64_t p;
+};
+
+__device__ __forceinline__ DrawMass draw_mass(const GenArgs& a, int b, int col_p, int rejected, const ColDesc& p,
+                                              const ColDesc& q, int v) {
+    DrawMass r;
+    const float xp = bf16_to_f32(column_ptr(a, b, col_p)[v]);
+    r.p = member_weight(p, xp, v);
+    r.res = 0;
+    if (rejected >= 0) {
+        const float xq = bf16_to_f32(column_ptr(a, b, a.K + 1 + rejected)[v]);
+        const uint64_t wq = member_weight(q, xq, v);
+        const u128 pv = static_cast<u128>(r.p) * q.zs;
+        const u128 qv = static_cast<u128>(wq) * p.zs;
+        r.res = pv > qv ? static_cast<uint64_t>((pv - qv) >> 40) : 0ull;
+    }
+    return r;
+}
+
+// ---- 6: per-tile masses of the draw --------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
+    __shared__ u128 shr[kThreads];
+    __shared__ uint64_t shp[kThreads];
+    const int t = blockIdx.x, b = blockIdx.y;
+    int rejected;
+    const int acc = decide(a, b, &rejected);
+    const int col_p = rejected >= 0 ? rejected : a.K;
+    const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
+    const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
+    (void)acc;
+    u128 res = 0;
+    uint64_t pm = 0;
+    const int v0 = t * kGenTile;
+    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
+        const int v = v0 + i;
+        if (v >= a.V) { break; }
+        const DrawMass dm = draw_mass(a, b, col_p, rejected, p, q, v);
+        res += dm.res;
+        pm += dm.p;
+    }
+    const u128 rtot = block_scan<u128>(res, shr);
+    const uint64_t ptot = block_scan<uint64_t>(pm, shp);
+    if (threadIdx.x == kThreads - 1) {
+        a.tile_res[(static_cast<int64_t>(b) * a.ntiles + t) * 2] = static_cast<uint64_t>(rtot);
+        a.tile_res[(static_cast<int64_t>(b) * a.ntiles + t) * 2 + 1] = static_cast<uint64_t>(rtot >> 64);
+        a.tile_p[static_cast<int64_t>(b) * a.ntiles + t] = ptot;
+    }
+}
+
+// ---- 7: locate the draw (first id whose running mass exceeds floor(total * u24 / 2^24), else the
+// last id with mass) and commit the round --------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
+    __shared__ u128 sh[kThreads];
+    __shared__ int first;
+    __shared__ int last_tile;
+    __shared__ int result;
+    const int b = blockIdx.x;
+    int rejected;
+    const int acc = decide(a, b, &rejected);
+    const int col_p = rejected >= 0 ? rejected : a.K;
+    const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
+    const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
+    // Tile totals of the chosen weights (residual, or p when there is no residual mass).
+    u128 rtot = 0;
+    if (static_cast<int>(threadIdx.x) < a.ntiles) {
+        const int64_t ti = static_cast<int64_t>(b) * a.ntiles + threadIdx.x;
+        rtot = (static_cast<u128>(a.tile_res[ti * 2 + 1]) << 64) | a.tile_res[ti * 2];
+    }
+    const u128 rincl = block_scan<u128>(rejected >= 0 ? rtot : u128(0), sh);
+    __shared__ u128 rall;
+    if (threadIdx.x == kThreads - 1) { rall = rincl; }
+    __syncthreads();
+    const bool use_res = rejected >= 0 && rall != 0;
+    u128 tt = 0;
+    if (static_cast<int>(threadIdx.x) < a.ntiles) {
+        tt = use_res ? rtot : static_cast<u128>(a.tile_p[static_cast<int64_t>(b) * a.ntiles + threadIdx.x]);
+    }
+    const u128 incl = block_scan<u128>(tt, sh);
+    __shared__ u128 total;
+    if (threadIdx.x == kThreads - 1) { total = incl; }
+    __syncthreads();
+    const float u = rejected >= 0 ? a.u_residual[b] : a.u_accept[b * (a.K + 1) + a.K];
+    const u128 goal = (total * fixed_u24(u)) >> 24;
+    int ts = block_first(static_cast<int>(threadIdx.x) < a.ntiles && tt != 0 && incl > goal, &first);
+    const bool crossing = ts < kThreads;
+    if (!crossing) {
+        // goal >= total: the draw is the last id with nonzero mass.
+        if (threadIdx.x == 0) { last_tile = 0; }
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < a.ntiles && tt != 0) { atomicMax(&last_tile, static_cast<int>(threadIdx.x)); }
+        __syncthreads();
+        ts = last_tile;
+    }
+    __shared__ u128 tile_before;
+    if (static_cast<int>(threadIdx.x) == ts) { tile_before = incl - tt; }
+    if (threadIdx.x == 0) { result = -1; }
+    __syncthreads();
+    // Rescan the tile: thread i owns tokens [16 i, 16 i + 16).
+    const int v0 = ts * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    uint64_t w[kPerThread];
+    u128 mine = 0;
+    for (int k = 0; k < kPerThread; ++k) {
+        const int v = v0 + k;
+        w[k] = 0;
+        if (v < a.V) {
+            const DrawMass dm = draw_mass(a, b, col_p, rejected, p, q, v);
+            w[k] = use_res ? dm.res : dm.p;
+        }
+        mine += w[k];
+    }
+    const u128 mincl = block_scan<u128>(mine, sh) + tile_before;
+    if (crossing) {
+        if (mine != 0 && mincl > goal && mincl - mine <= goal) {
+            u128 run = mincl - mine;
+            for (int k = 0; k < kPerThread; ++k) {
+                if (w[k] == 0) { continue; }
+                run += w[k];
+                if (goal < run) {
+                    result = v0 + k;
+                    break;
+                }
+            }
+        }
+    } else {
+        const int lastk = [&] {
+            int r = -1;
+            for (int k = 0; k < kPerThread; ++k) { if (w[k] != 0) { r = k; } }
+            return r;
+        }();
+        if (lastk >= 0) { atomicMax(&result, v0 + lastk); }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int tstar = result < 0 ? 0 : result;
+        commit_round(a.drafts + b * a.K, a.K, acc, tstar, a.length[b], a.length + b, a.token + b,
+                     a.sampled_out + b * (a.K + 1), a.num_sampled + b, a.accepted + b,
+                     a.stats + static_cast<int64_t>(b) * a.stats_stride);
+    }
+}
+
+} // namespace
+
+GenPlan plan_general(int32_t token_domain, int32_t K, int32_t B) {
+    GenPlan p;
+    p.ncols = 2 * K + 1;
+    p.ntiles = (token_domain + kGenTile - 1) / kGenTile;
+    const auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+    size_t at = 0;
+    const size_t cols = static_cast<size_t>(B) * p.ncols;
+    p.tile_max_offset = at;
+    at = align(at + cols * p.ntiles * sizeof(float));
+    p.cmass_offset = at;
+    at = align(at + cols * kGenBins * sizeof(uint64_t));
+    p.ccount_offset = at;
+    at = align(at + cols * kGenBins * sizeof(uint32_t));
+    p.desc_offset = at;
+    at = align(at + cols * kGenDescBytes);
+    p.fine_offset = at;
+    at = align(at + cols * p.ntiles * kGenBins * sizeof(uint32_t));
+    p.tile_res_offset = at;
+    at = align(at + static_cast<size_t>(B) * p.ntiles * 2 * sizeof(uint64_t));
+    p.tile_p_offset = at;
+    at = align(at + static_cast<size_t>(B) * p.ntiles * sizeof(uint64_t));
+    p.bytes = at;
+    return p;
+}
+
+void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* workspace, hipStream_t stream) {
+    char* ws = static_cast<char*>(workspace);
+    GenArgs a{};
+    a.logits = l.logits;
+    a.draft_logits = l.draft_logits;
+    a.drafts = l.drafts;
+    a.u_accept = l.u_accept;
+    a.u_residual = l.u_residual;
+    a.length = l.length;
+    a.token = l.token;
+    a.sampled_out = l.sampled_out;
+    a.num_sampled = l.num_sampled;
+    a.accepted = l.accepted;
+    a.stats = l.stats;
+    a.config = l.config;
+    a.logit_col = l.logit_col;
+    a.logit_seq = l.logit_seq;
+    a.draft_col = l.draft_col;
+    a.draft_seq = l.draft_seq;
+    a.stats_stride = l.stats_stride;
+    a.V = l.token_domain;
+    a.K = l.K;
+    a.ncols = plan.ncols;
+    a.ntiles = plan.ntiles;
+    a.tile_max = reinterpret_cast<float*>(ws + plan.tile_max_offset);
+    a.cmass = reinterpret_cast<uint64_t*>(ws + plan.cmass_offset);
+    a.ccount = reinterpret_cast<uint32_t*>(ws + plan.ccount_offset);
+    a.desc = reinterpret_cast<ColDesc*>(ws + plan.desc_offset);
+    a.fine = reinterpret_cast<uint32_t*>(ws + plan.fine_offset);
+    a.tile_res = reinterpret_cast<uint64_t*>(ws + plan.tile_res_offset);
+    a.tile_p = reinterpret_cast<uint64_t*>(ws + plan.tile_p_offset);
+    const dim3 tiles(plan.ntiles, plan.ncols, l.B);
+    const dim3 cols(plan.ncols, l.B);
+    hipLaunchKernelGGL(gen_max_kernel, tiles, dim3(kThreads), 0, stream, a);
+    check_launch("gen_max_kernel");
+    hipLaunchKernelGGL(gen_coarse_kernel, tiles, dim3(kThreads), 0, stream, a);
+    check_launch("gen_coarse_kernel");
+    hipLaunchKernelGGL(gen_cross_kernel, cols, dim3(kThreads), 0, stream, a);
+    check_launch("gen_cross_kernel");
+    hipLaunchKernelGGL(gen_fine_kernel, tiles, dim3(kThreads), 0, stream, a);
+    check_launch("gen_fine_kernel");
+    hipLaunchKernelGGL(gen_nucleus_kernel, cols, dim3(kThreads), 0, stream, a);
+    check_launch("gen_nucleus_kernel");
+    hipLaunchKernelGGL(gen_totals_kernel, dim3(plan.ntiles, l.B), dim3(kThreads), 0, stream, a);
+    check_launch("gen_totals_kernel");
+    hipLaunchKernelGGL(gen_pick_kernel, dim3(l.B), dim3(kThreads), 0, stream, a);
+    check_launch("gen_pick_kernel");
+}
+
+} // namespace nmi

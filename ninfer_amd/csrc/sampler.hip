@@ -142,24 +142,6 @@ __global__ void prepare_verify_inputs_kernel(const int32_t* token, const int32_t
     }
 }
 
-// ---- commit epilogue (src/ops/kernel/speculative_round.cuh:145-166) --------------------------------
-__device__ void commit_round(const int32_t* drafts, int K, int a, int tstar, int L, int32_t* length,
-                             int32_t* token, int32_t* sampled_out, int32_t* num_sampled,
-                             int32_t* accepted, int64_t* stats) {
-    for (int i = 0; i <= K; ++i) { sampled_out[i] = 0; }
-    for (int i = 0; i < a; ++i) { sampled_out[i] = drafts[i]; }
-    sampled_out[a] = tstar;
-    const int produced = a + 1;
-    *num_sampled = produced;
-    *accepted = a;
-    *token = tstar;
-    *length = L + produced;
-    stats[0] += K;
-    stats[1] += a;
-    stats[2] += 1;
-    for (int i = 0; i < a; ++i) { stats[kStatsPerPositionOffset + i] += 1; }
-}
-
 __device__ int pick_from_support(const int32_t* cand_idx, const float* prob, int n, int exclude, float u) {
     float mass = 0.0f; // src/ops/kernel/sampling_device.cuh:307-329
     for (int j = 0; j < n; ++j) {

@@ -109,3 +109,37 @@ def run_accept(logits, drafts, length, stats, token_domain, cfgs, target_tokens=
                token=d_tok.numpy(), length=d_len.numpy(), stats=d_stats.numpy().reshape(B, -1))
     out["token_counts"] = [tc.numpy() for tc in keep] if keep else None
     return out
+
+
+def run_general(target, draft, drafts, u_accept, u_residual, length, stats, token_domain, temperature, top_p):
+    """Mode F batch acceptance. target uint16 [B][K+1][rows]; draft uint16 [B][K][rows]."""
+    target = np.asarray(target, dtype=np.uint16)
+    draft = np.asarray(draft, dtype=np.uint16)
+    B, Kp1, rows = target.shape
+    K = Kp1 - 1
+    drafts = np.asarray(drafts, dtype=np.int32).reshape(B, K)
+    stats = np.asarray(stats, dtype=np.int64).reshape(B, -1)
+    d_t = DeviceArray.from_numpy(na.BF16, target, (rows, K + 1, B))
+    d_d = DeviceArray.from_numpy(na.BF16, draft, (rows, K, B))
+    d_dr = DeviceArray.from_numpy(na.I32, drafts, (K, B))
+    d_ua = DeviceArray.from_numpy(na.FP32, np.asarray(u_accept, dtype=np.float32).reshape(B, K + 1), (K + 1, B))
+    d_ur = DeviceArray.from_numpy(na.FP32, np.asarray(u_residual, dtype=np.float32).reshape(B), (1, B))
+    d_len = DeviceArray.from_numpy(na.I32, np.asarray(length, dtype=np.int32), (B,))
+    d_tok = DeviceArray.from_numpy(na.I32, np.full(B, -1, dtype=np.int32), (B,))
+    d_so = DeviceArray.from_numpy(na.I32, np.full((B, K + 1), -7, dtype=np.int32), (K + 1, B))
+    d_ns = DeviceArray.from_numpy(na.I32, np.zeros(B, dtype=np.int32), (B,))
+    d_acc = DeviceArray.from_numpy(na.I32, np.zeros(B, dtype=np.int32), (B,))
+    d_stats = DeviceArray.from_numpy(na.I64, stats, (stats.shape[1], B))
+    cfg = na.GeneralConfig()
+    cfg.temperature, cfg.top_p = temperature, top_p
+    cfg_buf = DeviceBuffer(8)
+    cfg_buf.upload(np.frombuffer(bytes(memoryview(cfg)), dtype=np.uint8))
+    ws = DeviceBuffer(ops.general_accept_workspace_bytes(token_domain, K, B))
+    ws.fill(0xFF)  # the op may not depend on what scratch held before
+    ops.speculative_accept_general(d_t.tensor(), d_d.tensor(), d_dr.tensor(), d_ua.tensor(), d_ur.tensor(),
+                                   d_len.tensor(), d_tok.tensor(), d_so.tensor(), d_ns.tensor(), d_acc.tensor(),
+                                   d_stats.tensor(), token_domain, cfg_buf.ptr, ws)
+    from ninfer_amd.device import synchronize
+    synchronize()
+    return dict(sampled_out=d_so.numpy().reshape(B, K + 1), num_sampled=d_ns.numpy(), accepted=d_acc.numpy(),
+                token=d_tok.numpy(), length=d_len.numpy(), stats=d_stats.numpy().reshape(B, -1))

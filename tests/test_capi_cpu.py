@@ -186,3 +186,42 @@ def test_dtype_values_match_reference_enum():
     for name, val in (("NMI_BF16", 0), ("NMI_FP32", 1), ("NMI_I32", 2), ("NMI_U8", 3), ("NMI_I64", 4),
                       ("NMI_I8", 5), ("NMI_FP16", 6)):
         assert re.search(rf"\b{name} = {val}\b", hdr), name
+
+
+def _general_args(K=3, B=1, V=248320, **over):
+    a = dict(logits=_t(na.BF16, (V, K + 1, B)), draft=_t(na.BF16, (V, K, B)), drafts=_t(na.I32, (K, B)),
+             ua=_t(na.FP32, (K + 1, B)), ur=_t(na.FP32, (1, B)), length=_t(na.I32, (B,)), token=_t(na.I32, (B,)),
+             so=_t(na.I32, (K + 1, B)), ns=_t(na.I32, (B,)), acc=_t(na.I32, (B,)), stats=_t(na.I64, (4 + K, B)))
+    a.update(over)
+    return a
+
+
+def _call_general(a, V=248320, ws=None, cfg=0x1000):
+    K = a["drafts"].ne[0]
+    ws = ws or _WS(ops.general_accept_workspace_bytes(V, max(K, 1), a["drafts"].ne[1]))
+    ops.speculative_accept_general(a["logits"], a["draft"], a["drafts"], a["ua"], a["ur"], a["length"], a["token"],
+                                   a["so"], a["ns"], a["acc"], a["stats"], V, cfg, ws)
+
+
+@pytest.mark.parametrize("override,needle", [
+    (dict(ua=_t(na.FP32, (3, 1))), "invalid vector shape for u_accept"),
+    (dict(ur=_t(na.I32, (1, 1))), "invalid dtype for u_residual"),
+    (dict(draft=_t(na.BF16, (248320, 2, 1))), "draft_logits must be"),
+    (dict(logits=_t(na.FP32, (248320, 4, 1))), "invalid dtype for logits"),
+    (dict(stats=_t(na.I64, (6, 1))), "invalid vector shape for stats"),
+])
+def test_general_accept_validation(override, needle):
+    with pytest.raises(ValueError, match=re.escape(needle)):
+        _call_general(_general_args(**override))
+
+
+def test_general_accept_limits():
+    with pytest.raises(ValueError, match="config must be non-null"):
+        _call_general(_general_args(), cfg=0)
+    with pytest.raises(ValueError, match="workspace"):
+        _call_general(_general_args(), ws=_WS(1024))
+    big = 1 << 21
+    with pytest.raises(ValueError, match="exceeds 1048576"):
+        _call_general(_general_args(V=big), V=big, ws=_WS(1 << 20))
+    assert ops.general_accept_workspace_bytes(248320, 3, 16) > 0
+    assert ops.general_accept_workspace_bytes(big, 3, 1) == 0
