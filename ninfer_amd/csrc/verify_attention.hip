@@ -52,8 +52,9 @@ constexpr int kStageKS = 8192;  // K scales: 64 keys x (group 0, group 1) FP16; 
 constexpr int kStageVS = 8448;  // V scales, same shape
 constexpr int kStageBytes = 8704;
 constexpr int kRingBytes = kWaves * 2 * kStageBytes; // two stages per wave: 69,632 B
-constexpr int kNewStage = kRingBytes;                 // A1: new rows quantized in-kernel
-constexpr int kSmemBytes = kRingBytes + kStageBytes;  // 78,336 B: two workgroups per CU
+constexpr int kNewStage = kRingBytes;                 // A1: new rows quantized in-kernel (Q tile before)
+constexpr int kPosLds = kNewStage + kStageBytes;      // positions[0 .. T), T <= 32
+constexpr int kSmemBytes = kPosLds + 128;             // 78,464 B: two workgroups per CU
 constexpr int kDmaPerChunk = 10;
 // Probabilities are FP16 exp2(score - m + 8); the reference maximum m moves only when a score
 // exceeds it by more than 2^7, so P <= 2^15 stays inside FP16 and most chunks skip the rescale.
@@ -413,37 +414,84 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const DmaLanes dl{(lane >> 3) * 128 + 16 * ((lane & 7) ^ (lane >> 3)), (lane >> 3) * 128 + 16 * (lane & 7), lane * 4};
     NMI_AS3 char* ring = (NMI_AS3 char*)smem + wave * 2 * kStageBytes;
 
-    // The first chunk does not depend on the positions: start its DMA right away.
-    const int first = k0 + kChunk * wave;
-    if (first + kChunk <= a.P) { issue_chunk(ring, hb, dl, first, lane); }
-
-    const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
-    const int32_t* par = a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr;
-    // Positions load while Q is converted: nothing in the Q operand depends on them.
-    const int pos_first = pos[0];
-    const int pos_last = pos[a.T - 1];
+    // Q tile (rows r = tl * G + gi of this workgroup, 256 B each) moves HBM -> LDS by DMA before
+    // any chunk DMA is queued, into the new-row stage area (free until an owner builds that stage).
+    // Wave 0 waits for it with an exact vmcnt that leaves the chunk DMAs in flight.
     const int t0 = rc * a.tokens_per_chunk;
     const int Tc = min(a.tokens_per_chunk, a.T - t0);
     const int R = Tc * a.G;
+    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + kNewStage;
+    NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + kPosLds);
+    const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
+    if (wave == 0) {
+        // Positions travel the same way (a vector load here would wait behind every chunk DMA).
+        if (lane < a.T) { __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)(pos + lane), (NMI_AS3 void*)pos_lds, 4, 0, 0); }
+#pragma unroll 1
+        for (int k = 0; 4 * k < R; ++k) {
+            const int row = 4 * k + (lane >> 4);
+            if (row < R) {
+                const int tl = row / a.G;
+                const int gi = row - tl * a.G;
+                // Slot (lane & 15) of the row holds piece (slot - row) & 15: rows rotate across the
+                // LDS banks, so the 16 lanes that read one column of rows do not conflict.
+                const int piece = ((lane & 15) - row) & 15;
+                const uint16_t* src = a.q + static_cast<int64_t>(D) * (h * a.G + gi + static_cast<int64_t>(a.Hq) * (t0 + tl + static_cast<int64_t>(a.T) * b)) + 8 * piece;
+                __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(qtile + k * 1024), 16, 0, 0);
+            }
+        }
+    }
 
-    // ---- Q operand: rows r = 16*nt + c; dims d = 64*gq + 16*g + 8*s + e.
+    // The first two chunks do not depend on the positions: start their DMA right away. A chunk
+    // that turns out to lie past the split's range is simply never read (it stays inside the
+    // padded cache, and the waits below fall back to vmcnt(0) when the next chunk is unused).
+    const int first = k0 + kChunk * wave;
+    if (first + kChunk <= a.P) { issue_chunk(ring, hb, dl, first, lane); }
+    if (first + kStride + kChunk <= a.P) { issue_chunk(ring + kStageBytes, hb, dl, first + kStride, lane); }
+    if (wave == 0) {
+        if (first + kStride + kChunk <= a.P) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kDmaPerChunk));
+        } else if (first + kChunk <= a.P) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kDmaPerChunk));
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        }
+    }
+    // A bare barrier: the DMA'd Q and positions are in LDS once wave 0's wait returns, and a full
+    // __syncthreads() would also wait for every chunk DMA.
+    __builtin_amdgcn_s_barrier();
+    i4 qraw[NT][G][2];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int r = 16 * nt + c;
+#pragma unroll
+        for (int gq = 0; gq < G; ++gq) {
+#pragma unroll
+            for (int hs = 0; hs < 2; ++hs) {
+                const int piece = 8 * gq + 2 * g + hs; // dims 8 * piece .. + 7
+                const i4 v = *(const NMI_AS3 i4*)(qtile + (r & 31) * 256 + 16 * ((piece + r) & 15));
+                qraw[nt][gq][hs] = r < R ? v : i4{0, 0, 0, 0};
+            }
+        }
+    }
+
+    const int32_t* par = a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr;
+    const int pos_first = __builtin_amdgcn_readfirstlane(pos_lds[0]);
+    const int pos_last = __builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]);
+
+    // ---- Q operand (B operand of S^T = K' Q^T) from the raw rows.
     RowState<NT> s;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int r = 16 * nt + c;
         const bool valid = r < R;
-        const int tl = valid ? r / a.G : 0;
-        const int gi = valid ? r - tl * a.G : 0;
-        const int t = t0 + tl;
-        const int qh = h * a.G + gi;
-        const uint16_t* qrow = a.q + static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b));
+        const int t = t0 + (valid ? r / a.G : 0);
         float x[G][2][8];
         float amax = 0.0f;
 #pragma unroll
         for (int gq = 0; gq < G; ++gq) {
 #pragma unroll
             for (int hs = 0; hs < 2; ++hs) {
-                const i4 raw = valid ? *reinterpret_cast<const i4*>(qrow + 64 * gq + 16 * g + 8 * hs) : i4{0, 0, 0, 0};
+                const i4 raw = qraw[nt][gq][hs];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     const int w = raw[e >> 1];
@@ -493,7 +541,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     float* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
 
-    if (first + kStride < hend) { issue_chunk(ring + kStageBytes, hb, dl, first + kStride, lane); }
 
     if (k0 >= hend && !owner) {
         __builtin_amdgcn_s_waitcnt(0);
@@ -508,10 +555,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // stage; wave 0 attends to them before its history chunks.
     if (owner) {
         NMI_AS3 char* ns = (NMI_AS3 char*)smem + kNewStage;
+        __syncthreads(); // every wave has read its Q rows from this area
         for (int i = threadIdx.x; i < kStageBytes / 16; i += blockDim.x) { *(NMI_AS3 i4*)(ns + 16 * i) = i4{0, 0, 0, 0}; }
         __syncthreads();
         for (int t = wave; t < a.T; t += kWaves) {
-            const int p = pos[t];
+            const int p = pos_lds[t];
             if (p < 0 || p >= a.P) { continue; }
             const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (t + static_cast<int64_t>(a.T) * b));
             append_row(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D, vbase + static_cast<int64_t>(p) * D,
@@ -565,7 +613,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             stage ^= 1;
             f4 sn[2][NT];
-            qk_chunk<NT>(rn, s, sn);
+            if (cn < hend) { qk_chunk<NT>(rn, s, sn); } // the last chunk has no successor
             pv_chunk<NT>(pop, vcur, vswcur, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
