@@ -48,6 +48,24 @@ def attn_bytes(L: int) -> int:
     return (L + T) * BYTES_PER_TOKEN + q + out + new_kv + new_codes
 
 
+def measured_traffic(workload: str) -> dict | None:
+    """HBM bytes per launch of the attention op from the committed counter passes: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) of its kernels, each scaled by the same counter's reading for a
+    copy of known size. None when the counter file is absent."""
+    path = Path(__file__).resolve().parent / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    cal = data["calibration"]
+    fetch_scale = cal["copy_bytes"] / 1024 / cal["fetch_kib"]
+    write_scale = cal["copy_bytes"] / 1024 / cal["write_kib"]
+    kernels = data["workloads"][workload]["kernels"]
+    fetch = sum(k["fetch_kib"] for k in kernels.values()) * fetch_scale * 1024
+    write = sum(k["write_kib"] for k in kernels.values()) * write_scale * 1024
+    return {"bytes": int(round(fetch + write)), "read_bytes": int(round(fetch)), "write_bytes": int(round(write)),
+            "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4)}
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -417,16 +435,22 @@ def main():
         line["sampler"] = {"workload": "stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95: Mode R (top-20 cap) "
                                        "and Mode F (full vocabulary, draft logits correlated 0.9)",
                            **{k: round(v, 2) for k, v in result["sampler"].items()}}
+    traffic = measured_traffic("c2")
     line["roofline"] = {
         "bound": "hbm",
         "achieved": round(c2["gbs"], 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(c2["gbs"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
-        "kernel": "verify attention op per layer (kv_quant_append + verify_attn_partial + verify_attn_merge)",
+        "traffic": traffic["bytes"] if traffic else None,
+        "kernel": "verify attention op per layer: verify_attn_partial (fused INT8 append of the new rows) + "
+                  "verify_attn_merge",
         "bytes_per_launch": attn_bytes(7680),
+        "traffic_detail": traffic,
     }
+    if "long_context" in line:
+        t3 = measured_traffic("c3")
+        line["long_context"]["traffic"] = t3["bytes"] if t3 else None
     if cpu is not None:
         line["cpu_baseline"] = {
             "value": round(attn_bytes(7680) / (cpu["us_per_layer"] * 1e-6) / 1e9, 3),
