@@ -129,8 +129,7 @@ int nmi_speculative_accept_greedy_drafts(const nmi_tensor* target_tokens, const 
                 "invalid vector shape for stats");
         require(config != nullptr, op, "config must be non-null");
         const SpecPlan plan = plan_spec(token_domain, K + 1, B);
-        require(static_cast<int64_t>(plan.ntiles) * kCandidateCap <= kMergeKeyCapacity, op,
-                "token_domain exceeds the candidate merge capacity (417792)");
+        require(plan.ntiles <= kMergeMaxTiles, op, "token_domain exceeds the candidate merge capacity (524288)");
         require_workspace(workspace, workspace_bytes, plan.bytes, op);
         char* ws = static_cast<char*>(workspace);
         SpecArgs a{};
@@ -145,10 +144,6 @@ int nmi_speculative_accept_greedy_drafts(const nmi_tensor* target_tokens, const 
         a.stats = static_cast<int64_t*>(stats->data);
         a.config = config;
         a.partial = reinterpret_cast<uint64_t*>(ws + plan.partial_offset);
-        a.dist_idx = reinterpret_cast<int32_t*>(ws + plan.dist_idx_offset);
-        a.dist_prob = reinterpret_cast<float*>(ws + plan.dist_prob_offset);
-        a.dist_support = reinterpret_cast<int32_t*>(ws + plan.dist_support_offset);
-        a.counters = reinterpret_cast<int32_t*>(ws + plan.counters_offset);
         a.logits_seq_stride = static_cast<int64_t>(logits->ne[0]) * logits->ne[1];
         a.physical_rows = logits->ne[0];
         a.token_domain = token_domain;

@@ -161,6 +161,104 @@ __device__ int pick_from_support(const int32_t* cand_idx, const float* prob, int
     return picked;
 }
 
+// ---- exact top-cap selection over unique 64-bit keys (0 = empty slot) -----------------------------
+//
+// A wave never extracts its keys one by one. A threshold T with at least cap keys >= T is found
+// first, with ballots only: MSB-first bit selection over the high words (ordered values) of a few
+// representative keys, the lane maxima or list heads. The keys >= T (a few dozen for real logits)
+// are compacted into LDS, and each one's rank is the number of candidates above it, so rank r goes
+// to out[r]. When more than 64 keys reach T (heavy ties), the exact cap-th largest key is found by a
+// 64-bit bit selection over every key and the ranking repeats with exactly cap candidates.
+
+__device__ __forceinline__ uint32_t key_high(uint64_t k) { return static_cast<uint32_t>(k >> 32); }
+
+// Lanes below this one that are set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+// Orders one wave's LDS writes before its later reads of the same slots by other lanes.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The cap-th largest high word among the wave's M values per lane (0 = no value): the largest t
+// with at least cap values whose high word is >= t. 0 when fewer than cap values exist.
+template <int M>
+__device__ __forceinline__ uint32_t wave_cap_high(const uint32_t (&hi)[M], int cap) {
+    uint32_t t = 0;
+#pragma unroll 1
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = t | (1u << bit);
+        int n = 0;
+#pragma unroll
+        for (int m = 0; m < M; ++m) { n += __popcll(__ballot(hi[m] >= c)); }
+        if (n >= cap) { t = c; }
+    }
+    return t;
+}
+
+// The exact cap-th largest key among the wave's N keys per lane (0 when fewer than cap exist).
+template <int N>
+__device__ __forceinline__ uint64_t wave_cap_key(const uint64_t (&k)[N], int cap) {
+    uint64_t t = 0;
+#pragma unroll 1
+    for (int bit = 63; bit >= 0; --bit) {
+        const uint64_t c = t | (1ull << bit);
+        int n = 0;
+#pragma unroll
+        for (int e = 0; e < N; ++e) { n += __popcll(__ballot(k[e] >= c)); }
+        if (n >= cap) { t = c; }
+    }
+    return t;
+}
+
+// Ranks the candidates {k[e] != 0, k[e] >= T} if there are at most 64 of them: the cap largest
+// go to out[0..cap) in descending order, 0-padded. cand: 64 slots of wave-private LDS.
+template <int N>
+__device__ __forceinline__ bool wave_rank_top(const uint64_t (&k)[N], uint64_t T, int cap, uint64_t* cand,
+                                              uint64_t* out) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+#pragma unroll
+    for (int e = 0; e < N; ++e) { total += __popcll(__ballot(k[e] != 0 && k[e] >= T)); }
+    if (total > 64) { return false; }
+    int base = 0;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+        const bool sel = k[e] != 0 && k[e] >= T;
+        const uint64_t mask = __ballot(sel);
+        if (sel) { cand[base + lanes_below(mask)] = k[e]; }
+        base += __popcll(mask);
+    }
+    wave_lds_sync();
+    if (lane < total) {
+        const uint64_t key = cand[lane];
+        int r = 0;
+        for (int j = 0; j < total; ++j) { r += cand[j] > key ? 1 : 0; }
+        if (r < cap) { out[r] = key; }
+    } else if (lane < cap) {
+        out[lane] = 0;
+    }
+    wave_lds_sync();
+    return true;
+}
+
+// Top cap of the wave's N keys per lane; `heads` are one or more keys per lane that include every
+// lane's (or list's) largest key, so at least cap keys reach the threshold derived from them.
+template <int N, int M>
+__device__ __forceinline__ void wave_top_cap(const uint64_t (&k)[N], const uint64_t (&heads)[M], int cap,
+                                             uint64_t* cand, uint64_t* out) {
+    uint32_t hi[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) { hi[m] = key_high(heads[m]); }
+    const uint64_t T = static_cast<uint64_t>(wave_cap_high(hi, cap)) << 32;
+    if (!wave_rank_top(k, T, cap, cand, out)) { wave_rank_top(k, wave_cap_key(k, cap), cap, cand, out); }
+}
+
 // ---- Mode R launch 1: per-tile top-cap candidates ------------------------------------------------
 
 __global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
@@ -168,7 +266,6 @@ __global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
     const int col = blockIdx.y;
     const int b = blockIdx.z;
     const nmi_sampling_config cfg = a.config[b];
-    if (tile == 0 && col == 0 && threadIdx.x == 0) { a.counters[b] = 0; }
     if (!(cfg.temperature > 0.0f)) { return; }
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -195,26 +292,41 @@ __global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
             keys[e] = v < a.token_domain ? sort_key(adjusted_logit(bf16_to_f32(x[v]), v, cfg, drafts, col), v) : 0ull;
         }
     }
+    __shared__ uint64_t cand[4][64];
     __shared__ uint64_t wtop[4][kCandidateCap];
-    wave_topk(keys, cap, wtop[wave]);
+    __shared__ uint64_t btop[kCandidateCap];
+    uint64_t head[1] = {keys[0]};
+#pragma unroll
+    for (int e = 1; e < 16; ++e) { head[0] = keys[e] > head[0] ? keys[e] : head[0]; }
+    wave_top_cap(keys, head, cap, cand[wave], wtop[wave]);
+    if (threadIdx.x < cap) { btop[threadIdx.x] = 0; }
     __syncthreads();
-    if (wave == 0) {
-        uint64_t k2[2];
-        k2[0] = lane < 4 * cap && (lane / cap) < 4 ? wtop[lane / cap][lane % cap] : 0ull;
-        const int l2 = lane + 64;
-        k2[1] = l2 < 4 * cap ? wtop[l2 / cap][l2 % cap] : 0ull;
+    // Block merge: key i of wave w's descending list ranks i + (keys of the other lists above it).
+    if (lane < cap) {
+        const uint64_t key = wtop[wave][lane];
+        if (key != 0) {
+            int r = lane;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                if (w == wave) { continue; }
+                for (int j = 0; j < cap; ++j) { r += wtop[w][j] > key ? 1 : 0; }
+            }
+            if (r < cap) { btop[r] = key; }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < cap) {
         uint64_t* dst = a.partial + ((static_cast<int64_t>(b) * a.columns + col) * a.ntiles + tile) * kCandidateCap;
-        __shared__ uint64_t btop[kCandidateCap];
-        wave_topk(k2, cap, btop);
-        if (lane < cap) { dst[lane] = btop[lane]; }
+        dst[threadIdx.x] = btop[threadIdx.x];
     }
 }
 
-// ---- Mode R launch 2: per-column merge + normalize, last column accepts ---------------------------
+// ---- Mode R launch 2: per-sequence merge, distributions and the sequential accept -----------------
 
+// One workgroup per sequence; wave w merges columns w, w + 4, ... (lane j holds tile lists j and
+// j + 64), builds each column's truncated distribution in LDS, then thread 0 runs the accept.
 __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
-    const int col = blockIdx.x;
-    const int b = blockIdx.y;
+    const int b = blockIdx.x;
     const nmi_sampling_config cfg = a.config[b];
     const int K = a.K;
     const int32_t* drafts = a.drafts + static_cast<int64_t>(b) * K;
@@ -227,7 +339,7 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
 
     if (!(cfg.temperature > 0.0f)) {
         // Greedy: src/ops/kernel/speculative_round.cuh:51-72.
-        if (col == 0 && threadIdx.x == 0) {
+        if (threadIdx.x == 0) {
             const int32_t* target = a.target_tokens + static_cast<int64_t>(b) * (K + 1);
             int acc = 0;
             while (acc < K && target[acc] == drafts[acc]) { ++acc; }
@@ -240,109 +352,106 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int cap = candidate_cap(cfg, a.token_domain);
-    const uint64_t* part = a.partial + (static_cast<int64_t>(b) * a.columns + col) * a.ntiles * kCandidateCap;
-    const int nkeys = a.ntiles * cap;
-    uint64_t keys[8];
+    __shared__ uint64_t cand[4][64];
+    __shared__ uint64_t top[4][kCandidateCap];
+    __shared__ float e_sh[4][kCandidateCap];
+    __shared__ int32_t d_idx[kMaxColumns][kCandidateCap];
+    __shared__ float d_prob[kMaxColumns][kCandidateCap];
+    __shared__ int32_t d_n[kMaxColumns];
+    const float inv_temp = 1.0f / cfg.temperature;
+    for (int col = wave; col <= K; col += 4) {
+        const uint64_t* part = a.partial + (static_cast<int64_t>(b) * a.columns + col) * a.ntiles * kCandidateCap;
+        uint64_t lk[2 * kCandidateCap];
+        uint64_t heads[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int p = wave * 512 + i * 64 + lane; // wave w owns keys [512w, 512w + 512)
-        if (p < nkeys) {
-            const int t = p / cap;
-            keys[i] = part[t * kCandidateCap + (p - t * cap)];
-        } else {
-            keys[i] = 0ull;
+        for (int h = 0; h < 2; ++h) {
+            const int j = lane + 64 * h;
+            if (j < a.ntiles) {
+                const i4* src = reinterpret_cast<const i4*>(part + static_cast<int64_t>(j) * kCandidateCap);
+#pragma unroll
+                for (int q = 0; q < kCandidateCap / 2; ++q) {
+                    const i4 v = src[q];
+                    lk[h * kCandidateCap + 2 * q] = (static_cast<uint64_t>(static_cast<uint32_t>(v[1])) << 32) | static_cast<uint32_t>(v[0]);
+                    lk[h * kCandidateCap + 2 * q + 1] = (static_cast<uint64_t>(static_cast<uint32_t>(v[3])) << 32) | static_cast<uint32_t>(v[2]);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < kCandidateCap; ++q) { lk[h * kCandidateCap + q] = 0; }
+            }
+#pragma unroll
+            for (int q = 0; q < kCandidateCap; ++q) {
+                if (q >= cap) { lk[h * kCandidateCap + q] = 0; } // slots past cap were never written
+            }
+            heads[h] = lk[h * kCandidateCap];
         }
-    }
-    __shared__ uint64_t wtop[4][kCandidateCap];
-    wave_topk(keys, cap, wtop[wave]);
-    __syncthreads();
-    __shared__ float e_sh[kCandidateCap];
-    __shared__ float x_sh[kCandidateCap];
-    __shared__ int32_t idx_sh[kCandidateCap];
-    if (wave == 0) {
-        uint64_t k2[2];
-        k2[0] = lane < 4 * cap ? wtop[lane / cap][lane % cap] : 0ull;
-        const int l2 = lane + 64;
-        k2[1] = l2 < 4 * cap ? wtop[l2 / cap][l2 % cap] : 0ull;
-        __shared__ uint64_t top[kCandidateCap];
-        wave_topk(k2, cap, top);
+        wave_top_cap(lk, heads, cap, cand[wave], top[wave]);
         // src/ops/kernel/sampling_device.cuh:190-223 with det_expf(fma(x, inv_temp, -m)).
-        const float inv_temp = 1.0f / cfg.temperature;
-        const float x0 = key_float(top[0]);
-        const float m = x0 * inv_temp;
+        const float m = key_float(top[wave][0]) * inv_temp;
         if (lane < cap) {
-            const float xj = key_float(top[lane]);
-            x_sh[lane] = xj;
-            idx_sh[lane] = key_index(top[lane]);
-            e_sh[lane] = det_expf(__builtin_fmaf(xj, inv_temp, -m));
+            const uint64_t key = top[wave][lane];
+            d_idx[col][lane] = key_index(key);
+            e_sh[wave][lane] = det_expf(__builtin_fmaf(key_float(key), inv_temp, -m));
         }
+        wave_lds_sync();
         if (lane == 0) {
+            const float* e = e_sh[wave];
             float sum = 0.0f;
-            for (int j = 0; j < cap; ++j) { sum = sum + e_sh[j]; }
-            const float e0 = e_sh[0];
+            for (int j = 0; j < cap; ++j) { sum = sum + e[j]; }
+            const float e0 = e[0];
             const float min_p_thresh = (cfg.min_p > 0.0f) ? cfg.min_p * e0 : -1.0f;
             const bool top_p_active = cfg.top_p < 1.0f;
             const float top_p_target = cfg.top_p * sum;
             float cum = 0.0f;
             int support = 0;
             for (int j = 0; j < cap; ++j) {
-                if (min_p_thresh >= 0.0f && e_sh[j] < min_p_thresh) { break; }
-                cum = cum + e_sh[j];
+                if (min_p_thresh >= 0.0f && e[j] < min_p_thresh) { break; }
+                cum = cum + e[j];
                 support = j + 1;
                 if (top_p_active && cum >= top_p_target) { break; }
             }
             if (support < 1) { support = 1; }
             float ssum = 0.0f;
-            for (int j = 0; j < support; ++j) { ssum = ssum + e_sh[j]; }
+            for (int j = 0; j < support; ++j) { ssum = ssum + e[j]; }
             const float inv = 1.0f / ssum;
-            const int64_t d = (static_cast<int64_t>(b) * a.columns + col) * kCandidateCap;
-            for (int j = 0; j < support; ++j) {
-                a.dist_idx[d + j] = idx_sh[j];
-                a.dist_prob[d + j] = e_sh[j] * inv;
-            }
-            a.dist_support[static_cast<int64_t>(b) * a.columns + col] = support;
-            __threadfence();
-            const int done = atomicAdd(&a.counters[b], 1) + 1;
-            if (done == K + 1) {
-                __threadfence();
-                // Sequential accept: src/ops/kernel/speculative_round.cuh:337-366.
-                const int L = *length;
-                int acc = 0;
-                int tstar = 0;
-                for (int i = 0; i <= K; ++i) {
-                    const int64_t di = (static_cast<int64_t>(b) * a.columns + i) * kCandidateCap;
-                    const int n = __atomic_load_n(&a.dist_support[static_cast<int64_t>(b) * a.columns + i], __ATOMIC_RELAXED);
-                    const int32_t* cidx = a.dist_idx + di;
-                    const float* cprob = a.dist_prob + di;
-                    if (i < K) {
-                        const int dtok = drafts[i];
-                        float pd = 0.0f;
-                        for (int j = 0; j < n; ++j) {
-                            if (cidx[j] == dtok) {
-                                pd = cprob[j];
-                                break;
-                            }
-                        }
-                        const float u = sampling_uniform(cfg.seed, L + i + 1, kPurposeAccept, 0u);
-                        if (u < pd) {
-                            acc = i + 1;
-                            continue;
-                        }
-                        const float ur = sampling_uniform(cfg.seed, L + i + 1, kPurposeCorrection, 0u);
-                        tstar = pick_from_support(cidx, cprob, n, dtok, ur);
-                        break;
-                    }
-                    const float u = sampling_uniform(cfg.seed, L + K + 1, kPurposeBonus, 0u);
-                    tstar = pick_from_support(cidx, cprob, n, -1, u);
-                }
-                commit_round(drafts, K, acc, tstar, L, length, token, sampled_out, num_sampled,
-                             accepted, stats);
-                if (cfg.token_counts != nullptr) {
-                    for (int i = 0; i <= acc; ++i) { atomicAdd(&cfg.token_counts[sampled_out[i]], 1); }
-                }
-                a.counters[b] = 0;
-            }
+            for (int j = 0; j < support; ++j) { d_prob[col][j] = e[j] * inv; }
+            d_n[col] = support;
         }
+        wave_lds_sync();
+    }
+    __syncthreads();
+    if (threadIdx.x != 0) { return; }
+    // Sequential accept: src/ops/kernel/speculative_round.cuh:337-366.
+    const int L = *length;
+    int acc = 0;
+    int tstar = 0;
+    for (int i = 0; i <= K; ++i) {
+        const int n = d_n[i];
+        const int32_t* cidx = d_idx[i];
+        const float* cprob = d_prob[i];
+        if (i < K) {
+            const int dtok = drafts[i];
+            float pd = 0.0f;
+            for (int j = 0; j < n; ++j) {
+                if (cidx[j] == dtok) {
+                    pd = cprob[j];
+                    break;
+                }
+            }
+            const float u = sampling_uniform(cfg.seed, L + i + 1, kPurposeAccept, 0u);
+            if (u < pd) {
+                acc = i + 1;
+                continue;
+            }
+            const float ur = sampling_uniform(cfg.seed, L + i + 1, kPurposeCorrection, 0u);
+            tstar = pick_from_support(cidx, cprob, n, dtok, ur);
+            break;
+        }
+        const float u = sampling_uniform(cfg.seed, L + K + 1, kPurposeBonus, 0u);
+        tstar = pick_from_support(cidx, cprob, n, -1, u);
+    }
+    commit_round(drafts, K, acc, tstar, L, length, token, sampled_out, num_sampled, accepted, stats);
+    if (cfg.token_counts != nullptr) {
+        for (int i = 0; i <= acc; ++i) { atomicAdd(&cfg.token_counts[sampled_out[i]], 1); }
     }
 }
 
@@ -418,10 +527,6 @@ SpecPlan plan_spec(int32_t token_domain, int32_t columns, int32_t batch) {
     };
     const size_t cols = static_cast<size_t>(columns) * batch;
     p.partial_offset = take(cols * p.ntiles * kCandidateCap * sizeof(uint64_t));
-    p.dist_idx_offset = take(cols * kCandidateCap * sizeof(int32_t));
-    p.dist_prob_offset = take(cols * kCandidateCap * sizeof(float));
-    p.dist_support_offset = take(cols * sizeof(int32_t));
-    p.counters_offset = take(static_cast<size_t>(batch) * sizeof(int32_t));
     p.bytes = off;
     return p;
 }
@@ -445,7 +550,7 @@ void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream)
     hipLaunchKernelGGL(spec_tile_topk_kernel, dim3(args.ntiles, args.K + 1, batch), dim3(256), 0,
                        stream, args);
     check_launch("spec_tile_topk_kernel");
-    hipLaunchKernelGGL(spec_merge_accept_kernel, dim3(args.K + 1, batch), dim3(256), 0, stream, args);
+    hipLaunchKernelGGL(spec_merge_accept_kernel, dim3(batch), dim3(256), 0, stream, args);
     check_launch("spec_merge_accept_kernel");
 }
 

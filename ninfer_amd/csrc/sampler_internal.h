@@ -13,15 +13,11 @@ inline constexpr int kPurposeBonus = 4;
 inline constexpr int kMaxColumns = 16;            // K <= 15 (reference kSamplerMaxColumns)
 inline constexpr int kTileTokens = 4096;   // tokens per candidate tile (256 threads x 16)
 inline constexpr int kMaxTreeNodes = 32;
-inline constexpr int kMergeKeyCapacity = 2048; // keys one merge block holds (4 waves x 512)
+inline constexpr int kMergeMaxTiles = 128;   // tile lists one merge wave holds (2 per lane)
 
 struct SpecPlan {
     int32_t ntiles = 0;
     size_t partial_offset = 0;
-    size_t dist_idx_offset = 0;
-    size_t dist_prob_offset = 0;
-    size_t dist_support_offset = 0;
-    size_t counters_offset = 0;
     size_t bytes = 0;
 };
 
@@ -36,11 +32,7 @@ struct SpecArgs {
     int32_t* accepted;
     int64_t* stats;               // [stats_stride, B]
     const nmi_sampling_config* config; // [B] device
-    uint64_t* partial;
-    int32_t* dist_idx;
-    float* dist_prob;
-    int32_t* dist_support;
-    int32_t* counters;
+    uint64_t* partial;            // [B][columns][ntiles][kCandidateCap] per-tile candidates
     int64_t logits_seq_stride;    // elements between sequences
     int32_t physical_rows;
     int32_t token_domain;

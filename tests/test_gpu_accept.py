@@ -188,6 +188,39 @@ def test_stochastic_batch_matches_oracle(gpu, oracle, seed, top_k, top_p, min_p)
         assert list(res["stats"][b]) == list(exp["stats"])
 
 
+@pytest.mark.parametrize("pattern", ["all_equal", "tie_at_max", "coarse_levels"])
+def test_stochastic_ties_match_oracle(gpu, oracle, pattern):
+    """Heavy ties: more than 64 keys share the top high word in a wave or a column, so the exact
+    64-bit selection path of the candidate merge runs (ties order by token id)."""
+    B, K, rows, domain = 4, 3, 248320, 248320
+    rng = np.random.default_rng(77)
+    if pattern == "all_equal":
+        x = np.full((B, K + 1, rows), 1.5, np.float32)
+    elif pattern == "tie_at_max":
+        x = rng.standard_normal((B, K + 1, rows), dtype=np.float32) * 3.0
+        for b in range(B):
+            for c in range(K + 1):
+                x[b, c, rng.choice(rows, 300, replace=False)] = 14.0
+    else:
+        x = np.round(rng.standard_normal((B, K + 1, rows), dtype=np.float32) * 1.5)
+    logits = BF(x)
+    drafts = np.zeros((B, K), np.int32)
+    for b in range(B):
+        for i in range(K):
+            order = np.lexsort((np.arange(rows), -x[b, i]))
+            drafts[b, i] = order[int(rng.integers(0, 30))]
+    lengths = np.full(B, 4096, np.int32)
+    cfgs = [_cfg(temperature=0.7, top_p=0.95, seed=1000 + b) for b in range(B)]
+    stats = np.zeros((B, 4 + K), dtype=np.int64)
+    res = gpu_runner.run_accept(logits, drafts, lengths, stats, domain, cfgs)
+    for b in range(B):
+        exp = oracle.speculative_accept(None, logits[b].reshape(-1), rows, drafts[b], int(lengths[b]), stats[b],
+                                        domain, _ocfg(cfgs[b]))
+        assert list(res["sampled_out"][b]) == list(exp["sampled_out"]), f"b={b}"
+        assert res["accepted"][b] == exp["accepted"]
+        assert list(res["stats"][b]) == list(exp["stats"])
+
+
 def test_penalties_and_token_counts_match_oracle(gpu, oracle):
     B, K, rows, domain = 4, 4, 50000, 49999
     logits, drafts, lengths, cfgs = _stochastic_batch(B, K, rows, domain, 9, temperature=1.0, top_p=0.9,
