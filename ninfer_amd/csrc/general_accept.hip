@@ -109,22 +109,55 @@ __device__ __forceinline__ float value_of_ordered16(uint32_t o) {
     return bf16_to_f32(static_cast<uint16_t>(bits));
 }
 
-// Block-wide inclusive scan over 256 threads (Hillis-Steele in LDS).
+template <typename T>
+__device__ __forceinline__ T shfl_up_any(T v, int off) {
+    constexpr int kWords = sizeof(T) / 4;
+    uint32_t w[kWords];
+    __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) { w[i] = static_cast<uint32_t>(__shfl_up(static_cast<int>(w[i]), off, 64)); }
+    T r;
+    __builtin_memcpy(&r, w, sizeof(T));
+    return r;
+}
+
+// Block-wide inclusive scan over 256 threads: a shuffle scan per wave, then the wave totals
+// through LDS (sh: at least kThreads / 64 entries). Integer sums, so any order gives the same bits.
 template <typename T>
 __device__ T block_scan(T v, T* sh) {
-    const int tid = threadIdx.x;
-    sh[tid] = v;
-    __syncthreads();
-#pragma unroll 1
-    for (int off = 1; off < kThreads; off <<= 1) {
-        const T add = tid >= off ? sh[tid - off] : T(0);
-        __syncthreads();
-        sh[tid] += add;
-        __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const T o = shfl_up_any(v, off);
+        if (lane >= off) { v += o; }
     }
-    const T r = sh[tid];
+    if (lane == 63) { sh[wave] = v; }
     __syncthreads();
-    return r;
+    T add = 0;
+    for (int w = 0; w < wave; ++w) { add += sh[w]; }
+    __syncthreads();
+    return v + add;
+}
+
+// The 16 tokens [v0, v0 + 16) of a column as floats (tokens >= V read as -inf), loaded with two
+// 16-byte loads when the run is whole and aligned.
+__device__ __forceinline__ void load16(const uint16_t* col, int v0, int V, float (&x)[16]) {
+    if (v0 + 16 <= V && (reinterpret_cast<uintptr_t>(col + v0) & 15u) == 0) {
+        const i4 r0 = *reinterpret_cast<const i4*>(col + v0);
+        const i4 r1 = *reinterpret_cast<const i4*>(col + v0 + 8);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t w = static_cast<uint32_t>(e < 8 ? r0[e >> 1] : r1[(e - 8) >> 1]);
+            x[e] = bf16_to_f32(static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu)));
+        }
+    } else {
+        uint16_t raw[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { raw[e] = v0 + e < V ? col[v0 + e] : static_cast<uint16_t>(0xff80u); }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { x[e] = bf16_to_f32(raw[e]); }
+    }
 }
 
 // Smallest thread index with `pred`, or kThreads.
@@ -160,12 +193,11 @@ __global__ __launch_bounds__(kThreads) void gen_max_kernel(GenArgs a) {
     __shared__ float red[kThreads / 64];
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const uint16_t* col = column_ptr(a, b, c);
-    const int v0 = t * kGenTile;
+    float x[16];
+    load16(col, t * kGenTile + kPerThread * static_cast<int>(threadIdx.x), a.V, x);
     float mx = -INFINITY;
-    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
-        const int v = v0 + i;
-        if (v < a.V) { mx = fmaxf(mx, bf16_to_f32(col[v])); }
-    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { mx = fmaxf(mx, x[e]); }
     mx = block_max(mx, red);
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
     if (threadIdx.x == 0) { a.tile_max[cb * a.ntiles + t] = mx; }
@@ -192,17 +224,18 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
     cnt[threadIdx.x] = 0;
     mass[threadIdx.x] = 0;
+    // The tile's tokens load while the column maximum is reduced.
+    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float x[16];
+    load16(column_ptr(a, b, c), v0, a.V, x);
     float m, inv_temp;
     column_scale(a, cb, red, &m, &inv_temp); // synchronizes the block
-    const uint16_t* col = column_ptr(a, b, c);
-    const int v0 = t * kGenTile;
-    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
-        const int v = v0 + i;
-        if (v >= a.V) { break; }
-        const float x = bf16_to_f32(col[v]);
-        const uint32_t bin = ordered16(x) >> 8;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        if (v0 + e >= a.V) { break; }
+        const uint32_t bin = ordered16(x[e]) >> 8;
         atomicAdd(&cnt[bin], 1u);
-        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x, inv_temp, m)));
+        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
     }
     __syncthreads();
     if (cnt[threadIdx.x] != 0) {
@@ -260,16 +293,17 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
     __shared__ uint32_t cnt[kGenBins];
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float x[16];
+    load16(column_ptr(a, b, c), v0, a.V, x); // issued before the descriptor arrives
     const ColDesc d = a.desc[cb];
     if (!d.nucleus) { return; }
     cnt[threadIdx.x] = 0;
     __syncthreads();
-    const uint16_t* col = column_ptr(a, b, c);
-    const int v0 = t * kGenTile;
-    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
-        const int v = v0 + i;
-        if (v >= a.V) { break; }
-        const uint32_t o = ordered16(bf16_to_f32(col[v]));
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        if (v0 + e >= a.V) { break; }
+        const uint32_t o = ordered16(x[e]);
         if (static_cast<int>(o >> 8) == d.c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
     }
     __syncthreads();
@@ -290,6 +324,7 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     // Fine bin f = 255 - tid (descending value order).
     const uint32_t f = kGenBins - 1 - threadIdx.x;
     uint64_t count = 0;
+#pragma unroll 8
     for (int t = 0; t < a.ntiles; ++t) { count += a.fine[(cb * a.ntiles + t) * kGenBins + f]; }
     const uint32_t o16 = (static_cast<uint32_t>(d.c1) << 8) | f;
     const float x = value_of_ordered16(o16);
@@ -321,17 +356,19 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     // Rescan that tile: thread i owns tokens [16 i, 16 i + 16) of it.
     const uint16_t* col = column_ptr(a, b, c);
     const int v0 = ts * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float xs[16];
+    load16(col, v0, a.V, xs);
     uint64_t mine = 0;
+#pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
-        const int v = v0 + k;
-        if (v < a.V && ordered16(bf16_to_f32(col[v])) == vstar) { ++mine; }
+        if (v0 + k < a.V && ordered16(xs[k]) == vstar) { ++mine; }
     }
     const uint64_t mincl = block_scan<uint64_t>(mine, sh);
     if (mine != 0 && mincl >= rank && mincl - mine < rank) {
         uint64_t need = rank - (mincl - mine);
         for (int k = 0; k < kPerThread; ++k) {
             const int v = v0 + k;
-            if (v < a.V && ordered16(bf16_to_f32(col[v])) == vstar && --need == 0) {
+            if (v < a.V && ordered16(xs[k]) == vstar && --need == 0) {
                 d.kstar = sort_key(value_of_ordered16(vstar), v);
                 d.zs = bcast[1];
                 a.desc[cb] = d;
@@ -341,10 +378,13 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     }
 }
 
-// Accept decisions of sequence b (identical in every block that evaluates them). Returns a; sets
-// *rejected to the rejected column (or -1 when all K drafts are accepted).
-__device__ int decide(const GenArgs& a, int b, int* rejected) {
-    for (int i = 0; i < a.K; ++i) {
+// Accept decisions of sequence b (identical in every block that evaluates them): thread i < K
+// tests draft i, and the first failing draft is the rejection. Returns a; sets *rejected to the
+// rejected column (or -1 when all K drafts are accepted).
+__device__ int decide(const GenArgs& a, int b, int* rejected, int* sh) {
+    bool fail = false;
+    const int i = static_cast<int>(threadIdx.x);
+    if (i < a.K) {
         const int d = a.drafts[b * a.K + i];
         const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + i];
         const ColDesc q = a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + i];
@@ -356,13 +396,11 @@ __device__ int decide(const GenArgs& a, int b, int* rejected) {
         const uint64_t wq = in_domain ? member_weight(q, xq, d) : 0ull;
         const u128 lhs = static_cast<u128>(fixed_u24(a.u_accept[b * (a.K + 1) + i])) * wq * p.zs;
         const u128 rhs = (static_cast<u128>(wp) * q.zs) << 24;
-        if (!(lhs < rhs)) {
-            *rejected = i;
-            return i;
-        }
+        fail = !(lhs < rhs);
     }
-    *rejected = -1;
-    return a.K;
+    const int f = block_first(fail, sh);
+    *rejected = f < a.K ? f : -1;
+    return f < a.K ? f : a.K;
 }
 
 // Draw weights of token v: residual (column pair i) or p (column i); both from one read.
@@ -371,14 +409,12 @@ struct DrawMass {
     uint64_t p;
 };
 
-__device__ __forceinline__ DrawMass draw_mass(const GenArgs& a, int b, int col_p, int rejected, const ColDesc& p,
-                                              const ColDesc& q, int v) {
+__device__ __forceinline__ DrawMass draw_mass_x(int rejected, const ColDesc& p, const ColDesc& q, float xp,
+                                                float xq, int v) {
     DrawMass r;
-    const float xp = bf16_to_f32(column_ptr(a, b, col_p)[v]);
     r.p = member_weight(p, xp, v);
     r.res = 0;
     if (rejected >= 0) {
-        const float xq = bf16_to_f32(column_ptr(a, b, a.K + 1 + rejected)[v]);
         const uint64_t wq = member_weight(q, xq, v);
         const u128 pv = static_cast<u128>(r.p) * q.zs;
         const u128 qv = static_cast<u128>(wq) * p.zs;
@@ -389,22 +425,26 @@ __device__ __forceinline__ DrawMass draw_mass(const GenArgs& a, int b, int col_p
 
 // ---- 6: per-tile masses of the draw --------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
-    __shared__ u128 shr[kThreads];
-    __shared__ uint64_t shp[kThreads];
+    __shared__ u128 shr[kThreads / 64];
+    __shared__ uint64_t shp[kThreads / 64];
+    __shared__ int first;
     const int t = blockIdx.x, b = blockIdx.y;
     int rejected;
-    const int acc = decide(a, b, &rejected);
+    const int acc = decide(a, b, &rejected, &first);
     const int col_p = rejected >= 0 ? rejected : a.K;
     const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
     const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
     (void)acc;
     u128 res = 0;
     uint64_t pm = 0;
-    const int v0 = t * kGenTile;
-    for (int i = threadIdx.x; i < kGenTile; i += kThreads) {
-        const int v = v0 + i;
-        if (v >= a.V) { break; }
-        const DrawMass dm = draw_mass(a, b, col_p, rejected, p, q, v);
+    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float xp[16], xq[16] = {};
+    load16(column_ptr(a, b, col_p), v0, a.V, xp);
+    if (rejected >= 0) { load16(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k) {
+        if (v0 + k >= a.V) { break; }
+        const DrawMass dm = draw_mass_x(rejected, p, q, xp[k], xq[k], v0 + k);
         res += dm.res;
         pm += dm.p;
     }
@@ -420,13 +460,13 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
 // ---- 7: locate the draw (first id whose running mass exceeds floor(total * u24 / 2^24), else the
 // last id with mass) and commit the round --------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
-    __shared__ u128 sh[kThreads];
+    __shared__ u128 sh[kThreads / 64];
     __shared__ int first;
     __shared__ int last_tile;
     __shared__ int result;
     const int b = blockIdx.x;
     int rejected;
-    const int acc = decide(a, b, &rejected);
+    const int acc = decide(a, b, &rejected, &first);
     const int col_p = rejected >= 0 ? rejected : a.K;
     const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
     const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
@@ -467,13 +507,17 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     __syncthreads();
     // Rescan the tile: thread i owns tokens [16 i, 16 i + 16).
     const int v0 = ts * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float xp[16], xq[16] = {};
+    load16(column_ptr(a, b, col_p), v0, a.V, xp);
+    if (rejected >= 0) { load16(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
     uint64_t w[kPerThread];
     u128 mine = 0;
+#pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
         const int v = v0 + k;
         w[k] = 0;
         if (v < a.V) {
-            const DrawMass dm = draw_mass(a, b, col_p, rejected, p, q, v);
+            const DrawMass dm = draw_mass_x(rejected, p, q, xp[k], xq[k], v);
             w[k] = use_res ? dm.res : dm.p;
         }
         mine += w[k];

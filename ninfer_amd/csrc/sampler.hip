@@ -100,14 +100,27 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* logits, in
     const int vec = valid_rows / 8;
     const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
     if (aligned) {
-        for (int i = threadIdx.x; i < vec; i += blockDim.x) {
-            const i4 raw = *reinterpret_cast<const i4*>(x + 8 * i);
+        // kArgmaxUnroll independent 16-byte loads per thread are in flight before any is used.
+        constexpr int kArgmaxUnroll = 8;
+        const int step = static_cast<int>(blockDim.x);
+        for (int i0 = threadIdx.x; i0 < vec; i0 += kArgmaxUnroll * step) {
+            i4 raw[kArgmaxUnroll];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t w = static_cast<uint32_t>(raw[e >> 1]);
-                const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
-                const uint64_t key = sort_key(bf16_to_f32(bits), 8 * i + e);
-                best = key > best ? key : best;
+            for (int u = 0; u < kArgmaxUnroll; ++u) {
+                const int i = i0 + u * step;
+                raw[u] = i < vec ? *reinterpret_cast<const i4*>(x + 8 * i) : i4{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int u = 0; u < kArgmaxUnroll; ++u) {
+                const int i = i0 + u * step;
+                if (i >= vec) { continue; }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t w = static_cast<uint32_t>(raw[u][e >> 1]);
+                    const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+                    const uint64_t key = sort_key(bf16_to_f32(bits), 8 * i + e);
+                    best = key > best ? key : best;
+                }
             }
         }
     }
