@@ -18,10 +18,10 @@
 // key threshold: token v is a member iff sort_key(x_v, v) >= kstar.
 //
 // Launches (tiles of 4096 tokens, all columns and sequences in one grid each):
-//   1 gen_max      tile maxima; zero the coarse histograms
+//   1 gen_max      tile maxima; zero the coarse histograms and the column fine counts
 //   2 gen_coarse   per-token weights -> coarse counts and masses (LDS, then global atomics)
 //   3 gen_cross    per column: total mass, top-p target, crossing coarse bin
-//   4 gen_fine     per tile: counts of the 256 values inside the crossing bin
+//   4 gen_fine     per tile: counts of the 256 values inside the crossing bin (also summed per column)
 //   5 gen_nucleus  per column: crossing value, rank cut, kstar and nucleus mass
 //   6 gen_totals   per tile: accept decision (recomputed per block), masses of the draw
 //   7 gen_pick     per sequence: locate the draw, commit the round
@@ -81,6 +81,7 @@ struct GenArgs {
     uint32_t* ccount;
     ColDesc* desc;
     uint32_t* fine;
+    uint32_t* fine_total;
     uint64_t* tile_res;
     uint64_t* tile_p;
 };
@@ -204,6 +205,7 @@ __global__ __launch_bounds__(kThreads) void gen_max_kernel(GenArgs a) {
     if (t == 0) {
         a.cmass[cb * kGenBins + threadIdx.x] = 0;
         a.ccount[cb * kGenBins + threadIdx.x] = 0;
+        a.fine_total[cb * kGenBins + threadIdx.x] = 0;
     }
 }
 
@@ -308,6 +310,7 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
     }
     __syncthreads();
     a.fine[(cb * a.ntiles + t) * kGenBins + threadIdx.x] = cnt[threadIdx.x];
+    if (cnt[threadIdx.x] != 0) { atomicAdd(&a.fine_total[cb * kGenBins + threadIdx.x], cnt[threadIdx.x]); }
 }
 
 // ---- 5: crossing value, rank cut among equal values, kstar --------------------------------------
@@ -323,9 +326,7 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     __syncthreads();
     // Fine bin f = 255 - tid (descending value order).
     const uint32_t f = kGenBins - 1 - threadIdx.x;
-    uint64_t count = 0;
-#pragma unroll 8
-    for (int t = 0; t < a.ntiles; ++t) { count += a.fine[(cb * a.ntiles + t) * kGenBins + f]; }
+    const uint64_t count = a.fine_total[cb * kGenBins + f];
     const uint32_t o16 = (static_cast<uint32_t>(d.c1) << 8) | f;
     const float x = value_of_ordered16(o16);
     const uint64_t w = gen_weight(x, d.inv_temp, d.m);
@@ -571,6 +572,8 @@ GenPlan plan_general(int32_t token_domain, int32_t K, int32_t B) {
     at = align(at + cols * kGenDescBytes);
     p.fine_offset = at;
     at = align(at + cols * p.ntiles * kGenBins * sizeof(uint32_t));
+    p.fine_total_offset = at;
+    at = align(at + cols * kGenBins * sizeof(uint32_t));
     p.tile_res_offset = at;
     at = align(at + static_cast<size_t>(B) * p.ntiles * 2 * sizeof(uint64_t));
     p.tile_p_offset = at;
@@ -608,6 +611,7 @@ void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* worksp
     a.ccount = reinterpret_cast<uint32_t*>(ws + plan.ccount_offset);
     a.desc = reinterpret_cast<ColDesc*>(ws + plan.desc_offset);
     a.fine = reinterpret_cast<uint32_t*>(ws + plan.fine_offset);
+    a.fine_total = reinterpret_cast<uint32_t*>(ws + plan.fine_total_offset);
     a.tile_res = reinterpret_cast<uint64_t*>(ws + plan.tile_res_offset);
     a.tile_p = reinterpret_cast<uint64_t*>(ws + plan.tile_p_offset);
     const dim3 tiles(plan.ntiles, plan.ncols, l.B);

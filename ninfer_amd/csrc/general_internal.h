@@ -19,6 +19,7 @@ struct GenPlan {
     size_t ccount_offset = 0;
     size_t desc_offset = 0;
     size_t fine_offset = 0;
+    size_t fine_total_offset = 0; // per column: fine counts summed over tiles
     size_t tile_res_offset = 0;
     size_t tile_p_offset = 0;
     size_t bytes = 0;

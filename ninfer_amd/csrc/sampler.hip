@@ -90,41 +90,87 @@ __device__ __forceinline__ float adjusted_logit(float raw, int v, const nmi_samp
 
 // ---- argmax ---------------------------------------------------------------------------------------
 
-// One 1024-thread block per column: 16-byte loads, packed (ordered value, ~id) max.
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// Two BF16 values -> their 16-bit ordered keys (larger key = larger value; NaN ordered as by bits,
+// -0 one below +0): negative halves are inverted, non-negative ones get the sign bit set.
+__device__ __forceinline__ us2 ordered16x2(uint32_t w) {
+    const uint32_t neg = (w >> 15) & 0x00010001u;
+    return __builtin_bit_cast(us2, w ^ (0x80008000u | (neg * 0x7fffu)));
+}
+
+// Largest ordered key among the 8 BF16 values of one 16-byte load.
+__device__ __forceinline__ uint32_t max_ordered8(const i4& raw) {
+    us2 m = __builtin_elementwise_max(ordered16x2(static_cast<uint32_t>(raw[0])), ordered16x2(static_cast<uint32_t>(raw[1])));
+    m = __builtin_elementwise_max(m, __builtin_elementwise_max(ordered16x2(static_cast<uint32_t>(raw[2])),
+                                                               ordered16x2(static_cast<uint32_t>(raw[3]))));
+    return m[0] > m[1] ? m[0] : m[1];
+}
+
+__device__ __forceinline__ uint16_t bf16_at(const i4& raw, int e) {
+    const uint32_t w = static_cast<uint32_t>(raw[e >> 1]);
+    return static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// One 1024-thread block per column. Pass 1 keeps, per thread, the largest 16-bit ordered key of
+// its 16-byte loads (packed max, 2 values per instruction) and the first load that reached it;
+// the winning element and its full key (value, then lowest id; -0 equals +0) are resolved from that
+// one load afterwards. A thread whose largest value is a zero rescans its loads for the first
+// zero of either sign.
 __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* logits, int32_t* out,
                                                       int32_t physical_rows, int32_t valid_rows,
                                                       int64_t column_stride) {
     const int col = blockIdx.x;
     const uint16_t* x = logits + static_cast<int64_t>(col) * column_stride;
     uint64_t best = 0;
-    const int vec = valid_rows / 8;
     const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    if (aligned) {
-        // kArgmaxUnroll independent 16-byte loads per thread are in flight before any is used.
-        constexpr int kArgmaxUnroll = 8;
-        const int step = static_cast<int>(blockDim.x);
-        for (int i0 = threadIdx.x; i0 < vec; i0 += kArgmaxUnroll * step) {
-            i4 raw[kArgmaxUnroll];
+    const int vec = aligned ? valid_rows / 8 : 0;
+    const int step = static_cast<int>(blockDim.x);
+    constexpr int kArgmaxUnroll = 8; // independent 16-byte loads in flight per thread
+    uint32_t top = 0;
+    int top_load = -1;
+    for (int i0 = threadIdx.x; i0 < vec; i0 += kArgmaxUnroll * step) {
+        i4 raw[kArgmaxUnroll];
 #pragma unroll
-            for (int u = 0; u < kArgmaxUnroll; ++u) {
-                const int i = i0 + u * step;
-                raw[u] = i < vec ? *reinterpret_cast<const i4*>(x + 8 * i) : i4{0, 0, 0, 0};
-            }
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const int i = i0 + u * step;
+            raw[u] = i < vec ? *reinterpret_cast<const i4*>(x + 8 * i) : i4{0, 0, 0, 0};
+        }
 #pragma unroll
-            for (int u = 0; u < kArgmaxUnroll; ++u) {
-                const int i = i0 + u * step;
-                if (i >= vec) { continue; }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t w = static_cast<uint32_t>(raw[u][e >> 1]);
-                    const uint16_t bits = static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
-                    const uint64_t key = sort_key(bf16_to_f32(bits), 8 * i + e);
-                    best = key > best ? key : best;
-                }
-            }
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const int i = i0 + u * step;
+            const uint32_t m = max_ordered8(raw[u]);
+            const bool take = i < vec && (m > top || top_load < 0);
+            top = take ? m : top;
+            top_load = take ? i : top_load;
         }
     }
-    for (int v = (aligned ? 8 * vec : 0) + threadIdx.x; v < valid_rows; v += blockDim.x) {
+    if (top_load >= 0) {
+        if (top == 0x8000u || top == 0x7fffu) {
+            // Largest value is a zero: the first zero of either sign among this thread's loads.
+            for (int i = threadIdx.x; i < vec; i += step) {
+                const i4 raw = *reinterpret_cast<const i4*>(x + 8 * i);
+                int e0 = -1;
+#pragma unroll
+                for (int e = 7; e >= 0; --e) { e0 = (bf16_at(raw, e) & 0x7fffu) == 0 ? e : e0; }
+                if (e0 >= 0) {
+                    best = sort_key(0.0f, 8 * i + e0);
+                    break;
+                }
+            }
+        } else {
+            const i4 raw = *reinterpret_cast<const i4*>(x + 8 * top_load);
+            int e0 = 7;
+#pragma unroll
+            for (int e = 7; e >= 0; --e) {
+                const uint16_t h = bf16_at(raw, e);
+                const uint32_t o = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+                e0 = o == top ? e : e0;
+            }
+            best = sort_key(bf16_to_f32(bf16_at(raw, e0)), 8 * top_load + e0);
+        }
+    }
+    for (int v = 8 * vec + threadIdx.x; v < valid_rows; v += blockDim.x) {
         const uint64_t key = sort_key(bf16_to_f32(x[v]), v);
         best = key > best ? key : best;
     }

@@ -62,6 +62,47 @@ def test_argmax_ties_and_domain(gpu, oracle):
     assert got[0] == 500 and got[2] == domain - 1 and got[3] == 0
 
 
+def test_argmax_packed_key_cases(gpu, oracle):
+    """Cases the packed 16-bit pass resolves afterwards: the maximum inside a load, ties inside one
+    load and across threads, all-negative columns, zero maxima with -0 after +0, and an odd
+    physical stride (scalar path)."""
+    C = 8
+    rows, domain = 248320, 248320
+    x = syn.normal_bf16(11, rows * C, std=2.0).reshape(C, rows)
+    big = BF(np.array([40.0], dtype=np.float32))[0]
+    x[0, 8 * 777 + 5] = big
+    x[1, 8 * 900 + 6] = big
+    x[1, 8 * 900 + 3] = big                                   # tie inside one load: id ...3 wins
+    x[2, 8 * 5000 + 1] = big
+    x[2, 8 * 4000 + 7] = big                                  # tie across threads: lower id wins
+    x[3, :] = BF(-np.abs(syn.bf16_bits_to_f32(x[3])) - 1.0)   # all negative
+    x[4, :] = BF(np.array([-3.0], dtype=np.float32))[0]
+    x[4, 8 * 1200 + 2] = 0                                    # +0 first ...
+    x[4, 8 * 3000 + 4] = BF(np.array([-0.0], dtype=np.float32))[0]  # ... then -0: +0 (lower id) wins
+    x[5, :] = BF(np.array([-3.0], dtype=np.float32))[0]
+    x[5, 8 * 2000 + 1] = BF(np.array([-0.0], dtype=np.float32))[0]  # only -0 at the top
+    x[6, 8 * 31000 + 7] = BF(np.array([np.inf], dtype=np.float32))[0]
+    x[7, :] = big                                             # everything ties: id 0
+    d = DeviceArray.from_numpy(na.BF16, x, (rows, C))
+    out = DeviceArray(na.I32, (C,))
+    ops.argmax(d.tensor(), out.tensor(), domain)
+    synchronize()
+    got = out.numpy()
+    exp = oracle.argmax(x.reshape(-1), rows, C, domain)
+    brute = [int(np.argmax(syn.bf16_bits_to_f32(x[c, :domain]))) for c in range(C)]
+    assert list(got) == list(exp) == brute
+    # odd physical stride: columns are not 16-byte aligned
+    rows2, dom2 = 4099, 4097
+    y = syn.normal_bf16(12, rows2 * 3, std=2.0).reshape(3, rows2)
+    y[1, 4096] = big
+    d2 = DeviceArray.from_numpy(na.BF16, y, (rows2, 3))
+    out2 = DeviceArray(na.I32, (3,))
+    ops.argmax(d2.tensor(), out2.tensor(), dom2)
+    synchronize()
+    exp2 = oracle.argmax(y.reshape(-1), rows2, 3, dom2)
+    assert list(out2.numpy()) == list(exp2)
+
+
 # ---- reference known answers -------------------------------------------------------------------------
 
 def test_prepare_verify_inputs_kat(gpu):
