@@ -192,6 +192,12 @@ int nmi_speculative_accept_general(const nmi_tensor* logits, const nmi_tensor* d
 int nmi_speculative_select_accepted_hidden(const nmi_tensor* hidden, const nmi_tensor* accepted,
                                            nmi_tensor* out, nmi_stream_t stream);
 
+/* Replaces mtp_prepare_alignment_ids (include/ninfer/ops/mtp_round.h:19-20): T = K+1 in [2,6];
+ * alignment_ids[i] = verify_ids[i+1] for i < K, then alignment_ids[*accepted] = *token (slot K is
+ * written only when *accepted == K). A device-side accepted outside [0, K] writes no token. */
+int nmi_mtp_prepare_alignment_ids(const nmi_tensor* verify_ids, const nmi_tensor* token,
+                                  const nmi_tensor* accepted, nmi_tensor* alignment_ids, nmi_stream_t stream);
+
 /* ---------------------------------------------------------------- commit / rollback (part c) */
 
 /* Replaces kv_cache_append_prefix (include/ninfer/ops/kv_cache_append_prefix.h:34-37) and

@@ -252,6 +252,14 @@ inline void speculative_select_accepted_hidden(const Tensor& hidden, const Tenso
     detail::check(nmi_speculative_select_accepted_hidden(&ch, &ca, &co, detail::st(stream)));
 }
 
+// include/ninfer/ops/mtp_round.h:19-20.
+inline void mtp_prepare_alignment_ids(const Tensor& verify_ids, const Tensor& token, const Tensor& accepted,
+                                      Tensor& alignment_ids, hipStream_t stream) {
+    const nmi_tensor cv = verify_ids.c(), ct = token.c(), ca = accepted.c();
+    nmi_tensor co = alignment_ids.c();
+    detail::check(nmi_mtp_prepare_alignment_ids(&cv, &ct, &ca, &co, detail::st(stream)));
+}
+
 // include/ninfer/ops/kv_cache_append_prefix.h:34-37 (linear cache; BF16 or INT8-G64).
 inline void kv_cache_append_prefix(const Tensor& k, const Tensor& v, const Tensor& positions,
                                    const Tensor& commit_count, KVCacheAppendPrefixExecutionEnvelope envelope,

@@ -109,6 +109,7 @@ _SIGNATURES = {
     "nmi_general_accept_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32]),
     "nmi_speculative_accept_general": (C.c_int, [_T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_int32, C.c_void_p, C.c_void_p, C.c_size_t, _STREAM]),
     "nmi_speculative_select_accepted_hidden": (C.c_int, [_T, _T, _T, _STREAM]),
+    "nmi_mtp_prepare_alignment_ids": (C.c_int, [_T, _T, _T, _T, _STREAM]),
     "nmi_kv_cache_append_prefix": (C.c_int, [_T, _T, _T, _T, CommitEnvelope, P(KVLayerView), _STREAM]),
     "nmi_kv_cache_rollback": (C.c_int, [_T, _T, P(KVLayerView), _STREAM]),
     "nmi_kv_cache_compact_path": (C.c_int, [_T, _T, _T, P(KVLayerView), _STREAM]),

@@ -174,6 +174,25 @@ int nmi_speculative_select_accepted_hidden(const nmi_tensor* hidden, const nmi_t
     });
 }
 
+// reference mtp_prepare_alignment_ids (src/ops/wrapper/mtp_round.cpp:36-48).
+int nmi_mtp_prepare_alignment_ids(const nmi_tensor* verify_ids, const nmi_tensor* token,
+                                  const nmi_tensor* accepted, nmi_tensor* alignment_ids, nmi_stream_t stream) {
+    const std::string op = "mtp_prepare_alignment_ids";
+    return guarded([&] {
+        require(verify_ids != nullptr, op, "verify_ids must be non-null");
+        const int32_t T = verify_ids->ne[0];
+        require(T >= 2 && T <= 6, op, "T must be in [2,6]");
+        require_scalars(verify_ids, NMI_I32, T, op, "verify_ids");
+        require_scalars(token, NMI_I32, 1, op, "token");
+        require_scalars(accepted, NMI_I32, 1, op, "accepted");
+        require_scalars(alignment_ids, NMI_I32, T, op, "alignment_ids");
+        require(alignment_ids->data != verify_ids->data, op, "verify_ids and alignment_ids must be distinct");
+        launch_mtp_alignment_ids(static_cast<const int32_t*>(verify_ids->data), static_cast<const int32_t*>(token->data),
+                                 static_cast<const int32_t*>(accepted->data), static_cast<int32_t*>(alignment_ids->data), T,
+                                 reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
 int nmi_tree_accept_greedy(const nmi_tensor* parents, const nmi_tensor* node_tokens,
                            const nmi_tensor* target_tokens, nmi_tensor* path, nmi_tensor* path_len,
                            nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,

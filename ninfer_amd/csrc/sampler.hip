@@ -514,6 +514,17 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     }
 }
 
+// ---- MTP alignment ids (include/ninfer/ops/mtp_round.h:10-20) ------------------------------------
+// alignment_ids[i] = verify_ids[i + 1] (i < K), then alignment_ids[accepted] = token; slot K keeps
+// its previous value unless accepted == K. An accepted count outside [0, K] writes no token.
+__global__ void mtp_alignment_ids_kernel(const int32_t* verify_ids, const int32_t* token,
+                                         const int32_t* accepted, int32_t* alignment_ids, int32_t T) {
+    const int i = threadIdx.x;
+    const int acc = *accepted;
+    if (i + 1 < T) { alignment_ids[i] = i == acc ? *token : verify_ids[i + 1]; }
+    if (i == T - 1 && acc == T - 1) { alignment_ids[i] = *token; }
+}
+
 // ---- accepted hidden (include/ninfer/ops/speculative_round.h:76-87) -------------------------------
 __global__ void select_hidden_kernel(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,
                                      int32_t rows, int32_t cols) {
@@ -611,6 +622,13 @@ void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream)
     check_launch("spec_tile_topk_kernel");
     hipLaunchKernelGGL(spec_merge_accept_kernel, dim3(batch), dim3(256), 0, stream, args);
     check_launch("spec_merge_accept_kernel");
+}
+
+void launch_mtp_alignment_ids(const int32_t* verify_ids, const int32_t* token, const int32_t* accepted,
+                              int32_t* alignment_ids, int32_t T, hipStream_t stream) {
+    hipLaunchKernelGGL(mtp_alignment_ids_kernel, dim3(1), dim3(64), 0, stream, verify_ids, token, accepted,
+                       alignment_ids, T);
+    check_launch("mtp_alignment_ids_kernel");
 }
 
 void launch_select_hidden(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,

@@ -50,6 +50,8 @@ void launch_prepare_verify_inputs(const int32_t* token, const int32_t* drafts, c
                                   int32_t* verify_ids, int32_t* positions, int32_t K, int32_t B,
                                   hipStream_t stream);
 void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream);
+void launch_mtp_alignment_ids(const int32_t* verify_ids, const int32_t* token, const int32_t* accepted,
+                              int32_t* alignment_ids, int32_t T, hipStream_t stream);
 void launch_select_hidden(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,
                           int32_t rows, int32_t cols, hipStream_t stream);
 void launch_tree_accept(const int32_t* parents, const int32_t* node_tokens,

@@ -108,6 +108,11 @@ def speculative_select_accepted_hidden(hidden, accepted, out, stream=None) -> No
     check(lib().nmi_speculative_select_accepted_hidden(_p(hidden), _p(accepted), _p(out), _s(stream)))
 
 
+def mtp_prepare_alignment_ids(verify_ids, token, accepted, alignment_ids, stream=None) -> None:
+    """include/ninfer/ops/mtp_round.h:19-20."""
+    check(lib().nmi_mtp_prepare_alignment_ids(_p(verify_ids), _p(token), _p(accepted), _p(alignment_ids), _s(stream)))
+
+
 def tree_accept_greedy(parents, node_tokens, target_tokens, path, path_len, length, token,
                        sampled_out, num_sampled, accepted, stats, stream=None) -> None:
     check(lib().nmi_tree_accept_greedy(_p(parents), _p(node_tokens), _p(target_tokens), _p(path),

@@ -349,6 +349,14 @@ void orc_prepare_verify_inputs(int32_t token, const int32_t* drafts, int32_t len
     }
 }
 
+// src/ops/kernel/mtp_round.cuh (contract include/ninfer/ops/mtp_round.h:10-17): the shifted
+// verify ids, then `token` at slot `accepted`; slot K keeps its previous value unless accepted == K.
+void orc_mtp_prepare_alignment_ids(const int32_t* verify_ids, int32_t T, int32_t token, int32_t accepted,
+                                   int32_t* alignment_ids) {
+    for (int32_t i = 0; i + 1 < T; ++i) { alignment_ids[i] = verify_ids[i + 1]; }
+    if (accepted >= 0 && accepted < T) { alignment_ids[accepted] = token; }
+}
+
 // Penalty: src/ops/kernel/sampling_device.cuh:137-149 (overlay = drafts[0..c-1]).
 static float adjusted_logit(float raw, int32_t v, const orc_sampling_config& c,
                             const int32_t* token_counts, const int32_t* overlay, int32_t overlay_len) {

@@ -69,6 +69,8 @@ typedef struct {
 } orc_sampling_config;
 
 // State scalars live in the caller's host memory; `token_counts` may be NULL.
+void orc_mtp_prepare_alignment_ids(const int32_t* verify_ids, int32_t T, int32_t token, int32_t accepted,
+                                   int32_t* alignment_ids);
 void orc_prepare_verify_inputs(int32_t token, const int32_t* drafts, int32_t length, int32_t K,
                                int32_t* verify_ids, int32_t* positions);
 

@@ -132,6 +132,15 @@ def prepare_verify_inputs(token, drafts, length):
     return ids, pos
 
 
+def mtp_prepare_alignment_ids(verify_ids, token, accepted, alignment_ids):
+    """Returns the updated alignment ids (a copy of `alignment_ids` with the op applied)."""
+    verify_ids = np.ascontiguousarray(verify_ids, dtype=np.int32)
+    out = np.array(alignment_ids, dtype=np.int32, copy=True)
+    lib().orc_mtp_prepare_alignment_ids(_ptr(verify_ids), C.c_int32(verify_ids.size), C.c_int32(token),
+                                        C.c_int32(accepted), _ptr(out))
+    return out
+
+
 def speculative_accept(target_tokens, logits, physical_rows, drafts, length, stats, token_domain, cfg,
                        token_counts=None):
     """Returns dict(sampled_out, num_sampled, accepted, token, length, stats, token_counts)."""

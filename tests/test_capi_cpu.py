@@ -152,6 +152,20 @@ def test_accept_validation():
         ops.speculative_accept_greedy_drafts(*bad, 248320, 0x1000, ws)
 
 
+def test_mtp_alignment_validation():
+    # src/ops/wrapper/mtp_round.cpp:36-48: T in [2,6], I32 contiguous vectors, distinct buffers.
+    with pytest.raises(ValueError, match=re.escape("T must be in [2,6]")):
+        ops.mtp_prepare_alignment_ids(_t(na.I32, (7,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (7,), 0x20000))
+    with pytest.raises(ValueError, match=re.escape("T must be in [2,6]")):
+        ops.mtp_prepare_alignment_ids(_t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (1,), 0x20000))
+    with pytest.raises(ValueError, match="alignment_ids"):
+        ops.mtp_prepare_alignment_ids(_t(na.I32, (4,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (3,), 0x20000))
+    with pytest.raises(ValueError, match="token"):
+        ops.mtp_prepare_alignment_ids(_t(na.I32, (4,)), _t(na.BF16, (1,)), _t(na.I32, (1,)), _t(na.I32, (4,), 0x20000))
+    with pytest.raises(ValueError, match="distinct"):
+        ops.mtp_prepare_alignment_ids(_t(na.I32, (4,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (4,)))
+
+
 def test_argmax_validation():
     with pytest.raises(ValueError, match="valid_rows"):
         ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (4,)), 101)

@@ -288,6 +288,24 @@ def test_select_accepted_hidden(gpu):
         assert np.array_equal(out.numpy(), hidden[a])
 
 
+def test_mtp_alignment_ids(gpu, oracle):
+    k = KATS["mtp_alignment"]
+    cases = [(k["verify_ids"], k["token"], c["accepted"], k["initial"]) for c in k["cases"]]
+    rng = np.random.default_rng(8)
+    for T in range(2, 7):
+        for acc in range(T):
+            cases.append((rng.integers(0, 248320, T), int(rng.integers(0, 248320)), acc, rng.integers(-5, 0, T)))
+    for verify, tok, acc, init in cases:
+        T = len(verify)
+        v = DeviceArray.from_numpy(na.I32, np.asarray(verify, np.int32), (T,))
+        t = DeviceArray.from_numpy(na.I32, np.array([tok], np.int32), (1,))
+        a = DeviceArray.from_numpy(na.I32, np.array([acc], np.int32), (1,))
+        out = DeviceArray.from_numpy(na.I32, np.asarray(init, np.int32), (T,))
+        ops.mtp_prepare_alignment_ids(v.tensor(), t.tensor(), a.tensor(), out.tensor())
+        synchronize()
+        assert list(out.numpy()) == list(oracle.mtp_prepare_alignment_ids(verify, tok, acc, init)), (T, acc)
+
+
 def test_tree_accept_matches_oracle(gpu, oracle):
     B, N = 8, 16
     parents = np.array([[-1] + [(u - 1) // 2 for u in range(1, N)]] * B, dtype=np.int32)

@@ -215,6 +215,13 @@ def test_prepare_verify_kat(oracle):
     assert list(ids) == k["verify_ids"] and list(pos) == k["positions"]
 
 
+def test_mtp_alignment_kat(oracle):
+    k = KATS["mtp_alignment"]
+    for case in k["cases"]:
+        got = oracle.mtp_prepare_alignment_ids(k["verify_ids"], k["token"], case["accepted"], k["initial"])
+        assert list(got) == case["alignment_ids"]
+
+
 @pytest.mark.parametrize("idx", range(4))
 def test_greedy_kats(oracle, idx):
     k = KATS["greedy"][idx]
