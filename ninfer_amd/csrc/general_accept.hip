@@ -234,10 +234,11 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
     column_scale(a, cb, red, &m, &inv_temp); // synchronizes the block
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        if (v0 + e >= a.V) { break; }
-        const uint32_t bin = ordered16(x[e]) >> 8;
-        atomicAdd(&cnt[bin], 1u);
-        atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
+        if (v0 + e < a.V) {
+            const uint32_t bin = ordered16(x[e]) >> 8;
+            atomicAdd(&cnt[bin], 1u);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
+        }
     }
     __syncthreads();
     if (cnt[threadIdx.x] != 0) {
@@ -304,9 +305,8 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        if (v0 + e >= a.V) { break; }
         const uint32_t o = ordered16(x[e]);
-        if (static_cast<int>(o >> 8) == d.c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
+        if (v0 + e < a.V && static_cast<int>(o >> 8) == d.c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
     }
     __syncthreads();
     a.fine[(cb * a.ntiles + t) * kGenBins + threadIdx.x] = cnt[threadIdx.x];
@@ -444,10 +444,11 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
     if (rejected >= 0) { load16(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
 #pragma unroll
     for (int k = 0; k < kPerThread; ++k) {
-        if (v0 + k >= a.V) { break; }
-        const DrawMass dm = draw_mass_x(rejected, p, q, xp[k], xq[k], v0 + k);
-        res += dm.res;
-        pm += dm.p;
+        if (v0 + k < a.V) {
+            const DrawMass dm = draw_mass_x(rejected, p, q, xp[k], xq[k], v0 + k);
+            res += dm.res;
+            pm += dm.p;
+        }
     }
     const u128 rtot = block_scan<u128>(res, shr);
     const uint64_t ptot = block_scan<uint64_t>(pm, shp);
