@@ -153,7 +153,7 @@ void validate_new_kv(const nmi_tensor* k, const nmi_tensor* v, int32_t D, int32_
 
 void require_built(const CacheRef& c, const std::string& op) {
     if (c.kc == nullptr) { throw Unsupported(op + ": BF16 KV cache attention is not built"); }
-    if (c.D != 128) { throw Unsupported(op + ": only head_dim 128 kernels are built"); }
+    if (c.D != 128 && c.D != 256) { throw Unsupported(op + ": head_dim 128 and 256 kernels are built"); }
 }
 
 void require_workspace(void* ws, size_t bytes, size_t need, const std::string& op) {
@@ -202,7 +202,7 @@ extern "C" {
 const char* nmi_last_error(void) { return g_last_error.c_str(); }
 
 const char* nmi_build_info(void) {
-    return "ninfer_amd gfx950: verify_attn_partial<128,{1,2}> fp16-MFMA 16x16x32, "
+    return "ninfer_amd gfx950: verify_attn_partial<{1,2},{128,256}> fp16-MFMA 16x16x32, "
            "verify_attn_merge, kv_quant_append, argmax, speculative accept (greedy, top-20 "
            "stochastic, general fixed-point), kv commit/rollback/compaction";
 }

@@ -45,17 +45,28 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kChunk = 32;
 constexpr int kStride = kChunk * kWaves; // keys between one wave's consecutive chunks
-// One 32-key stage of one KV head in LDS.
-constexpr int kStageK = 0;      // K codes: 32 rows x 128 B; row r's 16-byte piece p at slot p ^ (r & 7)
-constexpr int kStageV = 4096;   // V codes: 32 rows x 128 B, natural order
-constexpr int kStageKS = 8192;  // K scales: 64 keys x (group 0, group 1) FP16; keys 32-63 unused
-constexpr int kStageVS = 8448;  // V scales, same shape
-constexpr int kStageBytes = 8704;
-constexpr int kRingBytes = kWaves * 2 * kStageBytes; // two stages per wave: 69,632 B
-constexpr int kNewStage = kRingBytes;                 // A1: new rows quantized in-kernel (Q tile before)
-constexpr int kPosLds = kNewStage + kStageBytes;      // positions[0 .. T), T <= 32
-constexpr int kSmemBytes = kPosLds + 128;             // 78,464 B: two workgroups per CU
-constexpr int kDmaPerChunk = 10;
+
+// Geometry of one head dimension D (128 or 256): one 32-key stage of one KV head in LDS and the
+// workgroup's LDS map.
+template <int D>
+struct Geo {
+    static constexpr int GQ = D / 64;                  // INT8-G64 quant groups per row
+    static constexpr int PIECES = D / 16;              // 16-byte pieces of a code row
+    static constexpr int QPIECES = D / 8;              // 16-byte pieces of a BF16 Q row
+    static constexpr int kStageK = 0;                  // K codes: 32 rows x D B, piece p of row r at slot p ^ (r % PIECES)
+    static constexpr int kStageV = 32 * D;             // V codes: 32 rows x D B, natural order
+    static constexpr int kStageKS = 64 * D;            // K scales: 256 B (D=128: 64 keys x 2 FP16, keys 32-63 unused;
+                                                       //           D=256: 32 keys x 4 FP16)
+    static constexpr int kStageVS = 64 * D + 256;      // V scales, same shape
+    static constexpr int kStageBytes = 64 * D + 512;   // 8,704 B / 16,896 B
+    static constexpr int kScaleKeyBytes = 2 * GQ;      // scale bytes of one key
+    static constexpr int kDmaPerChunk = D / 16 + 2;    // code DMAs of 1 KB each + one per scale plane
+    static constexpr int kRingBytes = kWaves * 2 * kStageBytes; // two stages per wave
+    static constexpr int kNewStage = kRingBytes;       // A1: new rows quantized in-kernel (Q tile before)
+    static constexpr int kPosLds = kNewStage + kStageBytes; // positions[0 .. T), T <= 32
+    static constexpr int kSmemBytes = kPosLds + 128;   // D=128: 78,464 B (two workgroups per CU); D=256: 152,192 B
+};
+static_assert(Geo<128>::kStageBytes == 8704 && Geo<128>::kSmemBytes == 78464, "D=128 LDS map");
 // Probabilities are FP16 exp2(score - m + 8); the reference maximum m moves only when a score
 // exceeds it by more than 2^7, so P <= 2^15 stays inside FP16 and most chunks skip the rescale.
 constexpr float kPOffset = 8.0f;
@@ -67,9 +78,10 @@ constexpr int kWaitLgkm0 = 0xc07f;
 
 // Wait until one chunk's DMA has landed; with `next_in_flight` the following chunk's stays
 // outstanding (DMAs of one wave complete in issue order).
+template <int D>
 __device__ __forceinline__ void wait_chunk(bool next_in_flight) {
     if (next_in_flight) {
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm(kDmaPerChunk));
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(Geo<D>::kDmaPerChunk));
     } else {
         __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
@@ -137,8 +149,8 @@ __device__ __forceinline__ h8 scale_h8(h8 x, h2 s) {
 }
 
 // Byte (T & 3) of word (T >> 2) from key slots 2w and 2w+1 -> packed FP16 pair (V transpose).
-template <int T>
-__device__ __forceinline__ uint32_t v_pair(const i2& a, const i2& b) {
+template <int T, typename V>
+__device__ __forceinline__ uint32_t v_pair(const V& a, const V& b) {
     return i8x2_to_f16x2<T & 3>(static_cast<uint32_t>(a[T >> 2]), static_cast<uint32_t>(b[T >> 2]));
 }
 
@@ -151,12 +163,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, i
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
 }
 
-// Per-lane DMA source offsets, fixed for the whole kernel.
+// Per-lane DMA source offsets, fixed for the whole kernel. One 1 KB code DMA covers 1024 / D rows;
+// lane -> (row lane / PIECES, slot lane % PIECES). K slot s of row r holds piece s ^ (r % PIECES),
+// and r % PIECES depends on the DMA's index when a DMA covers fewer than PIECES rows (D = 256:
+// 4 rows per DMA, 16 pieces), so K keeps one offset per DMA index modulo kvar(D).
 struct DmaLanes {
-    int k;  // row lane >> 3, piece (lane & 7) ^ (lane >> 3): the swizzled K layout
-    int v;  // row lane >> 3, bytes 16 * (lane & 7)
+    int k[4];
+    int v;
     int sc; // scale word lane
 };
+
+template <int D>
+constexpr int kvar() { return Geo<D>::PIECES / (1024 / D) > 1 ? Geo<D>::PIECES / (1024 / D) : 1; }
+
+template <int D>
+__device__ __forceinline__ DmaLanes make_dma_lanes(int lane) {
+    constexpr int P = Geo<D>::PIECES;
+    constexpr int ROWS = 1024 / D;
+    const int row = lane / P;
+    const int slot = lane % P;
+    DmaLanes dl{};
+#pragma unroll
+    for (int q = 0; q < kvar<D>(); ++q) { dl.k[q] = row * D + 16 * (slot ^ ((ROWS * q + row) % P)); }
+    dl.v = row * D + 16 * slot;
+    dl.sc = lane * 4;
+    return dl;
+}
 
 // Issue the DMA of one 32-key chunk (c0 + 32 <= P) into `st`: 4 K blocks, 4 V blocks and the K and
 // V scale words of keys c0..c0+63 (the upper 32 are not used; the chunk offset of the scales sits in
@@ -164,48 +196,69 @@ struct DmaLanes {
 // codes go through soffset, which moves only the source address; the LDS address is M0 + 16 * lane
 // (4 * lane for scales). Both scale loads run on the full wave: lane-divergent descriptors would
 // turn one DMA into a waterfall loop.
-__device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers& hb, const DmaLanes& dl,
-                                            int c0, int lane) {
-    const int so = c0 * 128;
-#pragma unroll
-    for (int r8 = 0; r8 < 4; ++r8) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.k, (NMI_AS3 void*)(st + kStageK + r8 * 1024), 16, dl.k, so + r8 * 1024, 0, 0);
-    }
-#pragma unroll
-    for (int r8 = 0; r8 < 4; ++r8) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.v, (NMI_AS3 void*)(st + kStageV + r8 * 1024), 16, dl.v, so + r8 * 1024, 0, 0);
-    }
-    const int vso = dl.sc + c0 * 4;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.ks, (NMI_AS3 void*)(st + kStageKS), 4, vso, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(hb.vs, (NMI_AS3 void*)(st + kStageVS), 4, vso, 0, 0, 0);
+// One LDS-DMA instruction: 16 bytes (or 4 for scales) per lane from rsrc + voffset + soffset into
+// lds + 16 * lane (4 * lane). Plain functions: the host compile pass rejects these builtins inside
+// function templates.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char* lds, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NMI_AS3 void*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char* lds, int voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NMI_AS3 void*)lds, 4, voff, 0, 0, 0);
 }
 
-// One chunk in registers: K codes in A-operand order, the K scale word of key 16kt + c, the V scale
-// words of keys 4g..4g+3 and 16+4g..16+4g+3, and 8 bytes (dims 8c..8c+7) of the lane's 8 V rows.
+template <int D>
+__device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers& hb, const DmaLanes& dl,
+                                            int c0, int lane) {
+    using G = Geo<D>;
+    constexpr int NDMA = D / 32; // 1 KB code DMAs per plane
+    const int so = c0 * D;
+#pragma unroll
+    for (int r8 = 0; r8 < NDMA; ++r8) { dma16(hb.k, st + G::kStageK + r8 * 1024, dl.k[r8 % kvar<D>()], so + r8 * 1024); }
+#pragma unroll
+    for (int r8 = 0; r8 < NDMA; ++r8) { dma16(hb.v, st + G::kStageV + r8 * 1024, dl.v, so + r8 * 1024); }
+    const int vso = dl.sc + c0 * G::kScaleKeyBytes;
+    dma4(hb.ks, st + G::kStageKS, vso);
+    dma4(hb.vs, st + G::kStageVS, vso);
+}
+
+// One chunk in registers: K codes in A-operand order, the K scale words of key 16kt + c, the V
+// scale words of keys 4g..4g+3 and 16+4g..16+4g+3, and D/16 bytes (dims (D/16)c ..) of the lane's
+// 8 V rows.
+template <int D>
 struct ChunkRegs {
-    i4 kr[2][2];
-    uint32_t ksc[2];
-    i4 vsw[2];
-    i2 vr[8];
+    static constexpr int GQ = D / 64;
+    using VRow = std::conditional_t<D == 128, i2, i4>; // the lane's bytes of one V row
+    using KSc = std::conditional_t<D == 128, uint32_t, i2>; // one key's K scales
+    i4 kr[2][GQ];
+    KSc ksc[2];
+    i4 vsw[2][D / 128];
+    VRow vr[8];
 };
 
-__device__ __forceinline__ void read_chunk(const NMI_AS3 char* st, ChunkRegs& r, int lane, int c, int g) {
+template <int D>
+__device__ __forceinline__ void read_chunk(const NMI_AS3 char* st, ChunkRegs<D>& r, int lane, int c, int g) {
+    using G = Geo<D>;
+    using CR = ChunkRegs<D>;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) {
+        for (int gq = 0; gq < G::GQ; ++gq) {
             // A operand: key 16kt + c, dims 64gq + 16g .. +15 = piece 4gq + g of row 16kt + c.
-            const int slot = (4 * gq + g) ^ (c & 7);
-            r.kr[kt][gq] = *(const NMI_AS3 i4*)(st + kStageK + (16 * kt + c) * 128 + 16 * slot);
+            const int slot = (4 * gq + g) ^ ((16 * kt + c) % G::PIECES);
+            r.kr[kt][gq] = *(const NMI_AS3 i4*)(st + G::kStageK + (16 * kt + c) * D + 16 * slot);
         }
-        r.ksc[kt] = *(const NMI_AS3 uint32_t*)(st + kStageKS + 4 * (16 * kt + c));
+        r.ksc[kt] = *(const NMI_AS3 typename CR::KSc*)(st + G::kStageKS + G::kScaleKeyBytes * (16 * kt + c));
     }
-    r.vsw[0] = *(const NMI_AS3 i4*)(st + kStageVS + 16 * g);
-    r.vsw[1] = *(const NMI_AS3 i4*)(st + kStageVS + 64 + 16 * g);
+#pragma unroll
+    for (int h = 0; h < D / 128; ++h) {
+        // 4 keys' scales: 16 B (D = 128) or 32 B (D = 256).
+        r.vsw[0][h] = *(const NMI_AS3 i4*)(st + G::kStageVS + 4 * G::kScaleKeyBytes * g + 16 * h);
+        r.vsw[1][h] = *(const NMI_AS3 i4*)(st + G::kStageVS + G::kScaleKeyBytes * (16 + 4 * g) + 16 * h);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-        r.vr[j] = *(const NMI_AS3 i2*)(st + kStageV + row * 128 + 8 * c);
+        r.vr[j] = *(const NMI_AS3 typename CR::VRow*)(st + G::kStageV + row * D + (D / 16) * c);
     }
 }
 
@@ -219,25 +272,34 @@ struct KeyRange {
 };
 
 // Online-softmax state of one wave: NT tiles of 16 rows.
-template <int NT>
+template <int NT, int D>
 struct RowState {
-    h8 q[NT][2][2];   // B operand of Q^T: rows 16nt + c, dims 64gq + 16g + 8s + e
-    float rowmul[NT]; // softmax scale * log2(e) / Q power-of-two factor
-    float rowthr[NT]; // kLazyTau / rowmul: the lazy-rescale threshold in raw score units
+    h8 q[NT][D / 64][2]; // B operand of Q^T: rows 16nt + c, dims 64gq + 16g + 8s + e
+    float rowmul[NT];    // softmax scale * log2(e) / Q power-of-two factor
+    float rowthr[NT];    // kLazyTau / rowmul: the lazy-rescale threshold in raw score units
     uint32_t nmask[NT];
-    float m[NT];      // reference maximum in raw score units
-    f4 O[NT][8];      // O^T tiles: tile t row 4g+e is dim 8(4g+e) + t
-    f4 l[NT];         // row sums, equal in all four entries (ones x P^T)
+    float m[NT];         // reference maximum in raw score units
+    f4 O[NT][D / 16];    // O^T tiles: tile t row 4g+e is dim (D/16)(4g+e) + t
+    f4 l[NT];            // row sums, equal in all four entries (ones x P^T)
 };
 
+// FP16 scale `gq` of one key's scale word(s), broadcast to both halves of a pair.
+__device__ __forceinline__ uint32_t scale_pair(uint32_t w, int gq) {
+    return __builtin_amdgcn_perm(w, w, gq ? 0x03020302u : 0x01000100u);
+}
+__device__ __forceinline__ uint32_t scale_pair(const i2& w, int gq) {
+    const uint32_t x = static_cast<uint32_t>(w[gq >> 1]);
+    return __builtin_amdgcn_perm(x, x, (gq & 1) ? 0x03020302u : 0x01000100u);
+}
+
 // S^T = K' Q^T with K' = FP16(code * scale) as the A operand (key 16kt + c).
-template <int NT>
-__device__ __forceinline__ void qk_chunk(const ChunkRegs& r, const RowState<NT>& s, f4 (&sacc)[2][NT]) {
+template <int NT, int D>
+__device__ __forceinline__ void qk_chunk(const ChunkRegs<D>& r, const RowState<NT, D>& s, f4 (&sacc)[2][NT]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int gq = 0; gq < 2; ++gq) {
-            const uint32_t sp = __builtin_amdgcn_perm(r.ksc[kt], r.ksc[kt], gq ? 0x03020302u : 0x01000100u);
+        for (int gq = 0; gq < D / 64; ++gq) {
+            const uint32_t sp = scale_pair(r.ksc[kt], gq);
             const h2 s2 = __builtin_bit_cast(h2, sp);
             const h8 a0 = scale_h8(cvt_codes8(r.kr[kt][gq][0], r.kr[kt][gq][1]), s2);
             const h8 a1 = scale_h8(cvt_codes8(r.kr[kt][gq][2], r.kr[kt][gq][3]), s2);
@@ -253,8 +315,8 @@ __device__ __forceinline__ void qk_chunk(const ChunkRegs& r, const RowState<NT>&
 
 // Online softmax of one chunk; the S^T accumulator layout is the B-operand layout of P^T. `masked`
 // is uniform across the wave.
-template <int NT>
-__device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, bool masked, RowState<NT>& s,
+template <int NT, int D>
+__device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, bool masked, RowState<NT, D>& s,
                                               const KeyRange& kr, int g, h8 (&pop)[NT]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -282,7 +344,7 @@ __device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, b
             const float mn = need ? cmax : s.m[nt];
             const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) { s.O[nt][t] *= alpha; }
+            for (int t = 0; t < D / 16; ++t) { s.O[nt][t] *= alpha; }
             s.l[nt] *= alpha;
             s.m[nt] = mn;
         }
@@ -294,17 +356,43 @@ __device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, b
     }
 }
 
+// The FP16 V scales of the lane's group for its 8 keys (4g + j and 16 + 4g + j), as 4 key pairs.
+// D = 128: the lane's dims 8c..8c+7 lie in group c >> 3, and a key's scales are one word.
+// D = 256: dims 16c..16c+15 lie in group c >> 2, and a key's scales are two words.
+template <int D>
+__device__ __forceinline__ void v_scale_pairs(const i4 (&vsw)[2][D / 128], int c, h2 (&vsp)[4]) {
+    if constexpr (D == 128) {
+        const uint32_t vsel = (c >> 3) ? 0x07060302u : 0x05040100u; // FP16 half of this lane's group
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            vsp[2 * half] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[half][0][1]), static_cast<uint32_t>(vsw[half][0][0]), vsel));
+            vsp[2 * half + 1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[half][0][3]), static_cast<uint32_t>(vsw[half][0][2]), vsel));
+        }
+    } else {
+        const int grp = c >> 2;                               // FP16 index of the group in a key's 4
+        const uint32_t vsel = (grp & 1) ? 0x07060302u : 0x05040100u;
+        const int w = grp >> 1;                               // word of the key holding it
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            // keys j and j + 1 of this half: words [2j + w] of the 32 bytes (two i4)
+#pragma unroll
+            for (int p2 = 0; p2 < 2; ++p2) {
+                const uint32_t a = static_cast<uint32_t>(vsw[half][p2][w]);      // key 2 p2
+                const uint32_t b = static_cast<uint32_t>(vsw[half][p2][2 + w]);  // key 2 p2 + 1
+                vsp[2 * half + p2] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(b, a, vsel));
+            }
+        }
+    }
+}
+
 // O^T += V'^T P^T with V' = FP16(code * scale); l += ones x P^T. Keys at or past key_end of a
 // masked chunk get a zero V scale.
-template <int NT>
-__device__ __forceinline__ void pv_chunk(const h8 (&pop)[NT], const i2 (&vr)[8], const i4 (&vsw)[2], int c0,
-                                         bool masked, RowState<NT>& s, const KeyRange& kr, int c, int g) {
-    const uint32_t vsel = (c >> 3) ? 0x07060302u : 0x05040100u; // FP16 half of this lane's group
+template <int NT, int D>
+__device__ __forceinline__ void pv_chunk(const h8 (&pop)[NT], const typename ChunkRegs<D>::VRow (&vr)[8],
+                                         const i4 (&vsw)[2][D / 128], int c0, bool masked, RowState<NT, D>& s,
+                                         const KeyRange& kr, int c, int g) {
     h2 vsp[4];
-    vsp[0] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[0][1]), static_cast<uint32_t>(vsw[0][0]), vsel));
-    vsp[1] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[0][3]), static_cast<uint32_t>(vsw[0][2]), vsel));
-    vsp[2] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[1][1]), static_cast<uint32_t>(vsw[1][0]), vsel));
-    vsp[3] = __builtin_bit_cast(h2, __builtin_amdgcn_perm(static_cast<uint32_t>(vsw[1][3]), static_cast<uint32_t>(vsw[1][2]), vsel));
+    v_scale_pairs<D>(vsw, c, vsp);
     if (masked) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -331,34 +419,51 @@ __device__ __forceinline__ void pv_chunk(const h8 (&pop)[NT], const i2 (&vr)[8],
     NMI_PV_TILE(5)
     NMI_PV_TILE(6)
     NMI_PV_TILE(7)
+    if constexpr (D == 256) {
+        NMI_PV_TILE(8)
+        NMI_PV_TILE(9)
+        NMI_PV_TILE(10)
+        NMI_PV_TILE(11)
+        NMI_PV_TILE(12)
+        NMI_PV_TILE(13)
+        NMI_PV_TILE(14)
+        NMI_PV_TILE(15)
+    }
 #undef NMI_PV_TILE
     const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) { s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop[nt], s.l[nt], 0, 0, 0); }
 }
 
-template <int NT>
-__device__ __forceinline__ void compute_chunk(const ChunkRegs& r, int c0, bool masked, RowState<NT>& s,
+template <int NT, int D>
+__device__ __forceinline__ void compute_chunk(const ChunkRegs<D>& r, int c0, bool masked, RowState<NT, D>& s,
                                               const KeyRange& kr, int c, int g) {
     f4 sacc[2][NT];
-    qk_chunk<NT>(r, s, sacc);
+    qk_chunk<NT, D>(r, s, sacc);
     h8 pop[NT];
-    softmax_chunk<NT>(sacc, c0, masked, s, kr, g, pop);
-    pv_chunk<NT>(pop, r.vr, r.vsw, c0, masked, s, kr, c, g);
+    softmax_chunk<NT, D>(sacc, c0, masked, s, kr, g, pop);
+    pv_chunk<NT, D>(pop, r.vr, r.vsw, c0, masked, s, kr, c, g);
 }
 
-// Quantize one new token row of one KV head (one wave: lane owns dims lane and lane + 64 of K and
+// Quantize one new token row of one KV head (one wave: lane owns dim lane + 64 i of group i of K and
 // V; reference contract include/ninfer/ops/gqa_attention.h:25-30) into the cache and into key slot
 // u of the LDS stage `st`, in the layout the chunk DMA produces.
+template <int D>
 __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t* vsrc, int8_t* kdst,
                                            int8_t* vdst, uint16_t* ksdst, uint16_t* vsdst,
                                            NMI_AS3 char* st, int u, int lane) {
-    const float x[4] = {bf16_to_f32(ksrc[lane]), bf16_to_f32(ksrc[64 + lane]), bf16_to_f32(vsrc[lane]),
-                        bf16_to_f32(vsrc[64 + lane])};
-    uint16_t sbits[4];
-    int8_t code[4];
+    using G = Geo<D>;
+    constexpr int GQ = G::GQ;
+    float x[2 * GQ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < GQ; ++i) {
+        x[i] = bf16_to_f32(ksrc[64 * i + lane]);
+        x[GQ + i] = bf16_to_f32(vsrc[64 * i + lane]);
+    }
+    uint16_t sbits[2 * GQ];
+    int8_t code[2 * GQ];
+#pragma unroll
+    for (int i = 0; i < 2 * GQ; ++i) {
         const float amax = wave_max(fabsf(x[i]));
         sbits[i] = f32_to_f16_bits(amax > 0.0f ? amax / 127.0f : 0.0f);
         const float sc = f16_bits_to_f32(sbits[i]);
@@ -367,31 +472,39 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
         rr = fminf(127.0f, fmaxf(-127.0f, rr));
         code[i] = static_cast<int8_t>(rr);
     }
-    kdst[lane] = code[0];
-    kdst[64 + lane] = code[1];
-    vdst[lane] = code[2];
-    vdst[64 + lane] = code[3];
-    const uint32_t kw = static_cast<uint32_t>(sbits[0]) | (static_cast<uint32_t>(sbits[1]) << 16);
-    const uint32_t vw = static_cast<uint32_t>(sbits[2]) | (static_cast<uint32_t>(sbits[3]) << 16);
-    if (lane == 0) {
-        *reinterpret_cast<uint32_t*>(ksdst) = kw;
-        *reinterpret_cast<uint32_t*>(vsdst) = vw;
-        *(NMI_AS3 uint32_t*)(st + kStageKS + 4 * u) = kw;
-        *(NMI_AS3 uint32_t*)(st + kStageVS + 4 * u) = vw;
+#pragma unroll
+    for (int i = 0; i < GQ; ++i) {
+        kdst[64 * i + lane] = code[i];
+        vdst[64 * i + lane] = code[GQ + i];
     }
-    // Swizzled K row u: dim d sits in piece d >> 4 at slot (d >> 4) ^ (u & 7).
-    const int krow = kStageK + u * 128 + (lane & 15);
-    st[krow + 16 * ((lane >> 4) ^ (u & 7))] = static_cast<char>(code[0]);
-    st[krow + 16 * ((4 + (lane >> 4)) ^ (u & 7))] = static_cast<char>(code[1]);
-    st[kStageV + u * 128 + lane] = static_cast<char>(code[2]);
-    st[kStageV + u * 128 + 64 + lane] = static_cast<char>(code[3]);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < GQ; i += 2) {
+            const uint32_t kw = static_cast<uint32_t>(sbits[i]) | (static_cast<uint32_t>(sbits[i + 1]) << 16);
+            const uint32_t vw = static_cast<uint32_t>(sbits[GQ + i]) | (static_cast<uint32_t>(sbits[GQ + i + 1]) << 16);
+            *reinterpret_cast<uint32_t*>(ksdst + i) = kw;
+            *reinterpret_cast<uint32_t*>(vsdst + i) = vw;
+            *(NMI_AS3 uint32_t*)(st + G::kStageKS + G::kScaleKeyBytes * u + 2 * i) = kw;
+            *(NMI_AS3 uint32_t*)(st + G::kStageVS + G::kScaleKeyBytes * u + 2 * i) = vw;
+        }
+    }
+    // Swizzled K row u: dim d sits in piece d >> 4 at slot (d >> 4) ^ (u % PIECES).
+    const int krow = G::kStageK + u * D + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < GQ; ++i) {
+        st[krow + 16 * ((4 * i + (lane >> 4)) ^ (u % G::PIECES))] = static_cast<char>(code[i]);
+        st[G::kStageV + u * D + 64 * i + lane] = static_cast<char>(code[GQ + i]);
+    }
 }
 
-template <int NT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void verify_attn_partial_kernel(AttnArgs a) {
-    constexpr int D = 128;
-    constexpr int G = 2; // quant groups per row
-    __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+// D = 128: 78 KB of LDS and at most 256 registers, two workgroups per CU. D = 256: 152 KB of LDS,
+// one workgroup (one wave per SIMD) per CU, which leaves 512 registers per lane for the doubled
+// accumulators and chunk registers.
+template <int NT, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1, D == 128 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
+    constexpr int G = D / 64; // quant groups per row
+    using GE = Geo<D>;
+    __shared__ __attribute__((aligned(16))) char smem[GE::kSmemBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -410,9 +523,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     uint16_t* ksbase = a.ks + head_scale;
     uint16_t* vsbase = a.vs + head_scale;
     const HeadBuffers hb{raw_buffer(kbase, static_cast<int64_t>(a.P) * D), raw_buffer(vbase, static_cast<int64_t>(a.P) * D),
-                         raw_buffer(ksbase, static_cast<int64_t>(a.P) * 4), raw_buffer(vsbase, static_cast<int64_t>(a.P) * 4)};
-    const DmaLanes dl{(lane >> 3) * 128 + 16 * ((lane & 7) ^ (lane >> 3)), (lane >> 3) * 128 + 16 * (lane & 7), lane * 4};
-    NMI_AS3 char* ring = (NMI_AS3 char*)smem + wave * 2 * kStageBytes;
+                         raw_buffer(ksbase, static_cast<int64_t>(a.P) * 2 * G), raw_buffer(vsbase, static_cast<int64_t>(a.P) * 2 * G)};
+    const DmaLanes dl = make_dma_lanes<D>(lane);
+    NMI_AS3 char* ring = (NMI_AS3 char*)smem + wave * 2 * GE::kStageBytes;
 
     // Q tile (rows r = tl * G + gi of this workgroup, 256 B each) moves HBM -> LDS by DMA before
     // any chunk DMA is queued, into the new-row stage area (free until an owner builds that stage).
@@ -420,21 +533,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int t0 = rc * a.tokens_per_chunk;
     const int Tc = min(a.tokens_per_chunk, a.T - t0);
     const int R = Tc * a.G;
-    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + kNewStage;
-    NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + kPosLds);
+    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + GE::kNewStage;
+    NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GE::kPosLds);
     const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
     if (wave == 0) {
         // Positions travel the same way (a vector load here would wait behind every chunk DMA).
         if (lane < a.T) { __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)(pos + lane), (NMI_AS3 void*)pos_lds, 4, 0, 0); }
+        constexpr int QP = GE::QPIECES;  // 16-byte pieces of a Q row
+        constexpr int RPD = 64 / QP;     // Q rows per 1 KB DMA
 #pragma unroll 1
-        for (int k = 0; 4 * k < R; ++k) {
-            const int row = 4 * k + (lane >> 4);
+        for (int k = 0; RPD * k < R; ++k) {
+            const int row = RPD * k + lane / QP;
             if (row < R) {
                 const int tl = row / a.G;
                 const int gi = row - tl * a.G;
-                // Slot (lane & 15) of the row holds piece (slot - row) & 15: rows rotate across the
+                // Slot (lane % QP) of the row holds piece (slot - row) % QP: rows rotate across the
                 // LDS banks, so the 16 lanes that read one column of rows do not conflict.
-                const int piece = ((lane & 15) - row) & 15;
+                const int piece = ((lane % QP) - row) & (QP - 1);
                 const uint16_t* src = a.q + static_cast<int64_t>(D) * (h * a.G + gi + static_cast<int64_t>(a.Hq) * (t0 + tl + static_cast<int64_t>(a.T) * b)) + 8 * piece;
                 __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(qtile + k * 1024), 16, 0, 0);
             }
@@ -445,13 +560,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // that turns out to lie past the split's range is simply never read (it stays inside the
     // padded cache, and the waits below fall back to vmcnt(0) when the next chunk is unused).
     const int first = k0 + kChunk * wave;
-    if (first + kChunk <= a.P) { issue_chunk(ring, hb, dl, first, lane); }
-    if (first + kStride + kChunk <= a.P) { issue_chunk(ring + kStageBytes, hb, dl, first + kStride, lane); }
+    if (first + kChunk <= a.P) { issue_chunk<D>(ring, hb, dl, first, lane); }
+    if (first + kStride + kChunk <= a.P) { issue_chunk<D>(ring + GE::kStageBytes, hb, dl, first + kStride, lane); }
     if (wave == 0) {
         if (first + kStride + kChunk <= a.P) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kDmaPerChunk));
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * GE::kDmaPerChunk));
         } else if (first + kChunk <= a.P) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(kDmaPerChunk));
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(GE::kDmaPerChunk));
         } else {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         }
@@ -468,7 +583,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
             for (int hs = 0; hs < 2; ++hs) {
                 const int piece = 8 * gq + 2 * g + hs; // dims 8 * piece .. + 7
-                const i4 v = *(const NMI_AS3 i4*)(qtile + (r & 31) * 256 + 16 * ((piece + r) & 15));
+                const i4 v = *(const NMI_AS3 i4*)(qtile + (r & 31) * (2 * D) + 16 * ((piece + r) & (GE::QPIECES - 1)));
                 qraw[nt][gq][hs] = r < R ? v : i4{0, 0, 0, 0};
             }
         }
@@ -479,7 +594,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int pos_last = __builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]);
 
     // ---- Q operand (B operand of S^T = K' Q^T) from the raw rows.
-    RowState<NT> s;
+    RowState<NT, D> s;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int r = 16 * nt + c;
@@ -524,7 +639,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         s.m[nt] = -INFINITY;
         s.l[nt] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int t8 = 0; t8 < 8; ++t8) { s.O[nt][t8] = f4{0.f, 0.f, 0.f, 0.f}; }
+        for (int t8 = 0; t8 < D / 16; ++t8) { s.O[nt][t8] = f4{0.f, 0.f, 0.f, 0.f}; }
     }
 
 
@@ -554,67 +669,86 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // ---- fused A1 append: the owner quantizes the T new rows into the cache and into its new-row
     // stage; wave 0 attends to them before its history chunks.
     if (owner) {
-        NMI_AS3 char* ns = (NMI_AS3 char*)smem + kNewStage;
+        NMI_AS3 char* ns = (NMI_AS3 char*)smem + GE::kNewStage;
         __syncthreads(); // every wave has read its Q rows from this area
-        for (int i = threadIdx.x; i < kStageBytes / 16; i += blockDim.x) { *(NMI_AS3 i4*)(ns + 16 * i) = i4{0, 0, 0, 0}; }
+        for (int i = threadIdx.x; i < GE::kStageBytes / 16; i += blockDim.x) { *(NMI_AS3 i4*)(ns + 16 * i) = i4{0, 0, 0, 0}; }
         __syncthreads();
         for (int t = wave; t < a.T; t += kWaves) {
             const int p = pos_lds[t];
             if (p < 0 || p >= a.P) { continue; }
             const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (t + static_cast<int64_t>(a.T) * b));
-            append_row(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D, vbase + static_cast<int64_t>(p) * D,
+            append_row<D>(a.k_new + src, a.v_new + src, kbase + static_cast<int64_t>(p) * D, vbase + static_cast<int64_t>(p) * D,
                        ksbase + static_cast<int64_t>(p) * G, vsbase + static_cast<int64_t>(p) * G, ns, t, lane);
         }
         __syncthreads();
         if (wave == 0) {
-            ChunkRegs r;
-            read_chunk(ns, r, lane, c, g);
+            ChunkRegs<D> r;
+            read_chunk<D>(ns, r, lane, c, g);
             const KeyRange nk{L, L, min(window, L + a.T)};
-            compute_chunk<NT>(r, L, true, s, nk, c, g);
+            compute_chunk<NT, D>(r, L, true, s, nk, c, g);
         }
     }
 
     // ---- history chunks, software-pipelined: while chunk j's softmax and PV run, chunk j+1 is
-    // read from LDS and its QK^T issued, and chunks j+2, j+3 are in flight as DMA.
+    // read from LDS and its QK^T issued, and chunks j+2, j+3 are in flight as DMA. D = 256 holds
+    // one chunk in registers at a time (the DMA lookahead stays two chunks).
     const KeyRange hk{min(L, k1), L, hend};
-    if (first < hend) {
+    if constexpr (D == 256) {
+        int stage = 0;
+#pragma unroll 1
+        for (int cj = first; cj < hend; cj += kStride) {
+            NMI_AS3 char* st = ring + stage * GE::kStageBytes;
+            wait_chunk<D>(cj + kStride < hend); // chunk cj landed; the next one may stay in flight
+            ChunkRegs<D> r;
+            read_chunk<D>(st, r, lane, c, g);
+            if (cj + 2 * kStride < hend) {
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk cj sits in registers: reuse its stage
+                issue_chunk<D>(st, hb, dl, cj + 2 * kStride, lane);
+            }
+            compute_chunk<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
+            stage ^= 1;
+        }
+    } else if (first < hend) {
         int stage = 0;
         int cj = first;
-        ChunkRegs r;
-        wait_chunk(first + kStride < hend);
-        read_chunk(ring, r, lane, c, g);
+        ChunkRegs<D> r;
+        wait_chunk<D>(first + kStride < hend);
+        read_chunk<D>(ring, r, lane, c, g);
         if (first + 2 * kStride < hend) {
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-            issue_chunk(ring, hb, dl, first + 2 * kStride, lane);
+            issue_chunk<D>(ring, hb, dl, first + 2 * kStride, lane);
         }
         f4 sacc[2][NT];
-        qk_chunk<NT>(r, s, sacc);
-        i2 vcur[8];
-        i4 vswcur[2];
+        qk_chunk<NT, D>(r, s, sacc);
+        typename ChunkRegs<D>::VRow vcur[8];
+        i4 vswcur[2][D / 128];
 #pragma unroll
         for (int j = 0; j < 8; ++j) { vcur[j] = r.vr[j]; }
-        vswcur[0] = r.vsw[0];
-        vswcur[1] = r.vsw[1];
+#pragma unroll
+        for (int h = 0; h < D / 128; ++h) {
+            vswcur[0][h] = r.vsw[0][h];
+            vswcur[1][h] = r.vsw[1][h];
+        }
         stage = 1;
 #pragma unroll 1
         for (; cj < hend; cj += kStride) {
             const int cn = cj + kStride; // next chunk (if < hend, its DMA was issued two steps ago)
-            NMI_AS3 char* stn = ring + stage * kStageBytes;
+            NMI_AS3 char* stn = ring + stage * GE::kStageBytes;
             // Chunk j+1's DMA done (j+2's may stay outstanding). Reading a stage past the end is
             // harmless: those registers are never used.
-            wait_chunk(cn + kStride < hend);
-            ChunkRegs rn;
-            read_chunk(stn, rn, lane, c, g);
+            wait_chunk<D>(cn + kStride < hend);
+            ChunkRegs<D> rn;
+            read_chunk<D>(stn, rn, lane, c, g);
             h8 pop[NT];
-            softmax_chunk<NT>(sacc, cj, cj + kChunk > hk.vis_all, s, hk, g, pop);
+            softmax_chunk<NT, D>(sacc, cj, cj + kChunk > hk.vis_all, s, hk, g, pop);
             if (cn + 2 * kStride < hend) {
                 __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk j+1 sits in registers: reuse its stage
-                issue_chunk(stn, hb, dl, cn + 2 * kStride, lane);
+                issue_chunk<D>(stn, hb, dl, cn + 2 * kStride, lane);
             }
             stage ^= 1;
             f4 sn[2][NT];
-            if (cn < hend) { qk_chunk<NT>(rn, s, sn); } // the last chunk has no successor
-            pv_chunk<NT>(pop, vcur, vswcur, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
+            if (cn < hend) { qk_chunk<NT, D>(rn, s, sn); } // the last chunk has no successor
+            pv_chunk<NT, D>(pop, vcur, vswcur, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -622,8 +756,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) { vcur[j] = rn.vr[j]; }
-            vswcur[0] = rn.vsw[0];
-            vswcur[1] = rn.vsw[1];
+#pragma unroll
+            for (int h = 0; h < D / 128; ++h) {
+                vswcur[0][h] = rn.vsw[0][h];
+                vswcur[1][h] = rn.vsw[1][h];
+            }
         }
     }
 
@@ -631,6 +768,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
     __syncthreads();
     constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
+    static_assert(kWaves * 32 * (kRowStride + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
     float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
     float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
     float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
@@ -644,10 +782,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            // O^T tile t row (4g + e) is dim 8*(4g + e) + t: eight consecutive dims per (lane, e).
-            float* dst = sm_o + (wave * 32 + r) * kRowStride + 8 * (4 * g + e);
-            *reinterpret_cast<f4*>(dst) = f4{s.O[nt][0][e], s.O[nt][1][e], s.O[nt][2][e], s.O[nt][3][e]};
-            *reinterpret_cast<f4*>(dst + 4) = f4{s.O[nt][4][e], s.O[nt][5][e], s.O[nt][6][e], s.O[nt][7][e]};
+            // O^T tile t row (4g + e) is dim (D/16)(4g + e) + t: D/16 consecutive dims per (lane, e).
+            float* dst = sm_o + (wave * 32 + r) * kRowStride + (D / 16) * (4 * g + e);
+#pragma unroll
+            for (int q4 = 0; q4 < D / 64; ++q4) {
+                *reinterpret_cast<f4*>(dst + 4 * q4) =
+                    f4{s.O[nt][4 * q4][e], s.O[nt][4 * q4 + 1][e], s.O[nt][4 * q4 + 2][e], s.O[nt][4 * q4 + 3][e]};
+            }
         }
     }
     __syncthreads();
@@ -839,7 +980,9 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     p.tokens_per_chunk = std::min(p.tokens_per_chunk, T);
     p.row_chunks = (T + p.tokens_per_chunk - 1) / p.tokens_per_chunk;
     const int64_t units = static_cast<int64_t>(Hkv) * B * p.row_chunks;
-    const int64_t want = std::max<int64_t>(1, (kAttnTargetWorkgroups + units - 1) / units);
+    // D = 256 runs one workgroup per CU (its LDS map), D = 128 two.
+    const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
+    const int64_t want = std::max<int64_t>(1, (target + units - 1) / units);
     int64_t kps = (static_cast<int64_t>(max_visible_keys) + want - 1) / want;
     kps = ((kps + 127) / 128) * 128;
     kps = std::max<int64_t>(kps, kAttnMinKeysPerSplit);
@@ -857,10 +1000,16 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
                       const int32_t* count, int32_t T, const CacheRef& c, hipStream_t stream) {
-    if (c.D != 128) { throw Unsupported("kv append: only head_dim 128 is built"); }
     dim3 grid(T, c.B, c.Hkv);
-    hipLaunchKernelGGL(kv_quant_append_kernel<128>, grid, dim3(256), 0, stream, k, v, positions,
-                       count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
+    if (c.D == 128) {
+        hipLaunchKernelGGL(kv_quant_append_kernel<128>, grid, dim3(256), 0, stream, k, v, positions,
+                           count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
+    } else if (c.D == 256) {
+        hipLaunchKernelGGL(kv_quant_append_kernel<256>, grid, dim3(256), 0, stream, k, v, positions,
+                           count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
+    } else {
+        throw Unsupported("kv append: head_dim 128 and 256 are built");
+    }
     check_launch("kv_quant_append_kernel");
 }
 
@@ -869,7 +1018,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
                              int32_t Hq, const CacheRef& c, float scale, uint32_t max_keys,
                              void* workspace, const SplitPlan& plan, void* out, bool out_f32,
                              hipStream_t stream) {
-    if (c.D != 128) { throw Unsupported("verify attention: only head_dim 128 is built"); }
+    if (c.D != 128 && c.D != 256) { throw Unsupported("verify attention: head_dim 128 and 256 are built"); }
     if (plan.nsplit > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
     if (k_new != nullptr && plan.row_chunks > 1) {
         // Several row-chunk workgroups read the new rows: write them in a launch of their own.
@@ -905,10 +1054,16 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.scale_log2 = scale * 1.4426950408889634f;
     const int rows = plan.tokens_per_chunk * plan.G;
     dim3 grid(plan.nsplit, c.Hkv, c.B * plan.row_chunks);
-    if (rows <= 16) {
-        hipLaunchKernelGGL(verify_attn_partial_kernel<1>, grid, dim3(256), 0, stream, a);
+    if (c.D == 128) {
+        if (rows <= 16) {
+            hipLaunchKernelGGL((verify_attn_partial_kernel<1, 128>), grid, dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((verify_attn_partial_kernel<2, 128>), grid, dim3(256), 0, stream, a);
+        }
+    } else if (rows <= 16) {
+        hipLaunchKernelGGL((verify_attn_partial_kernel<1, 256>), grid, dim3(256), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(verify_attn_partial_kernel<2>, grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((verify_attn_partial_kernel<2, 256>), grid, dim3(256), 0, stream, a);
     }
     check_launch("verify_attn_partial_kernel");
 
@@ -924,7 +1079,11 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.row_chunks = plan.row_chunks;
     mg.nsplit = plan.nsplit;
     mg.out_f32 = out_f32 ? 1 : 0;
-    hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    if (c.D == 128) {
+        hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    } else {
+        hipLaunchKernelGGL(verify_attn_merge_kernel<256>, dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    }
     check_launch("verify_attn_merge_kernel");
 }
 
