@@ -49,6 +49,15 @@ def attn_bytes(L: int) -> int:
     return (L + T) * BYTES_PER_TOKEN + q + out + new_kv + new_codes
 
 
+def attn_bytes_bf16(L: int) -> int:
+    """Algorithmic bytes of one layer over a BF16 cache: K and V values of all L+T visible keys,
+    Q read, output write, new K/V read and written into the cache."""
+    q = D * HQ * T * 2
+    out = D * HQ * T * 2
+    new_kv = D * HKV * T * 2 * 2
+    return (L + T) * HKV * D * 2 * 2 + q + out + 2 * new_kv
+
+
 def measured_traffic(workload: str) -> dict | None:
     """HBM bytes per launch of the attention op from the committed counter passes: FETCH_SIZE and
     WRITE_SIZE (KiB per dispatch) of its kernels, each scaled by the same counter's reading for a
@@ -74,25 +83,38 @@ def log(msg: str) -> None:
 class Layer:
     """One attention layer: its own cache planes, inputs, output and positions."""
 
-    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22, copy_from=None):
+    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22, copy_from=None, kv_bf16=False):
         import ninfer_amd as na
         from ninfer_amd import device, ops, synthetic as syn
         from ninfer_amd.device import DeviceArray, synchronize
         from ninfer_amd.kv_cache import KVCacheLayer
 
         self.L = L
-        self.cache = KVCacheLayer(max_context, HKV, D)
+        self.cache = KVCacheLayer(max_context, HKV, D, dtype=na.BF16 if kv_bf16 else na.I8)
         rng = np.random.default_rng(seed)
         per_tok = D * HKV
         chunk = max(1, gen_chunk // per_tok)
         if copy_from is not None:
             # Same history as another layer, in planes of its own (a device-to-device copy).
-            for dst, src in zip((self.cache.k, self.cache.v, self.cache.k_scale, self.cache.v_scale),
-                                (copy_from.cache.k, copy_from.cache.v, copy_from.cache.k_scale, copy_from.cache.v_scale)):
+            for dst, src in zip(self.cache._planes(), copy_from.cache._planes()):
                 device.memcpy_dtod(dst.buf, src.buf, dst.nbytes)
             synchronize()
+        elif kv_bf16:
+            # History K/V stored as BF16: a generated block of N(0,1) values (optionally 1% outliers
+            # at +-20) repeated over the L rows of every head.
+            P = self.cache.padded_context
+            for arr in (self.cache.k, self.cache.v):
+                x = rng.standard_normal(gen_chunk, dtype=np.float32)
+                if outliers:
+                    sel = rng.random(gen_chunk) < 0.01
+                    x[sel] = np.where(rng.random(int(sel.sum())) < 0.5, -20.0, 20.0).astype(np.float32)
+                host = np.zeros((HKV, P, D), dtype=np.uint16)
+                host[:, :L] = np.resize(syn.f32_to_bf16_bits(x), HKV * L * D).reshape(HKV, L, D)
+                arr.upload(host)
+                del host
+            synchronize()
         # History K/V: BF16 N(0,1) (optionally 1% outliers at +-20), quantized on the GPU in chunks.
-        for start in range(0, L if copy_from is None else 0, chunk):
+        for start in range(0, L if copy_from is None and not kv_bf16 else 0, chunk):
             n = min(chunk, L - start)
             kv = []
             for _ in range(2):
@@ -278,7 +300,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "sampler", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "copy"], default=None,
                     help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
                          "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
@@ -334,6 +356,29 @@ def main():
                             target_us=attn_bytes(L3) / (0.7 * HBM_PEAK_GBS * 1e9) * 1e6)
         log(f"C3: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
         del c3_layers, first, g3
+        device.synchronize()
+
+    # ---- C3 over a BF16 cache (the reference's other cache format), same shape ------------------
+    if (args.only in (None, "c3_bf16")) and not args.skip_long:
+        L3 = 260096
+        t0 = time.perf_counter()
+        first = Layer(L3, L3 + T, seed=5, outliers=True, kv_bf16=True)
+        layers_b = [first] + [Layer(L3, L3 + T, seed=6 + i, outliers=True, copy_from=first, kv_bf16=True)
+                              for i in range(C3_LAYERS - 1)]
+        log(f"C3 BF16: {C3_LAYERS} layers generated in {time.perf_counter() - t0:.1f}s")
+        ws3 = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L3 + T))
+        g3 = capture(stream, lambda: [ly.launch(ws3, stream) for ly in layers_b])
+        ms3, p95_3, _ = time_graph(g3, stream, max(args.steps, 20), args.warmup)
+        ms3 /= C3_LAYERS
+        p95_3 /= C3_LAYERS
+        if args.only:
+            log(f"C3 BF16 {ms3 * 1e3:.1f} us/layer")
+            return
+        gbs3 = attn_bytes_bf16(L3) / (ms3 * 1e-3) / 1e9
+        result["c3_bf16"] = dict(us_per_layer=ms3 * 1e3, us_per_layer_p95=p95_3 * 1e3, gbs=gbs3,
+                                 bytes_per_layer=attn_bytes_bf16(L3), frac_of_peak=gbs3 / HBM_PEAK_GBS)
+        log(f"C3 BF16: {ms3 * 1e3:.1f} us/layer, {gbs3:.0f} GB/s ({gbs3 / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+        del layers_b, first, g3
         device.synchronize()
 
     # ---- C2: 64 layers at context 7680 + greedy acceptance --------------------------------------
@@ -444,6 +489,11 @@ def main():
     if "c3" in result:
         line["long_context"] = {"workload": "C3: context 260096, 1% outliers +-20, one layer",
                                 **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3"].items()}}
+    if "c3_bf16" in result:
+        line["long_context_bf16"] = {
+            "workload": "C3 shape over a BF16 KV cache: context 260096, 1% outliers +-20, one layer "
+                        "(new rows copied into the cache by their own launch, then attention)",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3_bf16"].items()}}
     if "sampler" in result:
         line["sampler"] = {"workload": "stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95: Mode R (top-20 cap) "
                                        "and Mode F (full vocabulary, draft logits correlated 0.9)",

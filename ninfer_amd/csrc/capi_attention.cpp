@@ -73,6 +73,8 @@ CacheRef validate_cache(const nmi_kv_layer_view* cache, int32_t kv_heads, int32_
     if (cache->dtype == NMI_BF16) {
         require(cache->k_scale.data == nullptr && cache->v_scale.data == nullptr, op,
                 "BF16 KV cache must not have scales");
+        r.kb = static_cast<uint16_t*>(cache->k.data);
+        r.vb = static_cast<uint16_t*>(cache->v.data);
         return r;
     }
     const int32_t groups = D / kQuantGroup;
@@ -152,7 +154,6 @@ void validate_new_kv(const nmi_tensor* k, const nmi_tensor* v, int32_t D, int32_
 }
 
 void require_built(const CacheRef& c, const std::string& op) {
-    if (c.kc == nullptr) { throw Unsupported(op + ": BF16 KV cache attention is not built"); }
     if (c.D != 128 && c.D != 256) { throw Unsupported(op + ": head_dim 128 and 256 kernels are built"); }
 }
 
@@ -202,8 +203,9 @@ extern "C" {
 const char* nmi_last_error(void) { return g_last_error.c_str(); }
 
 const char* nmi_build_info(void) {
-    return "ninfer_amd gfx950: verify_attn_partial<{1,2},{128,256}> fp16-MFMA 16x16x32, "
-           "verify_attn_merge, kv_quant_append, argmax, speculative accept (greedy, top-20 "
+    return "ninfer_amd gfx950: verify_attn_partial<{1,2},{128,256}> fp16-MFMA 16x16x32 (INT8-G64 KV), "
+           "verify_attn_partial_bf16<{1,2},{128,256}> bf16-MFMA 16x16x32 (BF16 KV), "
+           "verify_attn_merge, kv_quant_append, bf16_kv_append, argmax, speculative accept (greedy, top-20 "
            "stochastic, general fixed-point), kv commit/rollback/compaction";
 }
 

@@ -11,6 +11,8 @@ struct CacheRef {
     int8_t* vc = nullptr;
     uint16_t* ks = nullptr; // FP16 bits
     uint16_t* vs = nullptr;
+    uint16_t* kb = nullptr; // BF16 cache planes (kc/vc/ks/vs stay null)
+    uint16_t* vb = nullptr;
     int64_t code_seq = 0;  // code elements between sequences
     int64_t scale_seq = 0; // scale elements between sequences
     int32_t P = 0;         // padded context

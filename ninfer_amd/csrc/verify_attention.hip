@@ -88,6 +88,7 @@ __device__ __forceinline__ void wait_chunk(bool next_in_flight) {
 }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
 struct AttnArgs {
     const uint16_t* q;
@@ -99,6 +100,8 @@ struct AttnArgs {
     int8_t* vc;
     uint16_t* ks;
     uint16_t* vs;
+    const uint16_t* kb; // BF16 cache planes (BF16 kernel only)
+    const uint16_t* vb;
     float* part_o;  // [unit][nsplit][32][D]
     float* part_ml; // [unit][nsplit][32][2]
     int64_t code_seq;
@@ -314,10 +317,11 @@ __device__ __forceinline__ void qk_chunk(const ChunkRegs<D>& r, const RowState<N
 }
 
 // Online softmax of one chunk; the S^T accumulator layout is the B-operand layout of P^T. `masked`
-// is uniform across the wave.
-template <int NT, int D>
-__device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, bool masked, RowState<NT, D>& s,
-                                              const KeyRange& kr, int g, h8 (&pop)[NT]) {
+// is uniform across the wave. State is anything with m, rowmul, rowthr, nmask, O[NT][D/16] and
+// l; the probabilities come out as FP32 exp2(score * rowmul - m * rowmul + kPOffset).
+template <int NT, int D, typename State>
+__device__ __forceinline__ void softmax_probs(const f4 (&sacc)[2][NT], int c0, bool masked, State& s,
+                                              const KeyRange& kr, int g, float (&p)[NT][8]) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         float sv[8];
@@ -350,9 +354,19 @@ __device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, b
         }
         const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pop[nt][i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)));
-        }
+        for (int i = 0; i < 8; ++i) { p[nt][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)); }
+    }
+}
+
+template <int NT, int D>
+__device__ __forceinline__ void softmax_chunk(const f4 (&sacc)[2][NT], int c0, bool masked, RowState<NT, D>& s,
+                                              const KeyRange& kr, int g, h8 (&pop)[NT]) {
+    float p[NT][8];
+    softmax_probs<NT, D>(sacc, c0, masked, s, kr, g, p);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { pop[nt][i] = static_cast<_Float16>(p[nt][i]); }
     }
 }
 
@@ -494,6 +508,61 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
     for (int i = 0; i < GQ; ++i) {
         st[krow + 16 * ((4 * i + (lane >> 4)) ^ (u % G::PIECES))] = static_cast<char>(code[i]);
         st[G::kStageV + u * D + 64 * i + lane] = static_cast<char>(code[GQ + i]);
+    }
+}
+
+// Merge the four waves' (m, l, O) through LDS (reusing the staging area) and write the
+// workgroup's partial: out_o [32][D] (rows < R) and out_ml [32][2] (log2-domain max, row sum).
+template <int NT, int D, typename State>
+__device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
+                                              float* out_o, float* out_ml) {
+    constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
+    float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
+    float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
+    float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int r = 16 * nt + c;
+        if (g == 0) {
+            // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
+            sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
+            sm_l[wave * 32 + r] = s.l[nt][0];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // O^T tile t row (4g + e) is dim (D/16)(4g + e) + t: D/16 consecutive dims per (lane, e).
+            float* dst = sm_o + (wave * 32 + r) * kRowStride + (D / 16) * (4 * g + e);
+#pragma unroll
+            for (int q4 = 0; q4 < D / 64; ++q4) {
+                *reinterpret_cast<f4*>(dst + 4 * q4) =
+                    f4{s.O[nt][4 * q4][e], s.O[nt][4 * q4 + 1][e], s.O[nt][4 * q4 + 2][e], s.O[nt][4 * q4 + 3][e]};
+            }
+        }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < R * (D / 4); idx += blockDim.x) {
+        const int r = idx / (D / 4);
+        const int d4 = 4 * (idx - r * (D / 4));
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
+        f4 o = {0.f, 0.f, 0.f, 0.f};
+        float lsum = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float mw = sm_m[w * 32 + r];
+                if (mw == -INFINITY) { continue; }
+                const float wgt = __builtin_amdgcn_exp2f(mw - M);
+                o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
+                lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
+            }
+        }
+        *reinterpret_cast<f4*>(out_o + r * D + d4) = o;
+        if (d4 == 0) {
+            out_ml[2 * r] = M;
+            out_ml[2 * r + 1] = lsum;
+        }
     }
 }
 
@@ -767,55 +836,369 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
     // ---- merge the four waves through LDS (reusing the staging ring), then write the partial.
     __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
     __syncthreads();
-    constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
-    static_assert(kWaves * 32 * (kRowStride + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
-    float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
-    float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
-    float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
+    static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
+    write_partial<NT, D>(s, smem, R, wave, c, g, out_o, out_ml);
+}
+
+
+// ---- BF16 KV cache -------------------------------------------------------------------------------
+//
+// Same split-K structure. A stage holds 32 keys of BF16 K (row r's 16-byte piece p at slot
+// p ^ (r % PB)) and V (natural order), no scales; QK^T and PV run on v_mfma_f32_16x16x32_bf16 with
+// the cache values and BF16 Q exactly as stored. P goes to the MFMA as two BF16 terms
+// (hi = BF16(p), lo = BF16(p - hi)), so the product keeps ~16 significant bits of P. New rows are
+// copied into the cache by a launch of their own before this kernel (BF16 caches have no codec).
+template <int D>
+struct GeoB {
+    static constexpr int PB = D / 8;                // 16-byte pieces of a BF16 row
+    static constexpr int kStageK = 0;
+    static constexpr int kStageV = 64 * D;          // 32 rows x 2D B
+    static constexpr int kStageBytes = 128 * D;     // 16 KB / 32 KB
+    static constexpr int STAGES = D == 128 ? 2 : 1; // stages per wave (LDS budget)
+    static constexpr int kDmaPerChunk = D / 8;      // 1 KB DMAs: D/16 per plane
+    static constexpr int kRingBytes = kWaves * STAGES * kStageBytes;
+    static constexpr int kQTile = kRingBytes;       // Q tile: 32 rows x 2D B
+    static constexpr int kPosLds = kQTile + 64 * D;
+    static constexpr int kSmemBytes = kPosLds + 128; // D=128: 139,392 B; D=256: 147,584 B
+};
+
+// Lane -> (row lane / PB, slot lane % PB) of each 1 KB DMA (512 / D rows); K slot s of row r holds
+// piece s ^ (r % PB), so the K source offset depends on the DMA index (one XOR per DMA).
+struct DmaLanesB {
+    int row; // row within one DMA
+    int slot;
+    int v;
+};
+
+template <int D>
+__device__ __forceinline__ DmaLanesB make_dma_lanes_b(int lane) {
+    constexpr int PB = GeoB<D>::PB;
+    DmaLanesB dl;
+    dl.row = lane / PB;
+    dl.slot = lane % PB;
+    dl.v = dl.row * 2 * D + 16 * dl.slot;
+    return dl;
+}
+
+// K rows of chunk c0 into the stage's K plane (D/16 DMAs).
+template <int D>
+__device__ __forceinline__ void issue_k_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc_t rk, const DmaLanesB& dl, int c0) {
+    using G = GeoB<D>;
+    constexpr int ROWS = 512 / D; // rows per 1 KB DMA
+    const int so = c0 * 2 * D;
+#pragma unroll
+    for (int r = 0; r < D / 16; ++r) {
+        const int koff = dl.row * 2 * D + 16 * (dl.slot ^ ((ROWS * r + dl.row) % G::PB));
+        dma16(rk, st + G::kStageK + r * 1024, koff, so + r * 1024);
+    }
+}
+
+// V rows of chunk c0 into the stage's V plane (D/16 DMAs).
+template <int D>
+__device__ __forceinline__ void issue_v_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc_t rv, const DmaLanesB& dl, int c0) {
+    using G = GeoB<D>;
+    const int so = c0 * 2 * D;
+#pragma unroll
+    for (int r = 0; r < D / 16; ++r) { dma16(rv, st + G::kStageV + r * 1024, dl.v, so + r * 1024); }
+}
+
+template <int D>
+__device__ __forceinline__ void issue_chunk_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                              const DmaLanesB& dl, int c0) {
+    issue_k_b<D>(st, rk, dl, c0);
+    issue_v_b<D>(st, rv, dl, c0);
+}
+
+template <int D>
+struct ChunkRegsB {
+    i4 kb[2][D / 32];   // A operand of S^T: key 16kt + c, dims 32ks + 8g .. +7
+    i4 vr[8][D / 128];  // the lane's dims (D/16)c .. of V rows 4g + j and 16 + 4g + j
+};
+
+template <int D>
+__device__ __forceinline__ void read_k_b(const NMI_AS3 char* st, ChunkRegsB<D>& r, int c, int g) {
+    using G = GeoB<D>;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+            const int row = 16 * kt + c;
+            const int slot = (4 * ks + g) ^ (row % G::PB);
+            r.kb[kt][ks] = *(const NMI_AS3 i4*)(st + G::kStageK + row * 2 * D + 16 * slot);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void read_v_b(const NMI_AS3 char* st, ChunkRegsB<D>& r, int c, int g) {
+    using G = GeoB<D>;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
+#pragma unroll
+        for (int h = 0; h < D / 128; ++h) {
+            r.vr[j][h] = *(const NMI_AS3 i4*)(st + G::kStageV + row * 2 * D + (D / 8) * c + 16 * h);
+        }
+    }
+}
+
+// Q stays in LDS (the B operand of Q^T, rows 16nt + c, dims 32ks + 8g + e, is read per chunk).
+template <int NT, int D>
+struct RowStateB {
+    float rowmul[NT];   // softmax scale * log2(e)
+    float rowthr[NT];
+    uint32_t nmask[NT];
+    float m[NT];
+    f4 O[NT][D / 16];   // O^T tiles: tile t row 4g+e is dim (D/16)(4g+e) + t
+    f4 l[NT];
+};
+
+// Q^T operand for k-step ks of tile nt from the LDS Q tile (rows >= R read as zero).
+template <int D>
+__device__ __forceinline__ bf8 q_operand_b(const NMI_AS3 char* qtile, int nt, int ks, int c, int g, int R) {
+    const int r = 16 * nt + c;
+    const int piece = 4 * ks + g;
+    const i4 v = *(const NMI_AS3 i4*)(qtile + (r & 31) * (2 * D) + 16 * ((piece + r) & (D / 8 - 1)));
+    return __builtin_bit_cast(bf8, r < R ? v : i4{0, 0, 0, 0});
+}
+
+template <int NT, int D>
+__device__ __forceinline__ void qk_chunk_b(const ChunkRegsB<D>& r, const NMI_AS3 char* qtile, int c, int g, int R,
+                                           f4 (&sacc)[2][NT]) {
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+        bf8 qv[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) { qv[nt] = q_operand_b<D>(qtile, nt, ks, c, g, R); }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const bf8 a = __builtin_bit_cast(bf8, r.kb[kt][ks]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const f4 acc = ks == 0 ? f4{0.f, 0.f, 0.f, 0.f} : sacc[kt][nt];
+                sacc[kt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qv[nt], acc, 0, 0, 0);
+            }
+        }
+    }
+}
+
+// BF16 element t of the lane's slice of a V row.
+template <int D>
+__device__ __forceinline__ uint32_t v_word_b(const i4 (&row)[D / 128], int t) {
+    return static_cast<uint32_t>(row[t >> 3][(t >> 1) & 3]);
+}
+
+// O^T += V^T (P_hi + P_lo)^T and l += ones x (P_hi + P_lo)^T. V values of keys at or past key_end
+// in a masked chunk are replaced by zero (those rows may hold anything).
+template <int NT, int D>
+__device__ __forceinline__ void pv_chunk_b(const float (&p)[NT][8], const ChunkRegsB<D>& r, int c0, bool masked,
+                                           RowStateB<NT, D>& s, const KeyRange& kr, int g) {
+    bf8 phi[NT], plo[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const __bf16 hi = static_cast<__bf16>(p[nt][i]);
+            phi[nt][i] = hi;
+            plo[nt][i] = static_cast<__bf16>(p[nt][i] - static_cast<float>(hi));
+        }
+    }
+    uint32_t keep = 0xffu; // bit j: key j of the lane's 8 is below key_end
+    if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+            keep &= key < kr.key_end ? 0xffu : ~(1u << j);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+        uint32_t w[4];
+        const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = (keep >> (2 * q)) & 1u ? v_word_b<D>(r.vr[2 * q], t) : 0u;
+            const uint32_t hi = (keep >> (2 * q + 1)) & 1u ? v_word_b<D>(r.vr[2 * q + 1], t) : 0u;
+            w[q] = __builtin_amdgcn_perm(hi, lo, sel);
+        }
+        const bf8 va = __builtin_bit_cast(bf8, w);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            s.O[nt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, phi[nt], s.O[nt][t], 0, 0, 0);
+            s.O[nt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, plo[nt], s.O[nt][t], 0, 0, 0);
+        }
+    }
+    bf8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { ones[i] = static_cast<__bf16>(1.0f); }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, phi[nt], s.l[nt], 0, 0, 0);
+        s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, plo[nt], s.l[nt], 0, 0, 0);
+    }
+}
+
+template <int NT, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void verify_attn_partial_bf16_kernel(AttnArgs a) {
+    using GB = GeoB<D>;
+    __shared__ __attribute__((aligned(16))) char smem[GB::kSmemBytes];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int split = blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z / a.row_chunks;
+    const int rc = blockIdx.z - b * a.row_chunks;
+    const int k0 = split * a.kps;
+
+    const int64_t head = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
+    const __amdgpu_buffer_rsrc_t rk = raw_buffer(a.kb + head, static_cast<int64_t>(a.P) * D * 2);
+    const __amdgpu_buffer_rsrc_t rv = raw_buffer(a.vb + head, static_cast<int64_t>(a.P) * D * 2);
+    const DmaLanesB dl = make_dma_lanes_b<D>(lane);
+    NMI_AS3 char* ring = (NMI_AS3 char*)smem + wave * GB::STAGES * GB::kStageBytes;
+
+    // Q tile (rows r = tl * G + gi, 2D bytes each, piece p at slot (p + r) % QP) and positions by
+    // LDS DMA before the chunk DMAs, as in the INT8 kernel.
+    const int t0 = rc * a.tokens_per_chunk;
+    const int Tc = min(a.tokens_per_chunk, a.T - t0);
+    const int R = Tc * a.G;
+    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + GB::kQTile;
+    NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GB::kPosLds);
+    const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
+    if (wave == 0) {
+        if (lane < a.T) { __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)(pos + lane), (NMI_AS3 void*)pos_lds, 4, 0, 0); }
+        constexpr int QP = D / 8;
+        constexpr int RPD = 64 / QP;
+#pragma unroll 1
+        for (int k = 0; RPD * k < R; ++k) {
+            const int row = RPD * k + lane / QP;
+            if (row < R) {
+                const int tl = row / a.G;
+                const int gi = row - tl * a.G;
+                const int piece = ((lane % QP) - row) & (QP - 1);
+                const uint16_t* src = a.q + static_cast<int64_t>(D) * (h * a.G + gi + static_cast<int64_t>(a.Hq) * (t0 + tl + static_cast<int64_t>(a.T) * b)) + 8 * piece;
+                __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(qtile + k * 1024), 16, 0, 0);
+            }
+        }
+    }
+    const int first = k0 + kChunk * wave;
+    if (first + kChunk <= a.P) { issue_chunk_b<D>(ring, rk, rv, dl, first); }
+    if (GB::STAGES == 2 && first + kStride + kChunk <= a.P) { issue_chunk_b<D>(ring + GB::kStageBytes, rk, rv, dl, first + kStride); }
+    if (wave == 0) {
+        if (GB::STAGES == 2 && first + kStride + kChunk <= a.P) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * GB::kDmaPerChunk));
+        } else if (first + kChunk <= a.P) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(GB::kDmaPerChunk));
+        } else {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        }
+    }
+    __builtin_amdgcn_s_barrier();
+
+    // ---- per-row state (Q is used as stored: BF16 is exact for the BF16 MFMA).
+    RowStateB<NT, D> s;
+    const int32_t* par = a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int r = 16 * nt + c;
-        if (g == 0) {
-            // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
-            sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
-            sm_l[wave * 32 + r] = s.l[nt][0];
+        const bool valid = r < R;
+        const int t = t0 + (valid ? r / a.G : 0);
+        s.rowmul[nt] = a.scale_log2;
+        s.rowthr[nt] = kLazyTau / s.rowmul[nt];
+        s.nmask[nt] = valid ? new_key_mask(par, t) : 0u;
+        s.m[nt] = -INFINITY;
+        s.l[nt] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t8 = 0; t8 < D / 16; ++t8) { s.O[nt][t8] = f4{0.f, 0.f, 0.f, 0.f}; }
+    }
+
+    const int pos_first = __builtin_amdgcn_readfirstlane(pos_lds[0]);
+    const int pos_last = __builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]);
+    const int window = min(pos_last + 1, a.max_keys);
+    const int L = max(0, min(pos_first, window));
+    const int hend = min(k0 + a.kps, window); // the new rows are already in the cache
+    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
+    const int64_t pidx = unit * a.nsplit + split;
+    float* out_o = a.part_o + pidx * (32 * D);
+    float* out_ml = a.part_ml + pidx * 64;
+    if (k0 >= hend) {
+        __builtin_amdgcn_s_waitcnt(0);
+        if (threadIdx.x < 32) {
+            out_ml[2 * threadIdx.x] = -INFINITY;
+            out_ml[2 * threadIdx.x + 1] = 0.0f;
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            // O^T tile t row (4g + e) is dim (D/16)(4g + e) + t: D/16 consecutive dims per (lane, e).
-            float* dst = sm_o + (wave * 32 + r) * kRowStride + (D / 16) * (4 * g + e);
-#pragma unroll
-            for (int q4 = 0; q4 < D / 64; ++q4) {
-                *reinterpret_cast<f4*>(dst + 4 * q4) =
-                    f4{s.O[nt][4 * q4][e], s.O[nt][4 * q4 + 1][e], s.O[nt][4 * q4 + 2][e], s.O[nt][4 * q4 + 3][e]};
+        return;
+    }
+
+    const KeyRange hk{min(L, hend), L, hend};
+    if constexpr (GB::STAGES == 2) {
+        // ---- chunks: read one into registers, put the DMA of the chunk two steps ahead into its
+        // stage, then compute it.
+        int stage = 0;
+#pragma unroll 1
+        for (int cj = first; cj < hend; cj += kStride) {
+            NMI_AS3 char* st = ring + stage * GB::kStageBytes;
+            if (cj + kStride < hend) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(GB::kDmaPerChunk));
+            } else {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
             }
+            ChunkRegsB<D> r;
+            read_k_b<D>(st, r, c, g);
+            read_v_b<D>(st, r, c, g);
+            const int cn = cj + 2 * kStride;
+            if (cn < hend) {
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk cj sits in registers: reuse its stage
+                issue_chunk_b<D>(st, rk, rv, dl, cn);
+            }
+            f4 sacc[2][NT];
+            qk_chunk_b<NT, D>(r, qtile, c, g, R, sacc);
+            float p[NT][8];
+            const bool masked = cj + kChunk > hk.vis_all;
+            softmax_probs<NT, D>(sacc, cj, masked, s, hk, g, p);
+            pv_chunk_b<NT, D>(p, r, cj, masked, s, hk, g);
+            stage ^= 1;
+        }
+    } else {
+        // ---- one stage per wave: the K plane is refilled with the next chunk's keys as soon as
+        // they sit in registers, the V plane after the softmax, so K and V registers are never
+        // live together. DMAs complete in issue order (K(cj), V(cj), K(cn), V(cn)).
+        NMI_AS3 char* st = ring;
+#pragma unroll 1
+        for (int cj = first; cj < hend; cj += kStride) {
+            const int cn = cj + kStride;
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(GB::kDmaPerChunk / 2)); // K(cj) landed
+            ChunkRegsB<D> r;
+            read_k_b<D>(st, r, c, g);
+            if (cn < hend) {
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                issue_k_b<D>(st, rk, dl, cn);
+            }
+            f4 sacc[2][NT];
+            qk_chunk_b<NT, D>(r, qtile, c, g, R, sacc);
+            float p[NT][8];
+            const bool masked = cj + kChunk > hk.vis_all;
+            softmax_probs<NT, D>(sacc, cj, masked, s, hk, g, p);
+            if (cn < hend) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(GB::kDmaPerChunk / 2)); // V(cj) landed
+            } else {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            }
+            read_v_b<D>(st, r, c, g);
+            if (cn < hend) {
+                __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+                issue_v_b<D>(st, rv, dl, cn);
+            }
+            pv_chunk_b<NT, D>(p, r, cj, masked, s, hk, g);
         }
     }
+
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int idx = threadIdx.x; idx < R * (D / 4); idx += blockDim.x) {
-        const int r = idx / (D / 4);
-        const int d4 = 4 * (idx - r * (D / 4));
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
-        f4 o = {0.f, 0.f, 0.f, 0.f};
-        float lsum = 0.0f;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const float mw = sm_m[w * 32 + r];
-                if (mw == -INFINITY) { continue; }
-                const float wgt = __builtin_amdgcn_exp2f(mw - M);
-                o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
-                lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
-            }
-        }
-        *reinterpret_cast<f4*>(out_o + r * D + d4) = o;
-        if (d4 == 0) {
-            out_ml[2 * r] = M;
-            out_ml[2 * r + 1] = lsum;
-        }
-    }
+    static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GB::kSmemBytes, "wave merge exceeds the LDS map");
+    write_partial<NT, D>(s, smem, R, wave, c, g, out_o, out_ml);
 }
 
 struct MergeArgs {
@@ -970,6 +1353,25 @@ __global__ __launch_bounds__(256) void kv_quant_append_kernel(const uint16_t* k,
     }
 }
 
+// BF16 cache append (A2, and A1 on a BF16 cache): column t of sequence b is copied bit for bit into
+// row positions[t] (reference gqa_kv_append on a BF16 cache). Block (t, b, h).
+__global__ __launch_bounds__(64) void bf16_kv_append_kernel(const uint16_t* k, const uint16_t* v, const int32_t* positions,
+                                                            const int32_t* count, int32_t T, int32_t Hkv, int32_t P,
+                                                            int32_t D, uint16_t* kb, uint16_t* vb, int64_t seq) {
+    const int t = blockIdx.x;
+    const int b = blockIdx.y;
+    const int h = blockIdx.z;
+    if (count != nullptr && t >= count[b]) { return; }
+    const int pos = positions[static_cast<int64_t>(b) * T + t];
+    if (pos < 0 || pos >= P) { return; }
+    const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(Hkv) * (t + static_cast<int64_t>(T) * b));
+    const int64_t dst = static_cast<int64_t>(b) * seq + static_cast<int64_t>(D) * (pos + static_cast<int64_t>(P) * h);
+    for (int i = threadIdx.x; i < D / 8; i += blockDim.x) {
+        *reinterpret_cast<i4*>(kb + dst + 8 * i) = *reinterpret_cast<const i4*>(k + src + 8 * i);
+        *reinterpret_cast<i4*>(vb + dst + 8 * i) = *reinterpret_cast<const i4*>(v + src + 8 * i);
+    }
+}
+
 } // namespace
 
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
@@ -1001,6 +1403,12 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
                       const int32_t* count, int32_t T, const CacheRef& c, hipStream_t stream) {
     dim3 grid(T, c.B, c.Hkv);
+    if (c.kb != nullptr) {
+        hipLaunchKernelGGL(bf16_kv_append_kernel, grid, dim3(64), 0, stream, k, v, positions, count, T, c.Hkv, c.P, c.D,
+                           c.kb, c.vb, c.code_seq);
+        check_launch("bf16_kv_append_kernel");
+        return;
+    }
     if (c.D == 128) {
         hipLaunchKernelGGL(kv_quant_append_kernel<128>, grid, dim3(256), 0, stream, k, v, positions,
                            count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
@@ -1020,8 +1428,9 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
                              hipStream_t stream) {
     if (c.D != 128 && c.D != 256) { throw Unsupported("verify attention: head_dim 128 and 256 are built"); }
     if (plan.nsplit > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
-    if (k_new != nullptr && plan.row_chunks > 1) {
-        // Several row-chunk workgroups read the new rows: write them in a launch of their own.
+    if (k_new != nullptr && (plan.row_chunks > 1 || c.kb != nullptr)) {
+        // Several row-chunk workgroups read the new rows, or a BF16 cache (no in-kernel codec):
+        // write them in a launch of their own.
         launch_kv_append(k_new, v_new, positions, nullptr, T, c, stream);
         k_new = nullptr;
         v_new = nullptr;
@@ -1035,6 +1444,8 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.parents = parents;
     a.kc = c.kc;
     a.vc = c.vc;
+    a.kb = c.kb;
+    a.vb = c.vb;
     a.ks = c.ks;
     a.vs = c.vs;
     a.part_o = reinterpret_cast<float*>(ws + plan.part_o_offset);
@@ -1054,7 +1465,19 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.scale_log2 = scale * 1.4426950408889634f;
     const int rows = plan.tokens_per_chunk * plan.G;
     dim3 grid(plan.nsplit, c.Hkv, c.B * plan.row_chunks);
-    if (c.D == 128) {
+    if (c.kb != nullptr) {
+        if (c.D == 128) {
+            if (rows <= 16) {
+                hipLaunchKernelGGL((verify_attn_partial_bf16_kernel<1, 128>), grid, dim3(256), 0, stream, a);
+            } else {
+                hipLaunchKernelGGL((verify_attn_partial_bf16_kernel<2, 128>), grid, dim3(256), 0, stream, a);
+            }
+        } else if (rows <= 16) {
+            hipLaunchKernelGGL((verify_attn_partial_bf16_kernel<1, 256>), grid, dim3(256), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((verify_attn_partial_bf16_kernel<2, 256>), grid, dim3(256), 0, stream, a);
+        }
+    } else if (c.D == 128) {
         if (rows <= 16) {
             hipLaunchKernelGGL((verify_attn_partial_kernel<1, 128>), grid, dim3(256), 0, stream, a);
         } else {

@@ -68,6 +68,11 @@ def normal_bf16(seed: int, n: int, std: float = 1.0) -> np.ndarray:
     return f32_to_bf16_bits((normals(seed, n) * std).astype(np.float32))
 
 
+def uniform_bf16(seed: int, n: int, lo: float, hi: float) -> np.ndarray:
+    """n values uniform in [lo, hi), rounded to BF16."""
+    return f32_to_bf16_bits((lo + (hi - lo) * uniforms(seed, n)).astype(np.float32))
+
+
 def normal_bf16_with_outliers(seed: int, n: int, frac: float = 0.01, value: float = 20.0) -> np.ndarray:
     """N(0,1) with a seeded `frac` of entries replaced by +-value (long-context config)."""
     x = normals(seed, n).astype(np.float32)

@@ -220,17 +220,17 @@ void orc_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* position
 
 // FP64 ideal attention; restates cpu_gqa_decode/cpu_gqa_cached (tests/ops/test_gqa_attention.cpp:
 // 228-282) with the contract of include/ninfer/ops/gqa_attention.h:52-66 (BF16 Q, FP32-decoded
-// INT8-G64 cache values, score dot products, stable softmax and value reduction in FP64). The
-// visible key set generalizes the reference's `key <= positions[t]`
+// cache values, score dot products, stable softmax and value reduction in FP64). The visible key
+// set generalizes the reference's `key <= positions[t]`
 // (src/ops/kernel/gqa_attention_decode_i8.cuh:379-390) to an ancestor mask when `parents` is given.
-void orc_attention(const uint16_t* q, const int8_t* k_codes, const int8_t* v_codes,
-                   const uint16_t* k_scales, const uint16_t* v_scales, const int32_t* positions,
-                   const int32_t* parents, int32_t T, int32_t B, int32_t Hq, int32_t Hkv,
-                   int32_t D, int32_t padded_context, double scale, double* out, int32_t threads) {
+// `decode(b, h, j, kd, vd)` writes row j of head h of sequence b, in FP64, to kd[0..D) / vd[0..D).
+} // extern "C"
+namespace {
+template <class Decode>
+void attention_core(const uint16_t* q, const int32_t* positions, const int32_t* parents, int32_t T,
+                    int32_t B, int32_t Hq, int32_t Hkv, int32_t D, double scale, double* out,
+                    int32_t threads, const Decode& decode) {
     const int32_t G = Hq / Hkv;
-    const int32_t groups = D / kQuantGroup;
-    const size_t code_seq = static_cast<size_t>(D) * padded_context * Hkv;
-    const size_t scale_seq = static_cast<size_t>(groups) * padded_context * Hkv;
 
     auto work = [&](int32_t b, int32_t h) {
         const int32_t* pos = positions + static_cast<size_t>(b) * T;
@@ -256,20 +256,7 @@ void orc_attention(const uint16_t* q, const int8_t* k_codes, const int8_t* v_cod
         for (int32_t u = 0; u < T; ++u) { rows.push_back(pos[u]); }
         const size_t n = rows.size();
         std::vector<double> kd(n * D), vd(n * D);
-        for (size_t r = 0; r < n; ++r) {
-            const int32_t j = rows[r];
-            for (int32_t g = 0; g < groups; ++g) {
-                const size_t so = b * scale_seq + g + static_cast<size_t>(groups) * (j + static_cast<size_t>(padded_context) * h);
-                const float ks = orc_f16_bits_to_f32(k_scales[so]);
-                const float vs = orc_f16_bits_to_f32(v_scales[so]);
-                for (int32_t i = 0; i < kQuantGroup; ++i) {
-                    const int32_t d = g * kQuantGroup + i;
-                    const size_t co = b * code_seq + d + static_cast<size_t>(D) * (j + static_cast<size_t>(padded_context) * h);
-                    kd[r * D + d] = static_cast<double>(static_cast<float>(k_codes[co]) * ks);
-                    vd[r * D + d] = static_cast<double>(static_cast<float>(v_codes[co]) * vs);
-                }
-            }
-        }
+        for (size_t r = 0; r < n; ++r) { decode(b, h, rows[r], &kd[r * D], &vd[r * D]); }
         std::vector<double> sc(n), pr(n);
         for (int32_t t = 0; t < T; ++t) {
             for (int32_t gi = 0; gi < G; ++gi) {
@@ -316,6 +303,50 @@ void orc_attention(const uint16_t* q, const int8_t* k_codes, const int8_t* v_cod
         });
     }
     for (auto& th : pool) { th.join(); }
+}
+
+} // namespace
+extern "C" {
+
+// INT8-G64 cache: value = FP32(code) * FP32(scale) (src/ops/kernel/gqa_attention_kv_quant.cuh:63-78).
+void orc_attention(const uint16_t* q, const int8_t* k_codes, const int8_t* v_codes,
+                   const uint16_t* k_scales, const uint16_t* v_scales, const int32_t* positions,
+                   const int32_t* parents, int32_t T, int32_t B, int32_t Hq, int32_t Hkv,
+                   int32_t D, int32_t padded_context, double scale, double* out, int32_t threads) {
+    const int32_t groups = D / kQuantGroup;
+    const size_t code_seq = static_cast<size_t>(D) * padded_context * Hkv;
+    const size_t scale_seq = static_cast<size_t>(groups) * padded_context * Hkv;
+    attention_core(q, positions, parents, T, B, Hq, Hkv, D, scale, out, threads,
+                   [&](int32_t b, int32_t h, int32_t j, double* kd, double* vd) {
+        for (int32_t g = 0; g < groups; ++g) {
+            const size_t so = b * scale_seq + g + static_cast<size_t>(groups) * (j + static_cast<size_t>(padded_context) * h);
+            const float ks = orc_f16_bits_to_f32(k_scales[so]);
+            const float vs = orc_f16_bits_to_f32(v_scales[so]);
+            for (int32_t i = 0; i < kQuantGroup; ++i) {
+                const int32_t d = g * kQuantGroup + i;
+                const size_t co = b * code_seq + d + static_cast<size_t>(D) * (j + static_cast<size_t>(padded_context) * h);
+                kd[d] = static_cast<double>(static_cast<float>(k_codes[co]) * ks);
+                vd[d] = static_cast<double>(static_cast<float>(v_codes[co]) * vs);
+            }
+        }
+    });
+}
+
+// BF16 cache: the stored values themselves (tests/ops/test_gqa_attention.cpp:768-844 feeds the same
+// FP64 oracle the BF16-rounded cache rows).
+void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                        const int32_t* positions, const int32_t* parents, int32_t T, int32_t B,
+                        int32_t Hq, int32_t Hkv, int32_t D, int32_t padded_context, double scale,
+                        double* out, int32_t threads) {
+    const size_t seq = static_cast<size_t>(D) * padded_context * Hkv;
+    attention_core(q, positions, parents, T, B, Hq, Hkv, D, scale, out, threads,
+                   [&](int32_t b, int32_t h, int32_t j, double* kd, double* vd) {
+        const size_t row = b * seq + static_cast<size_t>(D) * (j + static_cast<size_t>(padded_context) * h);
+        for (int32_t d = 0; d < D; ++d) {
+            kd[d] = static_cast<double>(bf16(k_cache[row + d]));
+            vd[d] = static_cast<double>(bf16(v_cache[row + d]));
+        }
+    });
 }
 
 // ---- argmax ----------------------------------------------------------------------------------

@@ -53,6 +53,13 @@ void orc_attention(const uint16_t* q, const int8_t* k_codes, const int8_t* v_cod
                    const int32_t* parents, int32_t T, int32_t B, int32_t Hq, int32_t Hkv,
                    int32_t D, int32_t padded_context, double scale, double* out, int32_t threads);
 
+// Same oracle over a BF16 cache: k_cache/v_cache BF16 [B][Hkv][padded_context][D], values used as
+// stored (the new rows are expected to be in the planes already).
+void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                        const int32_t* positions, const int32_t* parents, int32_t T, int32_t B,
+                        int32_t Hq, int32_t Hkv, int32_t D, int32_t padded_context, double scale,
+                        double* out, int32_t threads);
+
 // ---- argmax ----------------------------------------------------------------------------------
 void orc_argmax(const uint16_t* logits, int32_t physical_rows, int32_t columns, int32_t valid_rows,
                 int32_t* out);

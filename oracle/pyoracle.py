@@ -116,6 +116,20 @@ def attention(q, kc, vc, ks, vs, positions, parents, T, B, Hq, Hkv, D, P, scale,
     return out
 
 
+def attention_bf16(q, kb, vb, positions, parents, T, B, Hq, Hkv, D, P, scale, threads=0):
+    """FP64 attention over BF16 cache planes kb/vb [B][Hkv][P][D] (new rows already written)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    kb = np.ascontiguousarray(kb, dtype=np.uint16)
+    vb = np.ascontiguousarray(vb, dtype=np.uint16)
+    positions = np.ascontiguousarray(positions, dtype=np.int32)
+    par = None if parents is None else np.ascontiguousarray(parents, dtype=np.int32)
+    out = np.zeros(D * Hq * T * B, dtype=np.float64)
+    lib().orc_attention_bf16(_ptr(q), _ptr(kb), _ptr(vb), _ptr(positions), _ptr(par), C.c_int32(T),
+                             C.c_int32(B), C.c_int32(Hq), C.c_int32(Hkv), C.c_int32(D), C.c_int32(P),
+                             C.c_double(scale), _ptr(out), C.c_int32(threads))
+    return out
+
+
 def argmax(logits, physical_rows, columns, valid_rows):
     logits = np.ascontiguousarray(logits, dtype=np.uint16)
     out = np.zeros(columns, dtype=np.int32)

@@ -10,8 +10,9 @@ from ninfer_amd.kv_cache import KVCacheLayer
 
 
 def upload_cache(case) -> KVCacheLayer:
-    cache = KVCacheLayer(case.max_context, case.Hkv, case.D, case.B)
-    cache.upload(case.kc, case.vc, case.ks, case.vs)
+    dtype = na.BF16 if getattr(case, "kv", "i8") == "bf16" else na.I8
+    cache = KVCacheLayer(case.max_context, case.Hkv, case.D, case.B, dtype=dtype)
+    cache.upload(*case.cache_planes())
     return cache
 
 

@@ -37,40 +37,77 @@ def reference_composite_ok(got: np.ndarray, ref: np.ndarray, tol=ATTENTION_BF16)
 
 
 class AttnCase:
-    """One verify-attention problem: BF16 history K/V quantized into INT8-G64 planes, T new K/V
-    columns, BF16 Q, positions L..L+T-1 per sequence."""
+    """One verify-attention problem: BF16 history K/V quantized into INT8-G64 planes (or stored
+    as BF16 when kv="bf16"), T new K/V columns, BF16 Q, positions L..L+T-1 per sequence."""
 
     def __init__(self, Ls, T=4, Hq=40, Hkv=8, D=128, seed=0, outliers=False, parents=None,
-                 max_context=None, qstd=1.0):
+                 max_context=None, qstd=1.0, kv="i8", dist="normal"):
         self.Ls = list(Ls)
         self.B = len(self.Ls)
         self.T, self.Hq, self.Hkv, self.D = T, Hq, Hkv, D
         self.max_context = max_context or (max(self.Ls) + T)
         self.P = align_up(self.max_context, 128)
         self.parents = parents
+        self.kv = kv
         B, P, G = self.B, self.P, D // 64
-        self.kc = np.zeros((B, Hkv, P, D), dtype=np.int8)
-        self.vc = np.zeros((B, Hkv, P, D), dtype=np.int8)
-        self.ks = np.zeros((B, Hkv, P, G), dtype=np.uint16)
-        self.vs = np.zeros((B, Hkv, P, G), dtype=np.uint16)
         gen = syn.normal_bf16_with_outliers if outliers else syn.normal_bf16
-        from oracle import pyoracle
-        for b, L in enumerate(self.Ls):
-            if L > 0:
-                hk = gen(syn.derive_seed(seed, 1, b), D * Hkv * L)
-                hv = gen(syn.derive_seed(seed, 2, b), D * Hkv * L)
-                pos = np.arange(L, dtype=np.int32)
-                kcb, vcb, ksb, vsb = self.kc[b], self.vc[b], self.ks[b], self.vs[b]
-                pyoracle.kv_append(hk, hv, pos, L, 1, Hkv, D, P, kcb, vcb, ksb, vsb)
-        self.k_new = np.concatenate([gen(syn.derive_seed(seed, 3, b), D * Hkv * T) for b in range(B)])
-        self.v_new = np.concatenate([gen(syn.derive_seed(seed, 4, b), D * Hkv * T) for b in range(B)])
-        self.q = np.concatenate([syn.normal_bf16(syn.derive_seed(seed, 5, b), D * Hq * T, qstd) for b in range(B)])
+        gen_k = gen_v = gen
+        gen_q = lambda sd, n: syn.normal_bf16(sd, n, qstd)  # noqa: E731
+        if dist == "uniform":
+            # the reference's op-test inputs: Q, K in [-0.25, 0.25), V in [-1, 1)
+            # (tests/ops/test_gqa_attention.cpp:778-782)
+            gen_k = gen_q = lambda sd, n: syn.uniform_bf16(sd, n, -0.25, 0.25)  # noqa: E731
+            gen_v = lambda sd, n: syn.uniform_bf16(sd, n, -1.0, 1.0)  # noqa: E731
+        if kv == "bf16":
+            # rows past each history hold a marker value the attention must never read
+            self.kb = np.full((B, Hkv, P, D), 0x7F80, dtype=np.uint16)
+            self.vb = np.full((B, Hkv, P, D), 0x7F80, dtype=np.uint16)
+            for b, L in enumerate(self.Ls):
+                if L > 0:
+                    hk = gen_k(syn.derive_seed(seed, 1, b), D * Hkv * L).reshape(L, Hkv, D)
+                    hv = gen_v(syn.derive_seed(seed, 2, b), D * Hkv * L).reshape(L, Hkv, D)
+                    self.kb[b, :, :L] = hk.transpose(1, 0, 2)
+                    self.vb[b, :, :L] = hv.transpose(1, 0, 2)
+        else:
+            self.kc = np.zeros((B, Hkv, P, D), dtype=np.int8)
+            self.vc = np.zeros((B, Hkv, P, D), dtype=np.int8)
+            self.ks = np.zeros((B, Hkv, P, G), dtype=np.uint16)
+            self.vs = np.zeros((B, Hkv, P, G), dtype=np.uint16)
+            from oracle import pyoracle
+            for b, L in enumerate(self.Ls):
+                if L > 0:
+                    hk = gen_k(syn.derive_seed(seed, 1, b), D * Hkv * L)
+                    hv = gen_v(syn.derive_seed(seed, 2, b), D * Hkv * L)
+                    pos = np.arange(L, dtype=np.int32)
+                    kcb, vcb, ksb, vsb = self.kc[b], self.vc[b], self.ks[b], self.vs[b]
+                    pyoracle.kv_append(hk, hv, pos, L, 1, Hkv, D, P, kcb, vcb, ksb, vsb)
+        self.k_new = np.concatenate([gen_k(syn.derive_seed(seed, 3, b), D * Hkv * T) for b in range(B)])
+        self.v_new = np.concatenate([gen_v(syn.derive_seed(seed, 4, b), D * Hkv * T) for b in range(B)])
+        self.q = np.concatenate([gen_q(syn.derive_seed(seed, 5, b), D * Hq * T) for b in range(B)])
         self.positions = np.concatenate([np.arange(L, L + T, dtype=np.int32) for L in self.Ls])
         self.scale = float(np.float32(1.0 / np.sqrt(D)))
+
+    def cache_planes(self):
+        """Host planes in the order KVCacheLayer.upload/download use."""
+        if self.kv == "bf16":
+            return self.kb, self.vb
+        return self.kc, self.vc, self.ks, self.vs
 
     def oracle_after_append(self):
         """Cache planes after appending the new columns, and the FP64 attention output."""
         from oracle import pyoracle
+        if self.kv == "bf16":
+            kb, vb = self.kb.copy(), self.vb.copy()
+            T, Hkv, D = self.T, self.Hkv, self.D
+            for b in range(self.B):
+                rows = self.positions[b * T:(b + 1) * T]
+                kn = self.k_new[b * D * Hkv * T:(b + 1) * D * Hkv * T].reshape(T, Hkv, D)
+                vn = self.v_new[b * D * Hkv * T:(b + 1) * D * Hkv * T].reshape(T, Hkv, D)
+                kb[b][:, rows] = kn.transpose(1, 0, 2)
+                vb[b][:, rows] = vn.transpose(1, 0, 2)
+            out = pyoracle.attention_bf16(self.q, kb, vb, self.positions, self.parents, self.T, self.B,
+                                          self.Hq, self.Hkv, self.D, self.P, float(self.scale))
+            return (kb, vb), out
         kc, vc, ks, vs = self.kc.copy(), self.vc.copy(), self.ks.copy(), self.vs.copy()
         pyoracle.kv_append(self.k_new, self.v_new, self.positions, self.T, self.B, self.Hkv, self.D, self.P,
                            kc, vc, ks, vs)

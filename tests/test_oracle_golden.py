@@ -193,6 +193,77 @@ def test_chain_tree_equals_causal_oracle(oracle):
     assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("tree", [False, True])
+def test_attention_bf16_equals_int8_oracle_on_exact_values(oracle, tree):
+    """With power-of-two FP16 scales every decoded INT8 value code * 2^e is exact in BF16, so the
+    BF16-cache oracle over those values must return the pinned INT8 oracle's output bit for bit
+    (checks its row decode, plane indexing and visibility against the INT8 path)."""
+    from helpers import AttnCase
+    T, Hq, Hkv, D = 5, 8, 2, 128
+    # parents [T, B]: one tree per sequence
+    parents = np.array([-1, 0, 0, 1, 2, -1, 0, 1, 1, 3], dtype=np.int32) if tree else None
+    case = AttnCase([0, 41], T=T, Hq=Hq, Hkv=Hkv, D=D, seed=8, parents=parents)
+    (kc, vc, ks, vs), _ = case.oracle_after_append()
+    rng = np.random.default_rng(8)
+    exps = rng.integers(-9, -2, size=ks.shape)
+    ks2 = ((exps + 15) << 10).astype(np.uint16)
+    vs2 = ((rng.integers(-9, -2, size=vs.shape) + 15) << 10).astype(np.uint16)
+    out_i8 = oracle.attention(case.q, kc, vc, ks2, vs2, case.positions, parents, T, case.B, Hq, Hkv, D,
+                              case.P, case.scale)
+    kval = kc.astype(np.float32).reshape(*kc.shape[:3], D // 64, 64) * \
+        ks2.view(np.float16).astype(np.float32)[..., None]
+    vval = vc.astype(np.float32).reshape(*vc.shape[:3], D // 64, 64) * \
+        vs2.view(np.float16).astype(np.float32)[..., None]
+    kb = syn.f32_to_bf16_bits(kval.reshape(kc.shape))
+    vb = syn.f32_to_bf16_bits(vval.reshape(vc.shape))
+    assert np.array_equal(syn.bf16_bits_to_f32(kb), kval.reshape(kc.shape))  # exact in BF16
+    out_bf = oracle.attention_bf16(case.q, kb, vb, case.positions, parents, T, case.B, Hq, Hkv, D, case.P,
+                                   case.scale)
+    assert np.array_equal(out_i8, out_bf)
+
+
+def test_attention_bf16_case_vs_numpy_restatement(oracle):
+    """BF16 case: the new rows land at their positions, rows past them keep the marker, and the
+    output equals an independent numpy softmax over the stored values."""
+    from helpers import AttnCase
+    T, Hq, Hkv, D, L = 4, 6, 2, 256, 29
+    case = AttnCase([L], T=T, Hq=Hq, Hkv=Hkv, D=D, seed=9, kv="bf16", dist="uniform")
+    (kb, vb), out = case.oracle_after_append()
+    kn = case.k_new.reshape(T, Hkv, D)
+    assert np.array_equal(kb[0, :, L:L + T], kn.transpose(1, 0, 2))
+    assert np.all(kb[0, :, L + T:] == 0x7F80) and np.all(vb[0, :, L + T:] == 0x7F80)
+    q = syn.bf16_bits_to_f32(case.q).astype(np.float64).reshape(T, Hq, D)
+    out = out.reshape(T, Hq, D)
+    G = Hq // Hkv
+    for h in range(Hkv):
+        kd = syn.bf16_bits_to_f32(kb[0, h, :L + T]).astype(np.float64)
+        vd = syn.bf16_bits_to_f32(vb[0, h, :L + T]).astype(np.float64)
+        for t in range(T):
+            vis = np.arange(L + T) <= L + t
+            for g in range(G):
+                ref = _numpy_attention(q[t, h * G + g], kd, vd, vis, case.scale)
+                np.testing.assert_allclose(out[t, h * G + g], ref, rtol=1e-9, atol=1e-12)
+
+
+def test_attention_bf16_stress_closed_form(oracle):
+    """The reference's stress decode (tests/ops/test_gqa_attention.cpp:772-777): Q = K_new = 8,
+    history K = -8. The new row's score exceeds every history score by 128 sqrt(D), so the output
+    is the new V row exactly."""
+    from helpers import AttnCase
+    D, Hq, Hkv, L = 256, 24, 4, 17
+    case = AttnCase([L], T=1, Hq=Hq, Hkv=Hkv, D=D, seed=31, kv="bf16")
+    eight = syn.f32_to_bf16_bits(np.array([8.0], np.float32))[0]
+    case.q[:] = eight
+    case.k_new[:] = eight
+    case.kb[0, :, :L] = syn.f32_to_bf16_bits(np.array([-8.0], np.float32))[0]
+    case.v_new[:] = syn.uniform_bf16(32, case.v_new.size, -8.0, 8.0)
+    case.vb[0, :, :L] = syn.uniform_bf16(33, Hkv * L * D, -8.0, 8.0).reshape(Hkv, L, D)
+    _, out = case.oracle_after_append()
+    vn = syn.bf16_bits_to_f32(case.v_new).astype(np.float64).reshape(Hkv, D)
+    expect = np.repeat(vn, Hq // Hkv, axis=0).ravel()
+    assert np.array_equal(out, expect)
+
+
 # ---- argmax ---------------------------------------------------------------------------------------
 
 def test_argmax_brute_force(oracle):
