@@ -259,6 +259,63 @@ def general_launch(dev, stream):
                                    VOCAB, dev["cfg"].ptr, dev["ws"], stream)
 
 
+GDN_S, GDN_HQK, GDN_HV, GDN_LAYERS = 128, 16, 48, 48  # Qwen3.6-27B (src/targets/qwen3_6_27b/impl/config.h:23-26)
+GDN_CONV = 2 * GDN_HQK * GDN_S + GDN_HV * GDN_S
+
+
+def gdn_bytes(T: int) -> int:
+    """HBM bytes of one hybrid layer's recurrent ops over T verify tokens: the FP32 state read from
+    the initial slot and T snapshots written, q/k/v/out, g/beta; the conv windows (read 3, write
+    3T) with x/out and the weight."""
+    state = GDN_S * GDN_S * GDN_HV * 4
+    gdn = state * (1 + T) + 2 * GDN_S * GDN_HQK * T * 2 + 2 * GDN_S * GDN_HV * T * 2 + 2 * GDN_HV * T * 4
+    conv = GDN_CONV * 2 * (3 + 3 * T + 2 * T + 4)
+    return gdn + conv
+
+
+def gdn_bench(stream, args):
+    """48 hybrid layers of one verify step (T = 4): conv1d + SiLU snapshot, then the Gated DeltaNet
+    snapshot recurrence, each layer with state slots of its own, in one captured graph."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray
+    S, Hqk, Hv, C, T = GDN_S, GDN_HQK, GDN_HV, GDN_CONV, 4
+    rng = np.random.default_rng(11)
+    q = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    dq = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(q), (S, Hqk, T))
+    dk = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(k), (S, Hqk, T))
+    dv = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, S * Hv * T)), (S, Hv, T))
+    dg = DeviceArray.from_numpy(na.FP32, rng.uniform(-4, 0, Hv * T).astype(np.float32), (Hv, T))
+    db = DeviceArray.from_numpy(na.FP32, rng.uniform(0.05, 0.95, Hv * T).astype(np.float32), (Hv, T))
+    dx = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-2, 2, C * T)), (C, T))
+    dw = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, C * 4)), (C, 4))
+    slot = DeviceArray.from_numpy(na.I32, np.array([1], np.int32), (1,))
+    state0 = rng.uniform(-0.1, 0.1, S * S * Hv * T).astype(np.float32)
+    win0 = syn.f32_to_bf16_bits(rng.uniform(-2, 2, C * 3 * T))
+    layers = []
+    for _ in range(GDN_LAYERS):
+        layers.append(dict(states=DeviceArray.from_numpy(na.FP32, state0, (S, S, Hv, T)),
+                           conv=DeviceArray.from_numpy(na.BF16, win0, (C, 3, T)),
+                           xo=DeviceArray(na.BF16, (C, T)), out=DeviceArray(na.BF16, (S, Hv, T))))
+    scale = float(np.float32(1 / np.sqrt(S)))
+
+    def step():
+        for ly in layers:
+            ops.causal_conv1d_silu_snapshot(dx.tensor(), dw.tensor(), ly["conv"].tensor(), slot.tensor(),
+                                            ly["xo"].tensor(), stream)
+            ops.gated_delta_rule_snapshot(dq.tensor(), dk.tensor(), dv.tensor(), dg.tensor(), db.tensor(), scale, False,
+                                          ly["states"].tensor(), slot.tensor(), ly["out"].tensor(), stream)
+    g = capture(stream, step)
+    ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)
+    us = ms * 1e3 / GDN_LAYERS
+    gbs = gdn_bytes(T) / (us * 1e-6) / 1e9
+    return dict(us_per_layer=us, us_per_layer_p95=p95 * 1e3 / GDN_LAYERS, gbs=gbs, bytes_per_layer=gdn_bytes(T),
+                frac_of_peak=gbs / HBM_PEAK_GBS, layers=GDN_LAYERS, tokens=T)
+
+
 def cpu_baseline(sample_layers: int):
     """Oracle attention on the host for `sample_layers` C2 layers (reported only)."""
     from oracle import pyoracle
@@ -300,7 +357,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "gdn", "copy"], default=None,
                     help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
                          "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
@@ -455,6 +512,15 @@ def main():
         log(f"sampler: B=1 {sres['b1_us']:.1f} us, B=16 {sres['b16_us_per_seq']:.2f} us/seq; "
             f"Mode F B=1 {sres['mode_f_b1_us']:.1f} us, B=16 {sres['mode_f_b16_us_per_seq']:.2f} us/seq")
 
+    # ---- hybrid layers: GDN recurrent state over the verify tokens (snapshot per token) ----------
+    if args.only in (None, "gdn"):
+        gres = gdn_bench(stream, args)
+        if args.only:
+            log(f"GDN {gres}")
+            return
+        result["gdn"] = gres
+        log(f"GDN snapshot: {gres['us_per_layer']:.2f} us/layer, {gres['gbs']:.0f} GB/s")
+
     cpu = None
     if not args.skip_cpu:
         t0 = time.perf_counter()
@@ -494,6 +560,11 @@ def main():
             "workload": "C3 shape over a BF16 KV cache: context 260096, 1% outliers +-20, one layer "
                         "(new rows copied into the cache by their own launch, then attention)",
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3_bf16"].items()}}
+    if "gdn" in result:
+        line["gdn_snapshot"] = {
+            "workload": "48 hybrid layers of a verify step (T=4): conv1d+SiLU snapshot (C=10240) and Gated DeltaNet "
+                        "snapshot recurrence (S=128, 16 q/k heads, 48 value heads, FP32 state), one graph",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["gdn"].items()}}
     if "sampler" in result:
         line["sampler"] = {"workload": "stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95: Mode R (top-20 cap) "
                                        "and Mode F (full vocabulary, draft logits correlated 0.9)",
@@ -511,6 +582,9 @@ def main():
         "bytes_per_launch": attn_bytes(7680),
         "traffic_detail": traffic,
     }
+    if "gdn_snapshot" in line:
+        tg = measured_traffic("gdn")
+        line["gdn_snapshot"]["traffic"] = tg["bytes"] if tg else None
     if "long_context" in line:
         t3 = measured_traffic("c3")
         line["long_context"]["traffic"] = t3["bytes"] if t3 else None

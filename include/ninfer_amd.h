@@ -14,7 +14,8 @@
  * (std::invalid_argument / std::overflow_error).
  *
  * Reference: Neroued/ninfer, include/ninfer/ops/{gqa_attention,argmax,sampling,
- * speculative_round,kv_cache_append_prefix}.h. Entries marked EXTENSION have no reference symbol.
+ * speculative_round,mtp_round,kv_cache_append_prefix,gated_delta_rule,causal_conv1d_silu,
+ * scalar}.h. Entries marked EXTENSION have no reference symbol.
  */
 #ifndef NINFER_AMD_H
 #define NINFER_AMD_H
@@ -230,6 +231,60 @@ int nmi_tree_accept_greedy(const nmi_tensor* parents, const nmi_tensor* node_tok
                            nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,
                            nmi_tensor* num_sampled, nmi_tensor* accepted, nmi_tensor* stats,
                            nmi_stream_t stream);
+
+/* ---------------------------------------------------------------- recurrent state (hybrid layers) */
+
+/* Replaces gated_delta_rule_workspace_bytes (include/ninfer/ops/gated_delta_rule.h:18-21), as a
+ * status with the size in *bytes. The recurrent kernel needs no transient storage for any T, so
+ * a valid geometry gives 0. */
+int nmi_gated_delta_rule_workspace_bytes(int32_t head_dim, int32_t qk_heads, int32_t value_heads,
+                                         int32_t tokens, int32_t normalize_qk, size_t* bytes);
+
+/* Replaces both gated_delta_rule forms (include/ninfer/ops/gated_delta_rule.h:23-55): for each
+ * value head h (q/k head h / (Hv/Hqk)), in token order: alpha = exp(g[h,t]);
+ * delta = beta[h,t] * (v[:,h,t] - alpha * S_h * k[:,qh,t]); S_h = alpha * S_h + outer(delta, k);
+ * out[:,h,t] = BF16(scale * S_h * q[:,qh,t]). q/k BF16 [S,Hqk,T], v/out BF16 [S,Hv,T], g/beta FP32
+ * [Hv,T], states FP32 [S,S,Hv] (row = value index, key index fastest), S in {16,32,64,128},
+ * scale = 1/sqrt(S). normalize_qk: q and k rows become x / sqrt(sum(x^2) + 1e-6) first.
+ * ssm_state_in and ssm_state_out may be the same storage (the in-place form) or disjoint. */
+int nmi_gated_delta_rule(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                         const nmi_tensor* g, const nmi_tensor* beta, float scale,
+                         int32_t normalize_qk, const nmi_tensor* ssm_state_in,
+                         nmi_tensor* ssm_state_out, nmi_tensor* out, nmi_stream_t stream);
+
+/* Replaces gated_delta_rule_snapshot (include/ninfer/ops/gated_delta_rule.h:57-68): ssm_states FP32
+ * [S,S,Hv,Slots], Slots >= T; slot *initial_slot (device I32) supplies the initial state and the
+ * state after token t is written to slot t; slots >= T are unchanged. After acceptance the next
+ * round starts from slot `accepted` (see nmi_assign_i32_scalar). A device-side initial slot
+ * outside [0, Slots) makes the call write nothing. */
+int nmi_gated_delta_rule_snapshot(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                                  const nmi_tensor* g, const nmi_tensor* beta, float scale,
+                                  int32_t normalize_qk, nmi_tensor* ssm_states,
+                                  const nmi_tensor* initial_slot, nmi_tensor* out,
+                                  nmi_stream_t stream);
+
+/* Replaces both causal_conv1d_silu forms (include/ninfer/ops/causal_conv1d_silu.h:9-31):
+ * out[c,t] = BF16(SiLU(sum_{j<4} weight[c,j] * u[c,t-3+j])) with u = state window (3 values,
+ * oldest first) followed by x. x/out BF16 [C,T], weight BF16 [C,4], states BF16 [C,3]; the final
+ * window is written to conv_state_out (which may be the same storage as conv_state_in). */
+int nmi_causal_conv1d_silu(const nmi_tensor* x, const nmi_tensor* weight,
+                           const nmi_tensor* conv_state_in, nmi_tensor* conv_state_out,
+                           nmi_tensor* out, nmi_stream_t stream);
+
+/* Replaces causal_conv1d_silu_snapshot (include/ninfer/ops/causal_conv1d_silu.h:33-40):
+ * conv_states BF16 [C,3,Slots], Slots >= T; window slot *initial_slot in, window after token t
+ * out to slot t. A device-side initial slot outside [0, Slots) makes the call write nothing. */
+int nmi_causal_conv1d_silu_snapshot(const nmi_tensor* x, const nmi_tensor* weight,
+                                    nmi_tensor* conv_states, const nmi_tensor* initial_slot,
+                                    nmi_tensor* out, nmi_stream_t stream);
+
+/* Replace set_i32_scalar / assign_i32_scalar / increment_i32_scalar / increment_i64_scalar
+ * (include/ninfer/ops/scalar.h:30-33): one-element device scalars; assign requires distinct
+ * storage. assign(accepted -> initial_slot) is the recurrent-state commit of a verify round. */
+int nmi_set_i32_scalar(nmi_tensor* destination, int32_t value, nmi_stream_t stream);
+int nmi_assign_i32_scalar(const nmi_tensor* source, nmi_tensor* destination, nmi_stream_t stream);
+int nmi_increment_i32_scalar(nmi_tensor* scalar, nmi_stream_t stream);
+int nmi_increment_i64_scalar(nmi_tensor* scalar, nmi_stream_t stream);
 
 #ifdef __cplusplus
 }

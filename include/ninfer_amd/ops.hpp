@@ -1,5 +1,6 @@
 // C++20 drop-in layer over the ninfer_amd C ABI: the reference's ninfer::ops signatures
-// (include/ninfer/ops/{gqa_attention,argmax,sampling,speculative_round,kv_cache_append_prefix}.h)
+// (include/ninfer/ops/{gqa_attention,argmax,sampling,speculative_round,mtp_round,
+// kv_cache_append_prefix,gated_delta_rule,causal_conv1d_silu,scalar}.h)
 // with hipStream_t in place of cudaStream_t. Statuses become the reference's exceptions:
 // std::invalid_argument, std::overflow_error, std::runtime_error (launch failure).
 //
@@ -294,6 +295,92 @@ inline void tree_accept_greedy(const Tensor& parents, const Tensor& node_tokens,
                cns = num_sampled.c(), cacc = accepted.c(), cst = stats.c();
     detail::check(nmi_tree_accept_greedy(&cpar, &cnt, &ctt, &cpath, &cpl, &clen, &ctok, &cso, &cns, &cacc, &cst,
                                          detail::st(stream)));
+}
+
+// ---- recurrent state of the hybrid layers -------------------------------------------------------
+
+// include/ninfer/ops/gated_delta_rule.h:18-21
+[[nodiscard]] inline std::size_t gated_delta_rule_workspace_bytes(int32_t head_dim, int32_t qk_heads,
+                                                                  int32_t value_heads, int32_t tokens,
+                                                                  bool normalize_qk) {
+    std::size_t n = 0;
+    detail::check(nmi_gated_delta_rule_workspace_bytes(head_dim, qk_heads, value_heads, tokens, normalize_qk ? 1 : 0,
+                                                       &n));
+    return n;
+}
+
+// include/ninfer/ops/gated_delta_rule.h:41-43 (in place) and :50-53 (distinct states). The
+// recurrent kernel uses no transient storage; `ws` is accepted for signature parity.
+inline void gated_delta_rule(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g, const Tensor& beta,
+                             float scale, bool normalize_qk, const Tensor& ssm_state_in, Tensor& ssm_state_out,
+                             Tensor& out, hipStream_t stream) {
+    const nmi_tensor cq = q.c(), ck = k.c(), cv = v.c(), cg = g.c(), cb = beta.c(), ci = ssm_state_in.c();
+    nmi_tensor co = ssm_state_out.c(), cout = out.c();
+    detail::check(nmi_gated_delta_rule(&cq, &ck, &cv, &cg, &cb, scale, normalize_qk ? 1 : 0, &ci, &co, &cout,
+                                       detail::st(stream)));
+}
+inline void gated_delta_rule(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g, const Tensor& beta,
+                             float scale, bool normalize_qk, WorkspaceArena& ws, Tensor& ssm_state, Tensor& out,
+                             hipStream_t stream) {
+    (void)ws;
+    gated_delta_rule(q, k, v, g, beta, scale, normalize_qk, ssm_state, ssm_state, out, stream);
+}
+inline void gated_delta_rule(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g, const Tensor& beta,
+                             float scale, bool normalize_qk, WorkspaceArena& ws, const Tensor& ssm_state_in,
+                             Tensor& ssm_state_out, Tensor& out, hipStream_t stream) {
+    (void)ws;
+    gated_delta_rule(q, k, v, g, beta, scale, normalize_qk, ssm_state_in, ssm_state_out, out, stream);
+}
+
+// include/ninfer/ops/gated_delta_rule.h:65-68
+inline void gated_delta_rule_snapshot(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g,
+                                      const Tensor& beta, float scale, bool normalize_qk, WorkspaceArena& ws,
+                                      Tensor& ssm_states, const Tensor& initial_slot, Tensor& out,
+                                      hipStream_t stream) {
+    (void)ws;
+    const nmi_tensor cq = q.c(), ck = k.c(), cv = v.c(), cg = g.c(), cb = beta.c(), cs = initial_slot.c();
+    nmi_tensor cst = ssm_states.c(), cout = out.c();
+    detail::check(nmi_gated_delta_rule_snapshot(&cq, &ck, &cv, &cg, &cb, scale, normalize_qk ? 1 : 0, &cst, &cs,
+                                                &cout, detail::st(stream)));
+}
+
+// include/ninfer/ops/causal_conv1d_silu.h:24-31
+inline void causal_conv1d_silu(const Tensor& x, const Tensor& weight, const Tensor& conv_state_in,
+                               Tensor& conv_state_out, Tensor& out, hipStream_t stream) {
+    const nmi_tensor cx = x.c(), cw = weight.c(), ci = conv_state_in.c();
+    nmi_tensor co = conv_state_out.c(), cout = out.c();
+    detail::check(nmi_causal_conv1d_silu(&cx, &cw, &ci, &co, &cout, detail::st(stream)));
+}
+inline void causal_conv1d_silu(const Tensor& x, const Tensor& weight, Tensor& conv_state, Tensor& out,
+                               hipStream_t stream) {
+    causal_conv1d_silu(x, weight, conv_state, conv_state, out, stream);
+}
+
+// include/ninfer/ops/causal_conv1d_silu.h:39-40
+inline void causal_conv1d_silu_snapshot(const Tensor& x, const Tensor& weight, Tensor& conv_states,
+                                        const Tensor& initial_slot, Tensor& out, hipStream_t stream) {
+    const nmi_tensor cx = x.c(), cw = weight.c(), cs = initial_slot.c();
+    nmi_tensor cst = conv_states.c(), cout = out.c();
+    detail::check(nmi_causal_conv1d_silu_snapshot(&cx, &cw, &cst, &cs, &cout, detail::st(stream)));
+}
+
+// include/ninfer/ops/scalar.h:30-33
+inline void set_i32_scalar(Tensor& destination, int32_t value, hipStream_t stream) {
+    nmi_tensor cd = destination.c();
+    detail::check(nmi_set_i32_scalar(&cd, value, detail::st(stream)));
+}
+inline void assign_i32_scalar(const Tensor& source, Tensor& destination, hipStream_t stream) {
+    const nmi_tensor cs = source.c();
+    nmi_tensor cd = destination.c();
+    detail::check(nmi_assign_i32_scalar(&cs, &cd, detail::st(stream)));
+}
+inline void increment_i32_scalar(Tensor& scalar, hipStream_t stream) {
+    nmi_tensor cs = scalar.c();
+    detail::check(nmi_increment_i32_scalar(&cs, detail::st(stream)));
+}
+inline void increment_i64_scalar(Tensor& scalar, hipStream_t stream) {
+    nmi_tensor cs = scalar.c();
+    detail::check(nmi_increment_i64_scalar(&cs, detail::st(stream)));
 }
 
 } // namespace ops

@@ -110,6 +110,15 @@ _SIGNATURES = {
     "nmi_speculative_accept_general": (C.c_int, [_T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_int32, C.c_void_p, C.c_void_p, C.c_size_t, _STREAM]),
     "nmi_speculative_select_accepted_hidden": (C.c_int, [_T, _T, _T, _STREAM]),
     "nmi_mtp_prepare_alignment_ids": (C.c_int, [_T, _T, _T, _T, _STREAM]),
+    "nmi_gated_delta_rule_workspace_bytes": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, P(C.c_size_t)]),
+    "nmi_gated_delta_rule": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),
+    "nmi_gated_delta_rule_snapshot": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),
+    "nmi_causal_conv1d_silu": (C.c_int, [_T, _T, _T, _T, _T, _STREAM]),
+    "nmi_causal_conv1d_silu_snapshot": (C.c_int, [_T, _T, _T, _T, _T, _STREAM]),
+    "nmi_set_i32_scalar": (C.c_int, [_T, C.c_int32, _STREAM]),
+    "nmi_assign_i32_scalar": (C.c_int, [_T, _T, _STREAM]),
+    "nmi_increment_i32_scalar": (C.c_int, [_T, _STREAM]),
+    "nmi_increment_i64_scalar": (C.c_int, [_T, _STREAM]),
     "nmi_kv_cache_append_prefix": (C.c_int, [_T, _T, _T, _T, CommitEnvelope, P(KVLayerView), _STREAM]),
     "nmi_kv_cache_rollback": (C.c_int, [_T, _T, P(KVLayerView), _STREAM]),
     "nmi_kv_cache_compact_path": (C.c_int, [_T, _T, _T, P(KVLayerView), _STREAM]),

@@ -206,7 +206,8 @@ const char* nmi_build_info(void) {
     return "ninfer_amd gfx950: verify_attn_partial<{1,2},{128,256}> fp16-MFMA 16x16x32 (INT8-G64 KV), "
            "verify_attn_partial_bf16<{1,2},{128,256}> bf16-MFMA 16x16x32 (BF16 KV), "
            "verify_attn_merge, kv_quant_append, bf16_kv_append, argmax, speculative accept (greedy, top-20 "
-           "stochastic, general fixed-point), kv commit/rollback/compaction";
+           "stochastic, general fixed-point), kv commit/rollback/compaction, gdn_recurrent<{16,32,64,128}> "
+           "(snapshot), conv1d_silu (snapshot), device scalars";
 }
 
 size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,

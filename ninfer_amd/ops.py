@@ -120,6 +120,60 @@ def tree_accept_greedy(parents, node_tokens, target_tokens, path, path_len, leng
                                        _p(num_sampled), _p(accepted), _p(stats), _s(stream)))
 
 
+# ---- recurrent state of the hybrid layers (gated_delta_rule.h, causal_conv1d_silu.h, scalar.h) --
+
+def gated_delta_rule_workspace_bytes(head_dim, qk_heads, value_heads, tokens, normalize_qk) -> int:
+    """include/ninfer/ops/gated_delta_rule.h:18-21 (raises ValueError on an invalid geometry)."""
+    import ctypes as C
+    n = C.c_size_t(0)
+    check(lib().nmi_gated_delta_rule_workspace_bytes(head_dim, qk_heads, value_heads, tokens,
+                                                     1 if normalize_qk else 0, C.byref(n)))
+    return n.value
+
+
+def gated_delta_rule(q, k, v, g, beta, scale, normalize_qk, ssm_state_in, ssm_state_out, out,
+                     stream=None) -> None:
+    """include/ninfer/ops/gated_delta_rule.h:41-55; pass the same tensor twice for the in-place form."""
+    check(lib().nmi_gated_delta_rule(_p(q), _p(k), _p(v), _p(g), _p(beta), scale, 1 if normalize_qk else 0,
+                                     _p(ssm_state_in), _p(ssm_state_out), _p(out), _s(stream)))
+
+
+def gated_delta_rule_snapshot(q, k, v, g, beta, scale, normalize_qk, ssm_states, initial_slot, out,
+                              stream=None) -> None:
+    """include/ninfer/ops/gated_delta_rule.h:57-68."""
+    check(lib().nmi_gated_delta_rule_snapshot(_p(q), _p(k), _p(v), _p(g), _p(beta), scale,
+                                              1 if normalize_qk else 0, _p(ssm_states), _p(initial_slot),
+                                              _p(out), _s(stream)))
+
+
+def causal_conv1d_silu(x, weight, conv_state_in, conv_state_out, out, stream=None) -> None:
+    """include/ninfer/ops/causal_conv1d_silu.h:23-31; pass the same tensor twice for the in-place form."""
+    check(lib().nmi_causal_conv1d_silu(_p(x), _p(weight), _p(conv_state_in), _p(conv_state_out), _p(out),
+                                       _s(stream)))
+
+
+def causal_conv1d_silu_snapshot(x, weight, conv_states, initial_slot, out, stream=None) -> None:
+    """include/ninfer/ops/causal_conv1d_silu.h:33-40."""
+    check(lib().nmi_causal_conv1d_silu_snapshot(_p(x), _p(weight), _p(conv_states), _p(initial_slot), _p(out),
+                                                _s(stream)))
+
+
+def set_i32_scalar(destination, value, stream=None) -> None:
+    check(lib().nmi_set_i32_scalar(_p(destination), value, _s(stream)))
+
+
+def assign_i32_scalar(source, destination, stream=None) -> None:
+    check(lib().nmi_assign_i32_scalar(_p(source), _p(destination), _s(stream)))
+
+
+def increment_i32_scalar(scalar, stream=None) -> None:
+    check(lib().nmi_increment_i32_scalar(_p(scalar), _s(stream)))
+
+
+def increment_i64_scalar(scalar, stream=None) -> None:
+    check(lib().nmi_increment_i64_scalar(_p(scalar), _s(stream)))
+
+
 # ---- commit / rollback (kv_cache_append_prefix.h + extensions) ----------------------------------
 
 def kv_cache_append_prefix(k, v, positions, commit_count, envelope, cache, stream=None) -> None:

@@ -349,6 +349,96 @@ void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16
     });
 }
 
+// ---- recurrent state of the hybrid layers -----------------------------------------------------
+
+// Restates gdn_ref::forward_recurrent (tests/ops/gdn_ref.h:342-410) for one sequence, with the
+// q/k normalization of normalize_qk_for_fused_oracle (tests/ops/test_gated_delta_rule.cpp:242-260).
+void orc_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                       const float* beta, const float* state_in, int32_t S, int32_t Hqk,
+                       int32_t Hv, int32_t T, double scale, int32_t normalize_qk, double* out,
+                       double* state_out, double* snapshots) {
+    // q/k as the floats the recurrence consumes
+    auto qk_rows = [&](const uint16_t* src) {
+        std::vector<float> rows(static_cast<size_t>(S) * Hqk * T);
+        for (size_t i = 0; i < rows.size(); ++i) { rows[i] = bf16(src[i]); }
+        if (normalize_qk) {
+            for (size_t r = 0; r < static_cast<size_t>(Hqk) * T; ++r) {
+                float* base = rows.data() + r * S;
+                double sumsq = 0.0;
+                for (int32_t d = 0; d < S; ++d) { sumsq += static_cast<double>(base[d]) * static_cast<double>(base[d]); }
+                const double inv = 1.0 / std::sqrt(sumsq + 1.0e-6);
+                for (int32_t d = 0; d < S; ++d) { base[d] = static_cast<float>(static_cast<double>(base[d]) * inv); }
+            }
+        }
+        return rows;
+    };
+    const std::vector<float> qf = qk_rows(q);
+    const std::vector<float> kf = qk_rows(k);
+    const size_t SS = static_cast<size_t>(S) * S;
+    std::vector<double> st(SS), delta(S);
+    for (int32_t h = 0; h < Hv; ++h) {
+        const int32_t qh = h / (Hv / Hqk);
+        for (size_t i = 0; i < SS; ++i) { st[i] = static_cast<double>(state_in[h * SS + i]); }
+        for (int32_t t = 0; t < T; ++t) {
+            const float* qt = qf.data() + (static_cast<size_t>(t) * Hqk + qh) * S;
+            const float* kt = kf.data() + (static_cast<size_t>(t) * Hqk + qh) * S;
+            const uint16_t* vt = v + (static_cast<size_t>(t) * Hv + h) * S;
+            const double alpha = std::exp(static_cast<double>(g[static_cast<size_t>(t) * Hv + h]));
+            const double b = static_cast<double>(beta[static_cast<size_t>(t) * Hv + h]);
+            for (int32_t r = 0; r < S; ++r) {
+                double* row = st.data() + static_cast<size_t>(r) * S;
+                double partial = 0.0;
+                for (int32_t c = 0; c < S; ++c) {
+                    row[c] *= alpha;
+                    partial += row[c] * static_cast<double>(kt[c]);
+                }
+                delta[r] = b * (static_cast<double>(bf16(vt[r])) - partial);
+            }
+            for (int32_t r = 0; r < S; ++r) {
+                double* row = st.data() + static_cast<size_t>(r) * S;
+                for (int32_t c = 0; c < S; ++c) { row[c] += delta[r] * static_cast<double>(kt[c]); }
+            }
+            double* ot = out + (static_cast<size_t>(t) * Hv + h) * S;
+            for (int32_t r = 0; r < S; ++r) {
+                const double* row = st.data() + static_cast<size_t>(r) * S;
+                double partial = 0.0;
+                for (int32_t c = 0; c < S; ++c) { partial += row[c] * static_cast<double>(qt[c]); }
+                ot[r] = partial * scale;
+            }
+            if (snapshots != nullptr) {
+                double* snap = snapshots + (static_cast<size_t>(t) * Hv + h) * SS;
+                for (size_t i = 0; i < SS; ++i) { snap[i] = st[i]; }
+            }
+        }
+        for (size_t i = 0; i < SS; ++i) { state_out[h * SS + i] = st[i]; }
+    }
+}
+
+// Restates cpu_prefill_ref (tests/ops/test_causal_conv1d_silu.cpp:48-75): tap j of channel c at
+// weight[j*C + c], window value s of channel c at state[s*C + c].
+void orc_causal_conv1d_silu(const uint16_t* x, const uint16_t* weight, const uint16_t* state,
+                            int32_t C, int32_t T, double* out, uint16_t* windows) {
+    const size_t Cs = static_cast<size_t>(C);
+    auto u = [&](int32_t c, int32_t t) -> uint16_t { // t >= -3
+        return t < 0 ? state[static_cast<size_t>(3 + t) * Cs + c] : x[static_cast<size_t>(t) * Cs + c];
+    };
+    for (int32_t t = 0; t < T; ++t) {
+        for (int32_t c = 0; c < C; ++c) {
+            double acc = 0.0;
+            for (int32_t j = 0; j < 4; ++j) {
+                acc += static_cast<double>(bf16(weight[static_cast<size_t>(j) * Cs + c])) *
+                       static_cast<double>(bf16(u(c, t - 3 + j)));
+            }
+            out[static_cast<size_t>(t) * Cs + c] = acc / (1.0 + std::exp(-acc));
+            if (windows != nullptr) {
+                for (int32_t s = 0; s < 3; ++s) {
+                    windows[static_cast<size_t>(t) * 3 * Cs + static_cast<size_t>(s) * Cs + c] = u(c, t - 2 + s);
+                }
+            }
+        }
+    }
+}
+
 // ---- argmax ----------------------------------------------------------------------------------
 
 // include/ninfer/ops/argmax.h:11-21: out[t] = min argmax_{v < valid_rows} float(logits[v,t]).

@@ -60,6 +60,22 @@ void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16
                         int32_t Hq, int32_t Hkv, int32_t D, int32_t padded_context, double scale,
                         double* out, int32_t threads);
 
+// ---- recurrent state of the hybrid layers -----------------------------------------------------
+// Gated DeltaNet recurrence in FP64 (one sequence). q/k BF16 [S,Hqk,T], v BF16 [S,Hv,T], g/beta
+// FP32 [Hv,T], state_in FP32 [S,S,Hv] (row = value index, key index fastest). normalize_qk: q and
+// k rows become float(x / sqrt(sum(x^2) + 1e-6)) first. out [S,Hv,T] and state_out [S,S,Hv] in
+// FP64; snapshots (may be NULL) receive the state after token t at t * Hv*S*S.
+void orc_gdn_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                       const float* beta, const float* state_in, int32_t S, int32_t Hqk,
+                       int32_t Hv, int32_t T, double scale, int32_t normalize_qk, double* out,
+                       double* state_out, double* snapshots);
+
+// Width-4 causal depthwise convolution + SiLU in FP64. x BF16 [C,T], weight BF16 [C,4], state
+// BF16 [C,3] (oldest first). out [C,T] in FP64 (before the BF16 boundary); windows (may be NULL)
+// receives the BF16 window after token t at t * 3*C, in the [C,3] layout.
+void orc_causal_conv1d_silu(const uint16_t* x, const uint16_t* weight, const uint16_t* state,
+                            int32_t C, int32_t T, double* out, uint16_t* windows);
+
 // ---- argmax ----------------------------------------------------------------------------------
 void orc_argmax(const uint16_t* logits, int32_t physical_rows, int32_t columns, int32_t valid_rows,
                 int32_t* out);

@@ -130,6 +130,36 @@ def attention_bf16(q, kb, vb, positions, parents, T, B, Hq, Hkv, D, P, scale, th
     return out
 
 
+def gdn_recurrent(q, k, v, g, beta, state, S, Hqk, Hv, T, normalize_qk=False, snapshots=False):
+    """FP64 Gated DeltaNet recurrence: (out [T,Hv,S], state_out [Hv,S,S], snapshots [T,Hv,S,S] or None)."""
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    beta = np.ascontiguousarray(beta, dtype=np.float32)
+    state = np.ascontiguousarray(state, dtype=np.float32)
+    out = np.zeros(S * Hv * T, dtype=np.float64)
+    st = np.zeros(S * S * Hv, dtype=np.float64)
+    snap = np.zeros(S * S * Hv * T, dtype=np.float64) if snapshots else None
+    lib().orc_gdn_recurrent(_ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(state), C.c_int32(S),
+                            C.c_int32(Hqk), C.c_int32(Hv), C.c_int32(T), C.c_double(1.0 / np.sqrt(S)),
+                            C.c_int32(1 if normalize_qk else 0), _ptr(out), _ptr(st), _ptr(snap))
+    return (out.reshape(T, Hv, S), st.reshape(Hv, S, S),
+            None if snap is None else snap.reshape(T, Hv, S, S))
+
+
+def causal_conv1d_silu(x, weight, state, channels, T):
+    """FP64 conv + SiLU: (out [T,C] before the BF16 boundary, windows uint16 [T,3,C])."""
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    weight = np.ascontiguousarray(weight, dtype=np.uint16)
+    state = np.ascontiguousarray(state, dtype=np.uint16)
+    out = np.zeros(channels * T, dtype=np.float64)
+    win = np.zeros(3 * channels * T, dtype=np.uint16)
+    lib().orc_causal_conv1d_silu(_ptr(x), _ptr(weight), _ptr(state), C.c_int32(channels), C.c_int32(T), _ptr(out),
+                                 _ptr(win))
+    return out.reshape(T, channels), win.reshape(T, 3, channels)
+
+
 def argmax(logits, physical_rows, columns, valid_rows):
     logits = np.ascontiguousarray(logits, dtype=np.uint16)
     out = np.zeros(columns, dtype=np.int32)

@@ -166,6 +166,89 @@ def test_mtp_alignment_validation():
         ops.mtp_prepare_alignment_ids(_t(na.I32, (4,)), _t(na.I32, (1,)), _t(na.I32, (1,)), _t(na.I32, (4,)))
 
 
+class _Arena:
+    """Distinct fake device addresses, one region per tensor (validation only, nothing launches)."""
+
+    def __init__(self):
+        self.at = 0x100000
+
+    def __call__(self, dtype, shape):
+        t = _t(dtype, shape, self.at)
+        self.at += 0x1000000
+        return t
+
+
+def _gdn_args(arena, S=128, Hqk=16, Hv=48, T=4):
+    return dict(q=arena(na.BF16, (S, Hqk, T)), k=arena(na.BF16, (S, Hqk, T)), v=arena(na.BF16, (S, Hv, T)),
+                g=arena(na.FP32, (Hv, T)), beta=arena(na.FP32, (Hv, T)), out=arena(na.BF16, (S, Hv, T)))
+
+
+def test_gdn_validation():
+    # src/ops/wrapper/gated_delta_rule.cpp:51-139
+    A = _Arena()
+    a = _gdn_args(A)
+    st = A(na.FP32, (128, 128, 48, 5))
+    slot = A(na.I32, (1,))
+    sc = 1.0 / np.sqrt(128.0)
+    with pytest.raises(ValueError, match="invalid shape for ssm_states snapshot"):
+        ops.gated_delta_rule_snapshot(a["q"], a["k"], a["v"], a["g"], a["beta"], sc, True,
+                                      A(na.FP32, (128, 128, 48, 3)), slot, a["out"])
+    with pytest.raises(ValueError, match="scale must be 1/sqrt"):
+        ops.gated_delta_rule_snapshot(a["q"], a["k"], a["v"], a["g"], a["beta"], 0.1, True, st, slot, a["out"])
+    with pytest.raises(ValueError, match="head dimension must be 16, 32, 64, or 128"):
+        b = _gdn_args(A, S=96)
+        ops.gated_delta_rule_snapshot(b["q"], b["k"], b["v"], b["g"], b["beta"], 1 / np.sqrt(96.0), False,
+                                      A(na.FP32, (96, 96, 48, 4)), slot, b["out"])
+    with pytest.raises(ValueError, match="divisible"):
+        b = _gdn_args(A, Hqk=16, Hv=40)
+        ops.gated_delta_rule_snapshot(b["q"], b["k"], b["v"], b["g"], b["beta"], sc, False,
+                                      A(na.FP32, (128, 128, 40, 4)), slot, b["out"])
+    with pytest.raises(ValueError, match="initial_slot"):
+        ops.gated_delta_rule_snapshot(a["q"], a["k"], a["v"], a["g"], a["beta"], sc, True, st,
+                                      A(na.I64, (1,)), a["out"])
+    with pytest.raises(ValueError, match="g"):
+        ops.gated_delta_rule_snapshot(a["q"], a["k"], a["v"], A(na.BF16, (48, 4)), a["beta"], sc, True, st, slot,
+                                      a["out"])
+    with pytest.raises(ValueError, match="ssm_states must not overlap"):
+        ops.gated_delta_rule_snapshot(a["q"], a["k"], a["v"], a["g"], a["beta"], sc, True,
+                                      _t(na.FP32, (128, 128, 48, 5), a["out"].data), slot, a["out"])
+    s0, s1 = A(na.FP32, (128, 128, 48)), A(na.FP32, (128, 128, 48))
+    with pytest.raises(ValueError, match="ssm_state_out"):
+        ops.gated_delta_rule(a["q"], a["k"], a["v"], a["g"], a["beta"], sc, False, s0, A(na.FP32, (128, 128, 47)),
+                             a["out"])
+    with pytest.raises(ValueError, match="disjoint or the same storage"):
+        ops.gated_delta_rule(a["q"], a["k"], a["v"], a["g"], a["beta"], sc, False, s0,
+                             _t(na.FP32, (128, 128, 48), s0.data + 64), a["out"])
+    assert ops.gated_delta_rule_workspace_bytes(128, 16, 48, 4096, True) == 0
+    with pytest.raises(ValueError, match="invalid geometry"):
+        ops.gated_delta_rule_workspace_bytes(128, 16, 40, 4, True)
+    del s1
+
+
+def test_conv_and_scalar_validation():
+    # src/ops/wrapper/causal_conv1d_silu.cpp:35-200, src/ops/wrapper/scalar.cpp:11-41
+    A = _Arena()
+    x, w, out = A(na.BF16, (256, 4)), A(na.BF16, (256, 4)), A(na.BF16, (256, 4))
+    slot = A(na.I32, (1,))
+    with pytest.raises(ValueError, match=re.escape("conv_states must have shape [C,3,S] with S>=T")):
+        ops.causal_conv1d_silu_snapshot(x, w, A(na.BF16, (256, 3, 3)), slot, out)
+    with pytest.raises(ValueError, match="weight"):
+        ops.causal_conv1d_silu_snapshot(x, A(na.BF16, (256, 3)), A(na.BF16, (256, 3, 4)), slot, out)
+    with pytest.raises(ValueError, match="out"):
+        ops.causal_conv1d_silu_snapshot(x, w, A(na.BF16, (256, 3, 4)), slot, A(na.BF16, (256, 5)))
+    with pytest.raises(ValueError, match="conv_state_out"):
+        ops.causal_conv1d_silu(x, w, A(na.BF16, (256, 3)), A(na.BF16, (255, 3)), out)
+    with pytest.raises(ValueError, match="x"):
+        ops.causal_conv1d_silu(A(na.FP32, (256, 4)), w, A(na.BF16, (256, 3)), A(na.BF16, (256, 3)), out)
+    s = A(na.I32, (1,))
+    with pytest.raises(ValueError, match="must not alias"):
+        ops.assign_i32_scalar(s, s)
+    with pytest.raises(ValueError, match="non-null contiguous scalar"):
+        ops.set_i32_scalar(A(na.I32, (2,)), 3)
+    with pytest.raises(ValueError, match="non-null contiguous scalar"):
+        ops.increment_i64_scalar(A(na.I32, (1,)))
+
+
 def test_argmax_validation():
     with pytest.raises(ValueError, match="valid_rows"):
         ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (4,)), 101)

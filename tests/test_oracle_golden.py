@@ -264,6 +264,125 @@ def test_attention_bf16_stress_closed_form(oracle):
     assert np.array_equal(out, expect)
 
 
+# ---- recurrent state (Gated DeltaNet, causal conv1d) ----------------------------------------------
+
+def _bf(x):
+    return syn.f32_to_bf16_bits(np.asarray(x, dtype=np.float32))
+
+
+def _gdn_numpy(q, k, v, g, beta, state, normalize):
+    """Independent vectorized restatement over all heads: q/k [T,Hqk,S], v [T,Hv,S], g/beta [T,Hv],
+    state [Hv,S,S] (row = value index)."""
+    T, Hv, S = v.shape
+    Hqk = q.shape[1]
+    if normalize:
+        q = (q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6)).astype(np.float32).astype(np.float64)
+        k = (k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)).astype(np.float32).astype(np.float64)
+    St = state.astype(np.float64).copy()
+    rep = Hv // Hqk
+    outs, snaps = [], []
+    for t in range(T):
+        kt = np.repeat(k[t], rep, axis=0)  # [Hv,S]
+        qt = np.repeat(q[t], rep, axis=0)
+        St = St * np.exp(g[t].astype(np.float64))[:, None, None]
+        delta = beta[t][:, None] * (v[t] - np.einsum("hrc,hc->hr", St, kt))
+        St = St + delta[:, :, None] * kt[:, None, :]
+        outs.append(np.einsum("hrc,hc->hr", St, qt) / np.sqrt(S))
+        snaps.append(St.copy())
+    return np.stack(outs), St, np.stack(snaps)
+
+
+def _gdn_inputs(seed, S, Hqk, Hv, T, raw=False):
+    rng = np.random.default_rng(seed)
+    q = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
+    k = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
+    if not raw:
+        q /= np.linalg.norm(q, axis=-1, keepdims=True)
+        k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.uniform(-1, 1, (T, Hv, S)).astype(np.float32)
+    g = rng.uniform(-4, 0, (T, Hv)).astype(np.float32)
+    beta = rng.uniform(0.05, 0.95, (T, Hv)).astype(np.float32)
+    state = rng.uniform(-0.1, 0.1, (Hv, S, S)).astype(np.float32)
+    return _bf(q), _bf(k), _bf(v), g, beta, state
+
+
+@pytest.mark.parametrize("normalize", [False, True])
+def test_gdn_oracle_vs_numpy_restatement(oracle, normalize):
+    S, Hqk, Hv, T = 32, 2, 6, 5
+    q, k, v, g, beta, state = _gdn_inputs(21, S, Hqk, Hv, T, raw=normalize)
+    out, st, snaps = oracle.gdn_recurrent(q, k, v, g, beta, state, S, Hqk, Hv, T, normalize, snapshots=True)
+    f = lambda a: syn.bf16_bits_to_f32(a).astype(np.float64)  # noqa: E731
+    ro, rst, rsn = _gdn_numpy(f(q), f(k), f(v), g, beta, state, normalize)
+    np.testing.assert_allclose(out, ro, rtol=1e-10, atol=1e-13)
+    np.testing.assert_allclose(st, rst, rtol=1e-10, atol=1e-13)
+    np.testing.assert_allclose(snaps, rsn, rtol=1e-10, atol=1e-13)
+
+
+def test_gdn_unit_key_writes_value_column(oracle):
+    """k = e_j, beta = 1: delta = v - alpha S e_j, so the new state's column j is v exactly and the
+    other columns are alpha S (a wrong row/column index or a misplaced alpha breaks this)."""
+    S, Hqk, Hv, j = 16, 1, 2, 5
+    q, _, v, _, _, state = _gdn_inputs(22, S, Hqk, Hv, 1)
+    k = np.zeros((1, Hqk, S), np.float32)
+    k[0, 0, j] = 1.0
+    g = np.full((1, Hv), -0.75, np.float32)
+    beta = np.ones((1, Hv), np.float32)
+    out, st, _ = oracle.gdn_recurrent(q, _bf(k), v, g, beta, state, S, Hqk, Hv, 1)
+    alpha = np.exp(np.float64(-0.75))
+    vf = syn.bf16_bits_to_f32(v).astype(np.float64).reshape(Hv, S)
+    np.testing.assert_allclose(st[:, :, j], vf, rtol=0, atol=1e-15)
+    others = [c for c in range(S) if c != j]
+    np.testing.assert_allclose(st[:, :, others], alpha * state[:, :, others].astype(np.float64), rtol=1e-15, atol=0)
+    qf = syn.bf16_bits_to_f32(q).astype(np.float64).reshape(S)
+    np.testing.assert_allclose(out[0], st @ qf / 4.0, rtol=1e-14, atol=1e-16)
+
+
+def test_gdn_zero_beta_is_pure_decay(oracle):
+    """beta = 0: the state only decays, S_T = exp(sum g) S_0, and out_t = scale S_t q_t."""
+    S, Hqk, Hv, T = 16, 2, 4, 3
+    q, k, v, g, _, state = _gdn_inputs(23, S, Hqk, Hv, T)
+    beta = np.zeros((T, Hv), np.float32)
+    out, st, snaps = oracle.gdn_recurrent(q, k, v, g, beta, state, S, Hqk, Hv, T, snapshots=True)
+    decay = np.exp(np.cumsum(g.astype(np.float64), axis=0))  # [T,Hv]
+    for t in range(T):
+        np.testing.assert_allclose(snaps[t], decay[t][:, None, None] * state, rtol=1e-13)
+
+
+def _conv_numpy(x, w, st):
+    """x [T,C], w [4,C], st [3,C] as floats."""
+    u = np.concatenate([st, x], axis=0)
+    T = x.shape[0]
+    acc = sum(w[j][None, :] * u[j:j + T] for j in range(4))
+    return acc / (1.0 + np.exp(-acc)), np.stack([u[t + 1:t + 4] for t in range(T)])
+
+
+def test_conv_oracle_vs_numpy_and_windows(oracle):
+    C, T = 37, 6
+    rng = np.random.default_rng(5)
+    x, w, st = _bf(rng.uniform(-2, 2, (T, C))), _bf(rng.uniform(-1, 1, (4, C))), _bf(rng.uniform(-2, 2, (3, C)))
+    out, win = oracle.causal_conv1d_silu(x, w, st, C, T)
+    f = lambda a: syn.bf16_bits_to_f32(a).astype(np.float64)  # noqa: E731
+    ro, rw = _conv_numpy(f(x), f(w), f(st))
+    np.testing.assert_allclose(out, ro, rtol=1e-13, atol=1e-15)
+    u = np.concatenate([st, x], axis=0)
+    for t in range(T):
+        assert np.array_equal(win[t], u[t + 1:t + 4])  # window after token t: u[t-2], u[t-1], u[t]
+
+
+@pytest.mark.parametrize("tap", [0, 3])
+def test_conv_one_hot_tap(oracle, tap):
+    """weight = e_tap: out[t] = SiLU(u[t - 3 + tap]) (tap 3 reads x[t], tap 0 reads the state for t < 3)."""
+    C, T = 8, 5
+    rng = np.random.default_rng(6)
+    x, st = _bf(rng.uniform(-3, 3, (T, C))), _bf(rng.uniform(-3, 3, (3, C)))
+    w = np.zeros((4, C), np.float32)
+    w[tap] = 1.0
+    out, _ = oracle.causal_conv1d_silu(x, _bf(w), st, C, T)
+    u = syn.bf16_bits_to_f32(np.concatenate([st, x], axis=0)).astype(np.float64)
+    a = u[tap:tap + T]
+    np.testing.assert_allclose(out, a / (1.0 + np.exp(-a)), rtol=1e-15, atol=0)
+
+
 # ---- argmax ---------------------------------------------------------------------------------------
 
 def test_argmax_brute_force(oracle):
