@@ -259,6 +259,69 @@ def general_launch(dev, stream):
                                    VOCAB, dev["cfg"].ptr, dev["ws"], stream)
 
 
+def lm_head_bytes(N: int, K: int, T: int) -> int:
+    """Bytes of one lm_head pass: the Q6 weight (32 + 16 + 2 B per 64 codes of every row), x, and
+    the BF16 logits when they are written (the fused argmax writes T ids instead)."""
+    G = (K + 127) // 128 * 2
+    return N * G * 50 + K * T * 2
+
+
+def lm_head_bench(stream, args):
+    """Q6G64_F16S output heads of the reference ([248320, 5120] 27B, [248320, 2048] 35B-A3B) over the
+    T = 4 verify columns: the fused linear -> argmax, and linear followed by argmax, each call
+    timed inside a captured graph of CALLS_PER_GRAPH calls. Weights from the reference's patterned
+    generator (random-like bytes; the time does not depend on them)."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd._capi import Q6G64_F16S
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    N, T = VOCAB, 4
+    res = {}
+    for K in (5120, 2048):
+        G = (K + 127) // 128 * 2
+        nb, hb, sb = N * G * 32, N * G * 16, N * G * 2
+        hoff = (nb + 255) // 256 * 256
+        soff = hoff + (hb + 255) // 256 * 256
+        buf = DeviceBuffer(soff + sb)
+        rng = np.random.default_rng(K)
+        chunk = 1 << 26
+        for off in range(0, soff + sb, chunk):  # random payload bytes, scales kept finite and small below
+            n = min(chunk, soff + sb - off)
+            buf.upload(rng.integers(0, 256, n, dtype=np.uint8), off)
+        buf.upload(np.full(N * G, 0x2C00, np.uint16).view(np.uint8), soff)  # scales 1/16
+        w = na.Weight()
+        w.payload, w.payload_bytes, w.high_plane_bytes = buf.ptr, soff + sb, hb
+        w.qtype, w.group_size, w.ndim = Q6G64_F16S, 64, 2
+        w.shape[:] = [N, K, 1, 1]
+        w.padded_shape[:] = [N, G * 64, 1, 1]
+        w.qdata, w.qhigh, w.scales = buf.ptr, buf.ptr + hoff, buf.ptr + soff
+        w.n, w.k, w.group, w.layout, w.scale_dtype = N, K, 64, 0, na.FP16
+        x = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, K * T).astype(np.float32)), (K, T))
+        logits = DeviceArray(na.BF16, (N, T))
+        ids = DeviceArray(na.I32, (T,))
+        ws = DeviceBuffer(ops.linear_argmax_workspace_bytes(T))
+
+        def fused():
+            ops.linear_argmax(x.tensor(), w, N, ws, ids.tensor(), stream)
+
+        def unfused():
+            ops.linear(x.tensor(), w, logits.tensor(), stream)
+            ops.argmax(logits.tensor(), ids.tensor(), N, stream)
+        out = {}
+        for name, fn in (("fused", fused), ("unfused", unfused)):
+            g = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
+            ms = time_graph(g, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
+            out[f"{name}_us"] = ms * 1e3
+            del g
+        byts = lm_head_bytes(N, K, T)
+        out["bytes"] = byts
+        out["fused_gbs"] = byts / (out["fused_us"] * 1e-6) / 1e9
+        out["fused_frac_of_peak"] = out["fused_gbs"] / HBM_PEAK_GBS
+        res[f"k{K}"] = out
+        del buf
+    return res
+
+
 GDN_S, GDN_HQK, GDN_HV, GDN_LAYERS = 128, 16, 48, 48  # Qwen3.6-27B (src/targets/qwen3_6_27b/impl/config.h:23-26)
 GDN_CONV = 2 * GDN_HQK * GDN_S + GDN_HV * GDN_S
 
@@ -357,7 +420,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "gdn", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "gdn", "lm_head", "copy"], default=None,
                     help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
                          "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
@@ -521,6 +584,16 @@ def main():
         result["gdn"] = gres
         log(f"GDN snapshot: {gres['us_per_layer']:.2f} us/layer, {gres['gbs']:.0f} GB/s")
 
+    # ---- lm_head: Q6 output head over the verify columns, fused with the argmax ------------------
+    if args.only in (None, "lm_head"):
+        lres = lm_head_bench(stream, args)
+        if args.only:
+            log(f"lm_head {lres}")
+            return
+        result["lm_head"] = lres
+        log("lm_head: " + ", ".join(f"K={k[1:]} fused {v['fused_us']:.1f} us ({v['fused_gbs']:.0f} GB/s), "
+                                    f"unfused {v['unfused_us']:.1f} us" for k, v in lres.items()))
+
     cpu = None
     if not args.skip_cpu:
         t0 = time.perf_counter()
@@ -560,6 +633,12 @@ def main():
             "workload": "C3 shape over a BF16 KV cache: context 260096, 1% outliers +-20, one layer "
                         "(new rows copied into the cache by their own launch, then attention)",
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3_bf16"].items()}}
+    if "lm_head" in result:
+        line["lm_head"] = {
+            "workload": "Q6G64_F16S output head [248320, K] over T=4 verify columns: fused linear->argmax "
+                        "(ids only) vs linear (BF16 logits) + argmax, per call in a graph of 10",
+            **{k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+               for k, v in result["lm_head"].items()}}
     if "gdn" in result:
         line["gdn_snapshot"] = {
             "workload": "48 hybrid layers of a verify step (T=4): conv1d+SiLU snapshot (C=10240) and Gated DeltaNet "

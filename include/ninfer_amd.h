@@ -102,6 +102,31 @@ typedef struct nmi_general_config {
     float top_p;
 } nmi_general_config;
 
+/* src/core/tensor.h:30-66 — the reference's quantized weight view, field for field. qtype values
+ * are ninfer::QType (Q4G64_F16S = 0, Q5G64_F16S = 1, Q6G64_F16S = 2, W8G32_F16S = 3), layout
+ * ninfer::QuantLayout (RowSplit = 0). */
+typedef struct nmi_weight {
+    const void* payload;
+    uint64_t payload_bytes;
+    uint64_t high_plane_bytes;
+    int32_t qtype;
+    uint32_t group_size;
+    int32_t shape[4];
+    int32_t padded_shape[4];
+    uint32_t ndim;
+    const void* qdata;
+    const void* qhigh;
+    const void* scales;
+    int32_t n;
+    int32_t k;
+    int32_t group;
+    int32_t layout;
+    int32_t scale_dtype; /* nmi_dtype */
+} nmi_weight;
+
+#define NMI_Q6G64_F16S 2
+#define NMI_ROW_SPLIT 0
+
 /* Thread-local text of the last non-OK status. */
 const char* nmi_last_error(void);
 /* Library build identification (architecture list and kernel set). */
@@ -231,6 +256,22 @@ int nmi_tree_accept_greedy(const nmi_tensor* parents, const nmi_tensor* node_tok
                            nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,
                            nmi_tensor* num_sampled, nmi_tensor* accepted, nmi_tensor* stats,
                            nmi_stream_t stream);
+
+/* ---------------------------------------------------------------- lm_head (logits of the verify columns) */
+
+/* Replaces linear (include/ninfer/ops/linear.h:27) for Q6G64_F16S RowSplit weights:
+ * out[n,t] = BF16(sum_k decode(w)[n,k] * x[k,t]), decode = 6-bit code * FP16 group scale. x BF16
+ * [K,T], out BF16 [N,T], T >= 1, padded K <= 8192 (the reference registers [248320,5120] and
+ * [248320,2048]; other shapes in range are also served). `ws` of the reference is not needed. */
+int nmi_linear(const nmi_tensor* x, const nmi_weight* w, nmi_tensor* out, nmi_stream_t stream);
+
+/* EXTENSION: the reference's deferred FUT-F03 linear_argmax
+ * (docs/maintainer/qwen3.6-35b-a3b-dflash-op-checklist.md:985-1001): out[t] = lowest v < valid_rows
+ * attaining max_v BF16(decode(w)[v,:] . x[:,t]), ties of -0 and +0 equal; the logits are never
+ * written. out I32 [T]. Workspace from nmi_linear_argmax_workspace_bytes. */
+size_t nmi_linear_argmax_workspace_bytes(int32_t tokens);
+int nmi_linear_argmax(const nmi_tensor* x, const nmi_weight* w, int32_t valid_rows, void* workspace,
+                      size_t workspace_bytes, nmi_tensor* out, nmi_stream_t stream);
 
 /* ---------------------------------------------------------------- recurrent state (hybrid layers) */
 

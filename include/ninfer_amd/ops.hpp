@@ -297,6 +297,31 @@ inline void tree_accept_greedy(const Tensor& parents, const Tensor& node_tokens,
                                          detail::st(stream)));
 }
 
+// ---- lm_head ----------------------------------------------------------------------------------------
+
+// include/ninfer/ops/linear.h:27 for Q6G64_F16S RowSplit weights. `w` is the reference's Weight
+// (src/core/tensor.h:47-66) copied field for field into nmi_weight by the binding.
+inline void linear(const Tensor& x, const nmi_weight& w, Tensor& out, WorkspaceArena& ws, hipStream_t stream) {
+    (void)ws;
+    const nmi_tensor cx = x.c();
+    nmi_tensor co = out.c();
+    detail::check(nmi_linear(&cx, &w, &co, detail::st(stream)));
+}
+
+// Extension: fused linear -> argmax (the reference's deferred FUT-F03 contract).
+[[nodiscard]] inline std::size_t linear_argmax_workspace_bytes(int32_t tokens) {
+    return nmi_linear_argmax_workspace_bytes(tokens);
+}
+inline void linear_argmax(const Tensor& x, const nmi_weight& w, int32_t valid_rows, WorkspaceArena& ws, Tensor& out,
+                          hipStream_t stream) {
+    const std::size_t need = linear_argmax_workspace_bytes(x.ne[1]);
+    auto scope = ws.scope();
+    void* p = ws.alloc_bytes(need);
+    const nmi_tensor cx = x.c();
+    nmi_tensor co = out.c();
+    detail::check(nmi_linear_argmax(&cx, &w, valid_rows, p, need, &co, detail::st(stream)));
+}
+
 // ---- recurrent state of the hybrid layers -------------------------------------------------------
 
 // include/ninfer/ops/gated_delta_rule.h:18-21

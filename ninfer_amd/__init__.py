@@ -10,10 +10,10 @@ from __future__ import annotations
 
 from . import _capi
 from ._capi import (BF16, FP16, FP32, I8, I32, I64, U8, CommitEnvelope, GeneralConfig, GqaEnvelope,
-                    KVLayerView, SamplingConfig, Tensor, lib)
+                    KVLayerView, SamplingConfig, Tensor, Weight, lib)
 
 __all__ = [
-    "BF16", "FP16", "FP32", "I8", "I32", "I64", "Tensor", "KVLayerView", "GqaEnvelope",
+    "BF16", "FP16", "FP32", "I8", "I32", "I64", "Tensor", "KVLayerView", "GqaEnvelope", "Weight",
     "CommitEnvelope", "SamplingConfig", "GeneralConfig", "lib", "build_info",
 ]
 

@@ -44,6 +44,33 @@ class Tensor(C.Structure):
         return t
 
 
+class Weight(C.Structure):
+    """nmi_weight (src/core/tensor.h:47-66), field for field."""
+
+    _fields_ = [
+        ("payload", C.c_void_p),
+        ("payload_bytes", C.c_uint64),
+        ("high_plane_bytes", C.c_uint64),
+        ("qtype", C.c_int32),
+        ("group_size", C.c_uint32),
+        ("shape", C.c_int32 * 4),
+        ("padded_shape", C.c_int32 * 4),
+        ("ndim", C.c_uint32),
+        ("qdata", C.c_void_p),
+        ("qhigh", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("n", C.c_int32),
+        ("k", C.c_int32),
+        ("group", C.c_int32),
+        ("layout", C.c_int32),
+        ("scale_dtype", C.c_int32),
+    ]
+
+
+Q6G64_F16S = 2
+ROW_SPLIT = 0
+
+
 class KVLayerView(C.Structure):
     """nmi_kv_layer_view (src/core/kv_cache.h:13-24)."""
 
@@ -110,6 +137,9 @@ _SIGNATURES = {
     "nmi_speculative_accept_general": (C.c_int, [_T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, C.c_int32, C.c_void_p, C.c_void_p, C.c_size_t, _STREAM]),
     "nmi_speculative_select_accepted_hidden": (C.c_int, [_T, _T, _T, _STREAM]),
     "nmi_mtp_prepare_alignment_ids": (C.c_int, [_T, _T, _T, _T, _STREAM]),
+    "nmi_linear": (C.c_int, [_T, P(Weight), _T, _STREAM]),
+    "nmi_linear_argmax_workspace_bytes": (C.c_size_t, [C.c_int32]),
+    "nmi_linear_argmax": (C.c_int, [_T, P(Weight), C.c_int32, C.c_void_p, C.c_size_t, _T, _STREAM]),
     "nmi_gated_delta_rule_workspace_bytes": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, P(C.c_size_t)]),
     "nmi_gated_delta_rule": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),
     "nmi_gated_delta_rule_snapshot": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),

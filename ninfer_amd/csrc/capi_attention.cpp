@@ -207,7 +207,8 @@ const char* nmi_build_info(void) {
            "verify_attn_partial_bf16<{1,2},{128,256}> bf16-MFMA 16x16x32 (BF16 KV), "
            "verify_attn_merge, kv_quant_append, bf16_kv_append, argmax, speculative accept (greedy, top-20 "
            "stochastic, general fixed-point), kv commit/rollback/compaction, gdn_recurrent<{16,32,64,128}> "
-           "(snapshot), conv1d_silu (snapshot), device scalars";
+           "(snapshot), conv1d_silu (snapshot), device scalars, linear_q6<{4,8,16} cols> f16-MFMA (Q6G64 lm_head, "
+           "fused argmax)";
 }
 
 size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,

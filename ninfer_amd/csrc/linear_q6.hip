@@ -1,0 +1,372 @@
+// Q6G64_F16S RowSplit linear (the lm_head of the verify step) and its fused argmax, gfx950.
+//
+// Contract (reference include/ninfer/ops/linear.h:10-27): out[n,t] = BF16(sum_k W[n,k] x[k,t]) with
+// W exactly decoded, code * FP16 scale per group of 64 along K. Storage (reference test packer
+// tests/ops/row_split_pack.h:143-195): per row, groups of 64 codes; the nibble plane holds 32 B per
+// group (code i in byte i/2, low nibble for even i), the high plane 16 B per group (bits 2i, 2i+1 of
+// the group's little-endian bit stream), the scale plane one FP16 per group; a code is the
+// sign-extended 6-bit value. The fused form (the reference's deferred FUT-F03 `linear_argmax`,
+// docs/maintainer/qwen3.6-35b-a3b-dflash-op-checklist.md:985-1001) returns, per column, the lowest
+// row attaining the maximum BF16 logit among rows [0, valid_rows), without writing the logits.
+//
+// One persistent workgroup per CU; each wave streams 16-row tiles of the weight by LDS-DMA (a
+// two-stage ring of 8-group chunks: 4 KB of nibbles, 2 KB of high bits, 256 B of scales) and runs
+// v_mfma_f32_16x16x32_f16 with x staged once per workgroup in LDS. A lane decodes 16 codes of one
+// row from one 8-byte nibble read and one 4-byte high read: each FP16 pair is built by bit
+// operations as 0x6400 | (code + 32) = 1056 + code, then one packed subtraction of 1056 leaves the
+// code itself, exactly, in the pairing (e, e + 4) of 8 codes. x is stored in LDS in the same order
+// as FP16, each column scaled by a power of two that puts its largest magnitude in [2^14, 2^15),
+// so every BF16 value of x is exact in FP16. The MFMA sums exact products in FP32 per group; the
+// group result times its FP16 scale is accumulated in FP32, and the column factor is undone
+// exactly at the end, so only FP32 summation rounds (the reference's tensor-core route rounds W to
+// BF16 first).
+#include "common.h"
+#include "device_utils.h"
+#include "lds_dma.h"
+#include "linear_internal.h"
+
+#include <algorithm>
+
+namespace nmi {
+namespace {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kTileRows = 16;
+constexpr int kChunkGroups = 8;
+constexpr int kNibStage = kTileRows * kChunkGroups * 32;  // 4096 B
+constexpr int kHighStage = kTileRows * kChunkGroups * 16; // 2048 B
+constexpr int kScaleStage = kTileRows * kChunkGroups * 2; // 256 B
+constexpr int kStageBytes = kNibStage + kHighStage + kScaleStage;
+constexpr int kDmaPerChunk = 4 + 2 + 1;
+constexpr int kXPad = 64;     // bytes between x columns in LDS (spreads the columns over the banks)
+
+__device__ __forceinline__ size_t x_lds_bytes(int TP, int Kp) { return static_cast<size_t>(TP) * (Kp * 2 + kXPad); }
+
+// 16 codes (elements 16b .. 16b + 15 of a group) -> two MFMA A operands of 8 FP16 codes each, in
+// the order (e0, e4, e1, e5, e2, e6, e3, e7) of each 8-code half.
+__device__ __forceinline__ void decode16(uint64_t nib, uint32_t hi, h8& a0, h8& a1) {
+    hi ^= 0xaaaaaaaau; // flips bit 5 of every code: (code & 63) ^ 32 = code + 32
+    const uint32_t hs0 = __builtin_amdgcn_perm(0u, hi, 0x0c010c00u); // high bytes 0, 1 -> bytes 0, 2
+    const uint32_t hs1 = __builtin_amdgcn_perm(0u, hi, 0x0c030c02u);
+    const uint32_t n0 = static_cast<uint32_t>(nib);
+    const uint32_t n1 = static_cast<uint32_t>(nib >> 32);
+    const h2 bias = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+    h2 c0[4], c1[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t h0 = p < 2 ? (hs0 << (4 - 2 * p)) : (hs0 >> (2 * p - 4));
+        const uint32_t h1 = p < 2 ? (hs1 << (4 - 2 * p)) : (hs1 >> (2 * p - 4));
+        const uint32_t w0 = ((n0 >> (4 * p)) & 0x000f000fu) | (h0 & 0x00300030u) | 0x64006400u;
+        const uint32_t w1 = ((n1 >> (4 * p)) & 0x000f000fu) | (h1 & 0x00300030u) | 0x64006400u;
+        c0[p] = __builtin_bit_cast(h2, w0) - bias; // 1056 + code - 1056: exact
+        c1[p] = __builtin_bit_cast(h2, w1) - bias;
+    }
+    a0 = __builtin_bit_cast(h8, c0);
+    a1 = __builtin_bit_cast(h8, c1);
+}
+
+// 64-bit argmax key of one BF16 logit: ordered value (larger = greater as a float, -0 = +0), then the
+// lower row. 0 is below every real key.
+__device__ __forceinline__ uint64_t logit_key(uint16_t b, int row) {
+    if (b == 0x8000u) { b = 0; }
+    const uint32_t ord = (b & 0x8000u) ? (~static_cast<uint32_t>(b) & 0xffffu) : (static_cast<uint32_t>(b) | 0x8000u);
+    return (static_cast<uint64_t>(ord) << 32) | (0xffffffffu - static_cast<uint32_t>(row));
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, 64);
+    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, 64);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Per-lane DMA source offsets within a tile (fixed for the kernel). Nibble DMA d covers rows
+// 4d .. 4d+3 (16 lanes x 16 B per row); LDS slot s of row r holds piece s ^ r. High DMA d covers
+// rows 8d .. 8d+7 (8 lanes per row); slot s of row r holds piece s ^ (r / 2 % 8). Scales: lane ->
+// (row lane / 4, 4-byte piece lane % 4).
+struct LinDma {
+    int n[4];
+    int h[2];
+    int s;
+};
+
+__device__ __forceinline__ LinDma make_lin_dma(int lane, int G) {
+    LinDma d;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int row = 4 * q + lane / 16;
+        const int slot = lane % 16;
+        d.n[q] = row * (G * 32) + 16 * (slot ^ row);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int row = 8 * q + lane / 8;
+        const int slot = lane % 8;
+        d.h[q] = row * (G * 16) + 16 * (slot ^ ((row >> 1) & 7));
+    }
+    d.s = (lane / 4) * (G * 2) + 4 * (lane % 4);
+    return d;
+}
+
+struct Planes {
+    __amdgpu_buffer_rsrc_t n, h, s;
+};
+
+// The whole source offset rides in the range-checked voffset (soffset is not checked), so rows past
+// N and groups past G at the end of a plane read as zero instead of past the allocation.
+__device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, const LinDma& d, int tile, int chunk,
+                                           int G) {
+    const int r0 = tile * kTileRows;
+    const int o_n = r0 * (G * 32) + chunk * (kChunkGroups * 32);
+    const int o_h = r0 * (G * 16) + chunk * (kChunkGroups * 16);
+    const int o_s = r0 * (G * 2) + chunk * (kChunkGroups * 2);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) { dma16(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) { dma16(pl.h, st + kNibStage + q * 1024, d.h[q] + o_h, 0); }
+    dma4s(pl.s, st + kNibStage + kHighStage, d.s + o_s, 0);
+}
+
+template <int TP, int W>
+__global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char dsmem[];
+    NMI_AS3 char* smem = (NMI_AS3 char*)dsmem;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int G = a.G;
+    const int xstride = a.Kp * 2 + kXPad;
+    NMI_AS3 char* xl = smem;
+    NMI_AS3 uint32_t* cmax = (NMI_AS3 uint32_t*)(smem + x_lds_bytes(TP, a.Kp)); // per column: max |x| (BF16 bits)
+    NMI_AS3 float* cfac = (NMI_AS3 float*)(cmax + TP);                         // per column: power-of-two factor
+    const size_t ring0 = (x_lds_bytes(TP, a.Kp) + static_cast<size_t>(TP) * 8 + 15) & ~static_cast<size_t>(15);
+    NMI_AS3 char* ring = smem + ring0 + static_cast<size_t>(wave) * 2 * kStageBytes;
+
+    // ---- x of this pass -> LDS as FP16, each 8-element block stored as (e0, e4, e1, e5, e2, e6, e3,
+    // e7); columns past the pass and elements past K are zero. Two passes over x (it is small):
+    // the column maxima, then the scaled values.
+    const int kb = a.Kp / 8;
+    const bool vec = (a.K & 7) == 0;
+    auto load8 = [&](int t, int k0, uint16_t (&v)[8]) {
+        if (t < a.tp && vec && k0 + 8 <= a.K) {
+            const i4 raw = *reinterpret_cast<const i4*>(a.x + k0 + static_cast<int64_t>(a.K) * (a.t0 + t));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) { v[e] = static_cast<uint16_t>(static_cast<uint32_t>(raw[e >> 1]) >> (16 * (e & 1))); }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[e] = (t < a.tp && k0 + e < a.K) ? a.x[k0 + e + static_cast<int64_t>(a.K) * (a.t0 + t)] : 0;
+            }
+        }
+    };
+    if (threadIdx.x < TP) { cmax[threadIdx.x] = 0; }
+    __syncthreads();
+    for (int i = threadIdx.x; i < TP * kb; i += 64 * W) {
+        const int t = i / kb;
+        uint16_t v[8];
+        load8(t, (i - t * kb) * 8, v);
+        uint32_t m = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { m = max(m, static_cast<uint32_t>(v[e] & 0x7fffu)); } // |x| orders as its bits
+        if (m != 0) { atomicMax((uint32_t*)&cmax[t], m); }
+    }
+    __syncthreads();
+    if (threadIdx.x < TP) {
+        // factor = 2^(14 - floor(log2 max|x|)): max|x| lands in [2^14, 2^15) and every BF16 value of the
+        // column is exact in FP16 down to 2^-28 of the maximum (clamped so the factor stays finite).
+        const uint32_t m = cmax[threadIdx.x];
+        float f = 1.0f;
+        if (m != 0 && m < 0x7f80u) { f = ldexpf(1.0f, 14 - max(static_cast<int>(m >> 7) - 127, -100)); }
+        cfac[threadIdx.x] = f;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < TP * kb; i += 64 * W) {
+        const int t = i / kb;
+        const int blk = i - t * kb;
+        uint16_t v[8];
+        load8(t, blk * 8, v);
+        const float f = cfac[t];
+        h2 pk[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            pk[p] = h2{static_cast<_Float16>(bf16_to_f32(v[p]) * f), static_cast<_Float16>(bf16_to_f32(v[p + 4]) * f)};
+        }
+        *(NMI_AS3 i4*)(xl + t * xstride + blk * 16) = __builtin_bit_cast(i4, pk);
+    }
+    __syncthreads();
+
+    const int gw = blockIdx.x * W + wave; // wave index of the launch
+    const int nch = (G + kChunkGroups - 1) / kChunkGroups;
+    const int ntw = gw < a.ntiles ? (a.ntiles - gw + a.waves - 1) / a.waves : 0;
+    const int items = ntw * nch;
+    const Planes pl{raw_buffer(a.qdata, a.nib_bytes), raw_buffer(a.qhigh, a.high_bytes), raw_buffer(a.scales, a.scale_bytes)};
+    const LinDma dl = make_lin_dma(lane, G);
+    const int c = lane & 15;  // MFMA column (x column) of this lane
+    const int b = lane >> 4;  // 16-code block of a group / accumulator row block
+
+    if (items > 0) { issue_item(ring, pl, dl, gw, 0, G); }
+    if (items > 1) { issue_item(ring + kStageBytes, pl, dl, gw + (1 / nch) * a.waves, 1 % nch, G); }
+
+    float tot[4] = {0.f, 0.f, 0.f, 0.f};
+    uint64_t best = 0;
+#pragma unroll 1
+    for (int j = 0; j < items; ++j) {
+        const int tile = gw + (j / nch) * a.waves;
+        const int chunk = j % nch;
+        NMI_AS3 char* st = ring + (j & 1) * kStageBytes;
+        if (j + 1 < items) {
+            __builtin_amdgcn_s_waitcnt((kDmaPerChunk & 0xf) | ((kDmaPerChunk >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+        } else {
+            __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));
+        }
+        // chunk j -> registers, then the stage takes chunk j + 2
+        uint64_t nib[kChunkGroups];
+        uint32_t hig[kChunkGroups];
+        i4 sc[4];
+        const int r = c; // A-operand row of this lane
+#pragma unroll
+        for (int gl = 0; gl < kChunkGroups; ++gl) {
+            nib[gl] = *(const NMI_AS3 uint64_t*)(st + r * 256 + 16 * ((2 * gl + (b >> 1)) ^ r) + 8 * (b & 1));
+            hig[gl] = *(const NMI_AS3 uint32_t*)(st + kNibStage + r * 128 + 16 * (gl ^ ((r >> 1) & 7)) + 4 * b);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { sc[i] = *(const NMI_AS3 i4*)(st + kNibStage + kHighStage + (4 * b + i) * 16); }
+        if (j + 2 < items) {
+            __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
+            issue_item(st, pl, dl, gw + ((j + 2) / nch) * a.waves, (j + 2) % nch, G);
+        }
+        const int ng = min(kChunkGroups, G - chunk * kChunkGroups);
+#pragma unroll
+        for (int gl = 0; gl < kChunkGroups; ++gl) {
+            if (gl < ng) {
+                const int ga = chunk * kChunkGroups + gl;
+                h8 a0, a1;
+                decode16(nib[gl], hig[gl], a0, a1);
+                i4 x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
+                if (c < TP) {
+                    const NMI_AS3 char* xp = xl + c * xstride + (8 * ga + 2 * b) * 16;
+                    x0 = *(const NMI_AS3 i4*)xp;
+                    x1 = *(const NMI_AS3 i4*)(xp + 16);
+                }
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w = static_cast<uint32_t>(sc[i][gl >> 1]);
+                    const float s = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
+                    tot[i] = fmaf(s, acc[i], tot[i]);
+                }
+            }
+        }
+        if (chunk == nch - 1) {
+            // tile done: lane holds rows 4b + i, column c
+            const int r0 = tile * kTileRows;
+            const float inv = c < TP ? 1.0f / cfac[c] : 0.0f; // a power of two: exact
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = r0 + 4 * b + i;
+                const uint16_t bfv = f32_to_bf16_bits(tot[i] * inv);
+                if (a.out != nullptr && c < a.tp && row < a.N) {
+                    a.out[row + static_cast<int64_t>(a.N) * (a.t0 + c)] = bfv;
+                }
+                if (row < a.valid_rows) { best = max_u64(best, logit_key(bfv, row)); }
+                tot[i] = 0.0f;
+            }
+        }
+    }
+    if (a.keys != nullptr) {
+        best = max_u64(best, shfl_xor_u64(best, 16));
+        best = max_u64(best, shfl_xor_u64(best, 32));
+        if (lane < a.tp) { a.keys[static_cast<int64_t>(a.t0 + lane) * a.waves + gw] = best; }
+    }
+}
+
+// One workgroup per column: the largest partial key -> the row.
+__global__ __launch_bounds__(256) void linear_argmax_reduce_kernel(const uint64_t* keys, int32_t waves, int32_t* out) {
+    const int t = blockIdx.x;
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < waves; i += 256) { best = max_u64(best, keys[static_cast<int64_t>(t) * waves + i]); }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) { best = max_u64(best, shfl_xor_u64(best, m)); }
+    __shared__ uint64_t wb[4];
+    if ((threadIdx.x & 63) == 0) { wb[threadIdx.x >> 6] = best; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        best = max_u64(max_u64(wb[0], wb[1]), max_u64(wb[2], wb[3]));
+        out[t] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(best));
+    }
+}
+
+size_t lds_bytes(int TP, int W, int Kp, int G) {
+    (void)G;
+    const size_t x = static_cast<size_t>(TP) * (Kp * 2 + kXPad) + static_cast<size_t>(TP) * 8;
+    return ((x + 15) & ~static_cast<size_t>(15)) + static_cast<size_t>(W) * 2 * kStageBytes;
+}
+
+} // namespace
+
+LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T) {
+    const int32_t G = Kp / 64;
+    const int32_t ntiles = (N + kTileRows - 1) / kTileRows;
+    constexpr size_t kLds = 160 * 1024;
+    // (columns per pass, waves) in order of preference; the first whose LDS map fits is taken.
+    static constexpr int kCand[4][2] = {{16, 4}, {8, 4}, {4, 8}, {4, 4}};
+    const int first = T <= 4 ? 2 : (T <= 8 ? 1 : 0);
+    LinearPlan p{};
+    for (int i = first; i < 4; ++i) {
+        p.tp = kCand[i][0];
+        p.waves = kCand[i][1];
+        if (lds_bytes(p.tp, p.waves, Kp, G) <= kLds) { break; }
+    }
+    p.lds = lds_bytes(p.tp, p.waves, Kp, G);
+    p.passes = (T + p.tp - 1) / p.tp;
+    p.grid = std::max<int32_t>(1, std::min<int32_t>(kLinearGrid, (ntiles + p.waves - 1) / p.waves));
+    return p;
+}
+
+size_t linear_argmax_workspace_bytes(int32_t T) {
+    return static_cast<size_t>(T) * kLinearGrid * kLinearMaxWaves * sizeof(uint64_t);
+}
+
+template <int TP, int W>
+void allow_lds() {
+    static const bool done = [] {
+        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_kernel<TP, W>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        return true;
+    }();
+    (void)done;
+}
+
+void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream) {
+    a.ntiles = (a.N + kTileRows - 1) / kTileRows;
+    a.waves = p.grid * p.waves;
+    allow_lds<4, 8>();
+    allow_lds<4, 4>();
+    allow_lds<8, 4>();
+    allow_lds<16, 4>();
+    for (int32_t pass = 0; pass < p.passes; ++pass) {
+        a.t0 = pass * p.tp;
+        a.tp = std::min(p.tp, a.T - a.t0);
+        const dim3 grid(p.grid), block(64 * p.waves);
+        if (p.tp == 4 && p.waves == 8) {
+            hipLaunchKernelGGL((linear_q6_kernel<4, 8>), grid, block, p.lds, stream, a);
+        } else if (p.tp == 4) {
+            hipLaunchKernelGGL((linear_q6_kernel<4, 4>), grid, block, p.lds, stream, a);
+        } else if (p.tp == 8) {
+            hipLaunchKernelGGL((linear_q6_kernel<8, 4>), grid, block, p.lds, stream, a);
+        } else {
+            hipLaunchKernelGGL((linear_q6_kernel<16, 4>), grid, block, p.lds, stream, a);
+        }
+        check_launch("linear_q6_kernel");
+    }
+}
+
+void launch_linear_argmax_reduce(const uint64_t* keys, int32_t T, int32_t waves, int32_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(linear_argmax_reduce_kernel, dim3(T), dim3(256), 0, stream, keys, waves, out);
+    check_launch("linear_argmax_reduce_kernel");
+}
+
+} // namespace nmi

@@ -36,8 +36,7 @@
 #include <cmath>
 #include <type_traits>
 
-#define NMI_AS1 __attribute__((address_space(1)))
-#define NMI_AS3 __attribute__((address_space(3)))
+#include "lds_dma.h"
 
 namespace nmi {
 namespace {
@@ -162,10 +161,6 @@ struct HeadBuffers {
     __amdgpu_buffer_rsrc_t k, v, ks, vs;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int64_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
-}
-
 // Per-lane DMA source offsets, fixed for the whole kernel. One 1 KB code DMA covers 1024 / D rows;
 // lane -> (row lane / PIECES, slot lane % PIECES). K slot s of row r holds piece s ^ (r % PIECES),
 // and r % PIECES depends on the DMA's index when a DMA covers fewer than PIECES rows (D = 256:
@@ -199,16 +194,6 @@ __device__ __forceinline__ DmaLanes make_dma_lanes(int lane) {
 // codes go through soffset, which moves only the source address; the LDS address is M0 + 16 * lane
 // (4 * lane for scales). Both scale loads run on the full wave: lane-divergent descriptors would
 // turn one DMA into a waterfall loop.
-// One LDS-DMA instruction: 16 bytes (or 4 for scales) per lane from rsrc + voffset + soffset into
-// lds + 16 * lane (4 * lane). Plain functions: the host compile pass rejects these builtins inside
-// function templates.
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char* lds, int voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NMI_AS3 void*)lds, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char* lds, int voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NMI_AS3 void*)lds, 4, voff, 0, 0, 0);
-}
-
 template <int D>
 __device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers& hb, const DmaLanes& dl,
                                             int c0, int lane) {

@@ -120,6 +120,23 @@ def tree_accept_greedy(parents, node_tokens, target_tokens, path, path_len, leng
                                        _p(num_sampled), _p(accepted), _p(stats), _s(stream)))
 
 
+# ---- lm_head (linear.h + the fused linear -> argmax) ----------------------------------------------
+
+def linear(x, weight, out, stream=None) -> None:
+    """include/ninfer/ops/linear.h:27 (Q6G64_F16S RowSplit weights)."""
+    check(lib().nmi_linear(_p(x), C.byref(weight), _p(out), _s(stream)))
+
+
+def linear_argmax_workspace_bytes(tokens) -> int:
+    return lib().nmi_linear_argmax_workspace_bytes(tokens)
+
+
+def linear_argmax(x, weight, valid_rows, ws, out, stream=None) -> None:
+    """Fused linear -> argmax (the reference's deferred FUT-F03 contract)."""
+    check(lib().nmi_linear_argmax(_p(x), C.byref(weight), int(valid_rows), C.c_void_p(ws.ptr), ws.nbytes, _p(out),
+                                  _s(stream)))
+
+
 # ---- recurrent state of the hybrid layers (gated_delta_rule.h, causal_conv1d_silu.h, scalar.h) --
 
 def gated_delta_rule_workspace_bytes(head_dim, qk_heads, value_heads, tokens, normalize_qk) -> int:

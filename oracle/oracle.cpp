@@ -349,6 +349,52 @@ void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16
     });
 }
 
+// ---- lm_head: Q6G64_F16S RowSplit linear ----------------------------------------------------------
+
+// Restates unpack_lowbit_code (tests/ops/row_split_pack.h:174-192) for 6-bit codes: the low nibble
+// of code i sits in byte i/2 (high half for odd i), its two high bits at bit 2i of the group's high
+// bytes, and the 6-bit value is sign-extended.
+static int q6_code(const uint8_t* nib, const uint8_t* high, int i) {
+    const uint32_t low = (i & 1) ? (nib[i >> 1] >> 4) : (nib[i >> 1] & 0x0fu);
+    const uint32_t hi = (high[(2 * i) >> 3] >> ((2 * i) & 7)) & 0x03u;
+    const uint32_t u = low | (hi << 4);
+    return (u & 0x20u) ? static_cast<int>(u) - 64 : static_cast<int>(u);
+}
+
+// include/ninfer/ops/linear.h:17-20: exact decode, naive FP64 dot products.
+void orc_linear_q6(const uint8_t* qdata, const uint8_t* qhigh, const uint16_t* scales, int32_t N,
+                   int32_t K, const uint16_t* x, int32_t T, double* out, int32_t threads) {
+    const int32_t Kp = (K + 127) / 128 * 128;
+    const int32_t G = Kp / 64;
+    std::vector<double> xf(static_cast<size_t>(K) * T);
+    for (size_t i = 0; i < xf.size(); ++i) { xf[i] = static_cast<double>(bf16(x[i])); }
+    auto rows = [&](int32_t r0, int32_t r1) {
+        std::vector<double> w(K);
+        for (int32_t n = r0; n < r1; ++n) {
+            for (int32_t k = 0; k < K; ++k) {
+                const size_t g = static_cast<size_t>(n) * G + k / 64;
+                const int code = q6_code(qdata + g * 32, qhigh + g * 16, k % 64);
+                w[k] = static_cast<double>(code) * static_cast<double>(orc_f16_bits_to_f32(scales[g]));
+            }
+            for (int32_t t = 0; t < T; ++t) {
+                const double* xt = xf.data() + static_cast<size_t>(t) * K;
+                double acc = 0.0;
+                for (int32_t k = 0; k < K; ++k) { acc += w[k] * xt[k]; }
+                out[n + static_cast<size_t>(N) * t] = acc;
+            }
+        }
+    };
+    int32_t nt = threads > 0 ? threads : static_cast<int32_t>(std::thread::hardware_concurrency());
+    nt = std::max(1, std::min(nt, N));
+    std::vector<std::thread> pool;
+    for (int32_t w = 0; w < nt; ++w) {
+        const int32_t r0 = static_cast<int32_t>(static_cast<int64_t>(N) * w / nt);
+        const int32_t r1 = static_cast<int32_t>(static_cast<int64_t>(N) * (w + 1) / nt);
+        pool.emplace_back(rows, r0, r1);
+    }
+    for (auto& th : pool) { th.join(); }
+}
+
 // ---- recurrent state of the hybrid layers -----------------------------------------------------
 
 // Restates gdn_ref::forward_recurrent (tests/ops/gdn_ref.h:342-410) for one sequence, with the

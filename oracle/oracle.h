@@ -60,6 +60,13 @@ void orc_attention_bf16(const uint16_t* q, const uint16_t* k_cache, const uint16
                         int32_t Hq, int32_t Hkv, int32_t D, int32_t padded_context, double scale,
                         double* out, int32_t threads);
 
+// ---- lm_head: Q6G64_F16S RowSplit linear ----------------------------------------------------------
+// out[n + N*t] = sum_k decode(w)[n,k] * bf16(x[k + K*t]) in FP64, decode = sign-extended 6-bit code
+// times the group's FP16 scale, exactly. qdata: N x G x 32 B, qhigh: N x G x 16 B, scales: N x G
+// FP16, G = align_up(K, 128) / 64. `threads` <= 0 uses hardware_concurrency.
+void orc_linear_q6(const uint8_t* qdata, const uint8_t* qhigh, const uint16_t* scales, int32_t N,
+                   int32_t K, const uint16_t* x, int32_t T, double* out, int32_t threads);
+
 // ---- recurrent state of the hybrid layers -----------------------------------------------------
 // Gated DeltaNet recurrence in FP64 (one sequence). q/k BF16 [S,Hqk,T], v BF16 [S,Hv,T], g/beta
 // FP32 [Hv,T], state_in FP32 [S,S,Hv] (row = value index, key index fastest). normalize_qk: q and

@@ -130,6 +130,18 @@ def attention_bf16(q, kb, vb, positions, parents, T, B, Hq, Hkv, D, P, scale, th
     return out
 
 
+def linear_q6(qdata, qhigh, scales, N, K, x, T, threads=0):
+    """FP64 Q6 linear: [T, N] doubles (before the BF16 boundary). x uint16 BF16 [T, K]."""
+    qdata = np.ascontiguousarray(qdata, dtype=np.uint8)
+    qhigh = np.ascontiguousarray(qhigh, dtype=np.uint8)
+    scales = np.ascontiguousarray(scales, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out = np.zeros(N * T, dtype=np.float64)
+    lib().orc_linear_q6(_ptr(qdata), _ptr(qhigh), _ptr(scales), C.c_int32(N), C.c_int32(K), _ptr(x), C.c_int32(T),
+                        _ptr(out), C.c_int32(threads))
+    return out.reshape(T, N)
+
+
 def gdn_recurrent(q, k, v, g, beta, state, S, Hqk, Hv, T, normalize_qk=False, snapshots=False):
     """FP64 Gated DeltaNet recurrence: (out [T,Hv,S], state_out [Hv,S,S], snapshots [T,Hv,S,S] or None)."""
     q = np.ascontiguousarray(q, dtype=np.uint16)

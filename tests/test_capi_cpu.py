@@ -249,6 +249,56 @@ def test_conv_and_scalar_validation():
         ops.increment_i64_scalar(A(na.I32, (1,)))
 
 
+def _q6_weight(n=248320, k=5120, base=0x10000000):
+    G = (k + 127) // 128 * 2
+    nb, hb, sb = n * G * 32, n * G * 16, n * G * 2
+    hoff = (nb + 255) // 256 * 256
+    soff = hoff + (hb + 255) // 256 * 256
+    w = na.Weight()
+    w.payload, w.payload_bytes, w.high_plane_bytes = base, soff + sb, hb
+    w.qtype, w.group_size, w.ndim = 2, 64, 2
+    w.shape[:] = [n, k, 1, 1]
+    w.padded_shape[:] = [n, G * 64, 1, 1]
+    w.qdata, w.qhigh, w.scales = base, base + hoff, base + soff
+    w.n, w.k, w.group, w.layout, w.scale_dtype = n, k, 64, 0, na.FP16
+    return w
+
+
+def test_linear_validation():
+    # src/ops/linear/linear.cpp:65-152 and the Q6 alignment rule :200-209
+    x, out = _t(na.BF16, (5120, 4), 0x100000), _t(na.BF16, (248320, 4), 0x200000)
+    w = _q6_weight()
+    w.payload_bytes -= 1
+    with pytest.raises(ValueError, match="payload is too small"):
+        ops.linear(x, w, out)
+    w = _q6_weight()
+    w.padded_shape[1] = 5248
+    with pytest.raises(ValueError, match="padded shape is invalid"):
+        ops.linear(x, w, out)
+    w = _q6_weight()
+    w.qtype = 0
+    with pytest.raises(ValueError, match="only Q6G64_F16S"):
+        ops.linear(x, w, out)
+    w = _q6_weight()
+    w.scales += 2
+    with pytest.raises(ValueError, match="alignment"):
+        ops.linear(x, w, out)
+    with pytest.raises(ValueError, match="x K dimension"):
+        ops.linear(_t(na.BF16, (2048, 4), 0x100000), _q6_weight(), out)
+    with pytest.raises(ValueError, match="out must have shape"):
+        ops.linear(x, _q6_weight(), _t(na.BF16, (248320, 3), 0x200000))
+    w = _q6_weight(k=16384)
+    with pytest.raises(NotImplementedError, match="padded K <= 8192"):
+        ops.linear(_t(na.BF16, (16384, 4), 0x100000), w, out)
+    ws = _WS(ops.linear_argmax_workspace_bytes(4))
+    with pytest.raises(ValueError, match="valid_rows"):
+        ops.linear_argmax(x, _q6_weight(), 248321, ws, _t(na.I32, (4,), 0x300000))
+    with pytest.raises(ValueError, match="workspace"):
+        ops.linear_argmax(x, _q6_weight(), 248320, _WS(1024), _t(na.I32, (4,), 0x300000))
+    with pytest.raises(ValueError, match="I32"):
+        ops.linear_argmax(x, _q6_weight(), 248320, ws, _t(na.BF16, (4,), 0x300000))
+
+
 def test_argmax_validation():
     with pytest.raises(ValueError, match="valid_rows"):
         ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (4,)), 101)

@@ -264,6 +264,66 @@ def test_attention_bf16_stress_closed_form(oracle):
     assert np.array_equal(out, expect)
 
 
+# ---- lm_head: Q6G64_F16S RowSplit linear ---------------------------------------------------------
+
+def test_q6_packer_known_bytes():
+    """One group holding codes -32 .. 31 in order: by the packer's definition
+    (tests/ops/row_split_pack.h:143-172) code i = i - 32 has u = i ^ 32, so byte j of the nibble plane
+    is (u(2j) & 15) | (u(2j+1) & 15) << 4 and each high byte packs four 2-bit fields: codes -32..-17
+    give 0xAA, -16..-1 give 0xFF, 0..15 give 0x00, 16..31 give 0x55."""
+    import q6_pack as qp
+    codes = np.arange(-32, 32).reshape(1, 64)
+    nib, high = qp.pack_codes(codes)
+    u = np.arange(64) ^ 32
+    assert np.array_equal(nib[0, 0], ((u[0::2] & 15) | ((u[1::2] & 15) << 4)).astype(np.uint8))
+    assert np.array_equal(high[0, 0], np.array([0xAA] * 4 + [0xFF] * 4 + [0x00] * 4 + [0x55] * 4, np.uint8))
+    assert np.array_equal(qp.unpack_codes(nib, high), codes)
+
+
+def test_q6_patterned_generator_known_values():
+    """make_patterned_weight (tests/ops/row_split_pack.h:228-285) by hand: row 3 (mix 3), group 2,
+    seed 4226: nibble byte b = (3*37 + 2*29 + 17b + 4226) & 255 = 43 + 17b, high byte b =
+    (3*43 + 2*31 + 13b + 3*4226) & 255; scale index (3 ^ 2 ^ 4226) & 3 = 3 -> 0x3d00."""
+    import q6_pack as qp
+    nib, high, sc = qp.patterned(8, 300, 4226)
+    assert list(nib[3, 2, :3]) == [43, 60, 77]
+    assert high[3, 2, 1] == (3 * 43 + 2 * 31 + 13 + 3 * 4226) & 255
+    assert sc[3, 2] == 0x3D00
+    nib2, _, _ = qp.patterned(301, 64, 7)  # row 300: mix = 300 ^ (300 >> 8) = 301
+    assert nib2[300, 0, 0] == ((300 ^ 1) * 37 + 7) & 255
+
+
+def test_linear_q6_oracle_unit_columns(oracle):
+    """x = unit columns e_{k_t}: out[t, n] is exactly code[n, k_t] * scale[n, k_t / 64] (pins the
+    oracle's decode of every nibble and high-bit position against the packer)."""
+    import q6_pack as qp
+    rng = np.random.default_rng(12)
+    N, K = 37, 200
+    Kp = qp.align_up(K, 128)
+    codes = rng.integers(-32, 32, (N, Kp))
+    nib, high = qp.pack_codes(codes)
+    sc = np.float16(rng.uniform(0.01, 2.0, (N, Kp // 64))).view(np.uint16)
+    ks = np.arange(K)
+    T = K
+    x = np.zeros((T, K), np.uint16)
+    x[np.arange(T), ks] = 0x3F80  # BF16 1.0
+    out = oracle.linear_q6(nib, high, sc, N, K, x, T)
+    expect = codes[:, ks].T * sc.view(np.float16).astype(np.float64)[:, ks // 64].T
+    assert np.array_equal(out, expect)
+
+
+def test_linear_q6_oracle_vs_numpy(oracle):
+    import q6_pack as qp
+    rng = np.random.default_rng(13)
+    N, K, T = 50, 384, 3
+    nib, high, sc = qp.patterned(N, K, 99)
+    codes = qp.unpack_codes(nib, high)[:, :K].astype(np.float64)
+    w = codes * np.repeat(sc.view(np.float16).astype(np.float64), 64, axis=1)[:, :K]
+    x = syn.f32_to_bf16_bits(rng.uniform(-1, 1, (T, K)).astype(np.float32))
+    out = oracle.linear_q6(nib, high, sc, N, K, x, T)
+    np.testing.assert_allclose(out, (w @ syn.bf16_bits_to_f32(x).astype(np.float64).T).T, rtol=1e-12, atol=1e-12)
+
+
 # ---- recurrent state (Gated DeltaNet, causal conv1d) ----------------------------------------------
 
 def _bf(x):
