@@ -661,6 +661,9 @@ def main():
         "bytes_per_launch": attn_bytes(7680),
         "traffic_detail": traffic,
     }
+    if "lm_head" in line:
+        tl = measured_traffic("lm_head_k5120")
+        line["lm_head"]["k5120"]["traffic"] = tl["bytes"] if tl else None
     if "gdn_snapshot" in line:
         tg = measured_traffic("gdn")
         line["gdn_snapshot"]["traffic"] = tg["bytes"] if tg else None

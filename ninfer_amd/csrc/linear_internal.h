@@ -8,7 +8,7 @@
 namespace nmi {
 
 inline constexpr int kLinearGrid = 256;       // persistent workgroups (one per CU)
-inline constexpr int kLinearMaxWaves = 8;     // waves per workgroup
+inline constexpr int kLinearMaxWaves = 16;    // waves per workgroup
 inline constexpr int kLinearMaxPaddedK = 8192;
 
 struct LinearArgs {
@@ -30,6 +30,7 @@ struct LinearArgs {
 struct LinearPlan {
     int32_t tp;      // 4, 8 or 16
     int32_t waves;   // per workgroup
+    int32_t cg;      // groups of 64 codes per streamed chunk (4 or 8)
     int32_t grid;    // workgroups
     size_t lds;
     int32_t passes;

@@ -33,13 +33,30 @@ namespace {
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kTileRows = 16;
-constexpr int kChunkGroups = 8;
-constexpr int kNibStage = kTileRows * kChunkGroups * 32;  // 4096 B
-constexpr int kHighStage = kTileRows * kChunkGroups * 16; // 2048 B
-constexpr int kScaleStage = kTileRows * kChunkGroups * 2; // 256 B
-constexpr int kStageBytes = kNibStage + kHighStage + kScaleStage;
-constexpr int kDmaPerChunk = 4 + 2 + 1;
 constexpr int kXPad = 64;     // bytes between x columns in LDS (spreads the columns over the banks)
+constexpr int kOutOfRange = 0x40000000; // a DMA source offset past every plane: reads zero
+
+// One streamed chunk of a 16-row tile: CG groups (64 codes each) of every row. LDS stage: nibble
+// rows (CG * 32 B), high rows (CG * 16 B), then scales (CG * 2 B per row) in one full-wave 4-byte
+// DMA slot of 256 B. A row of R bytes holds R / 16 pieces of 16 B; piece p of row r sits at slot
+// p ^ sw(r), sw(r) = (r / (256 / R)) % (R / 16): rows whose bank phase coincides get distinct
+// slots, so the 16 lanes of one column of rows read conflict-free.
+template <int CG>
+struct Chunk {
+    static constexpr int kNibRow = CG * 32;
+    static constexpr int kHighRow = CG * 16;
+    static constexpr int kScaleRow = CG * 2;
+    static constexpr int kNib = kTileRows * kNibRow;
+    static constexpr int kHigh = kTileRows * kHighRow;
+    static constexpr int kStage = kNib + kHigh + 256;
+    static constexpr int kNibDma = kNib / 1024;
+    static constexpr int kHighDma = kHigh / 1024;
+    static constexpr int kDma = kNibDma + kHighDma + 1;
+    static_assert(kNib % 1024 == 0 && kHigh % 1024 == 0 && kTileRows * kScaleRow <= 256, "chunk geometry");
+};
+
+template <int R>
+__device__ __forceinline__ int swz(int row) { return (row / (256 / R)) % (R / 16); }
 
 __device__ __forceinline__ size_t x_lds_bytes(int TP, int Kp) { return static_cast<size_t>(TP) * (Kp * 2 + kXPad); }
 
@@ -86,27 +103,33 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
 // 4d .. 4d+3 (16 lanes x 16 B per row); LDS slot s of row r holds piece s ^ r. High DMA d covers
 // rows 8d .. 8d+7 (8 lanes per row); slot s of row r holds piece s ^ (r / 2 % 8). Scales: lane ->
 // (row lane / 4, 4-byte piece lane % 4).
+template <int CG>
 struct LinDma {
-    int n[4];
-    int h[2];
+    int n[Chunk<CG>::kNibDma];
+    int h[Chunk<CG>::kHighDma];
     int s;
 };
 
-__device__ __forceinline__ LinDma make_lin_dma(int lane, int G) {
-    LinDma d;
+template <int CG>
+__device__ __forceinline__ LinDma<CG> make_lin_dma(int lane, int G) {
+    using C = Chunk<CG>;
+    LinDma<CG> d;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int row = 4 * q + lane / 16;
-        const int slot = lane % 16;
-        d.n[q] = row * (G * 32) + 16 * (slot ^ row);
+    for (int q = 0; q < C::kNibDma; ++q) {
+        constexpr int P = C::kNibRow / 16;
+        const int row = (1024 / C::kNibRow) * q + lane / P;
+        const int slot = lane % P;
+        d.n[q] = row * (G * 32) + 16 * (slot ^ swz<C::kNibRow>(row));
     }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        const int row = 8 * q + lane / 8;
-        const int slot = lane % 8;
-        d.h[q] = row * (G * 16) + 16 * (slot ^ ((row >> 1) & 7));
+    for (int q = 0; q < C::kHighDma; ++q) {
+        constexpr int P = C::kHighRow / 16;
+        const int row = (1024 / C::kHighRow) * q + lane / P;
+        const int slot = lane % P;
+        d.h[q] = row * (G * 16) + 16 * (slot ^ swz<C::kHighRow>(row));
     }
-    d.s = (lane / 4) * (G * 2) + 4 * (lane % 4);
+    constexpr int SL = C::kScaleRow / 4; // 4-byte scale words per row
+    d.s = lane < kTileRows * SL ? (lane / SL) * (G * 2) + 4 * (lane % SL) : kOutOfRange;
     return d;
 }
 
@@ -116,21 +139,24 @@ struct Planes {
 
 // The whole source offset rides in the range-checked voffset (soffset is not checked), so rows past
 // N and groups past G at the end of a plane read as zero instead of past the allocation.
-__device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, const LinDma& d, int tile, int chunk,
+template <int CG>
+__device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, const LinDma<CG>& d, int tile, int chunk,
                                            int G) {
+    using C = Chunk<CG>;
     const int r0 = tile * kTileRows;
-    const int o_n = r0 * (G * 32) + chunk * (kChunkGroups * 32);
-    const int o_h = r0 * (G * 16) + chunk * (kChunkGroups * 16);
-    const int o_s = r0 * (G * 2) + chunk * (kChunkGroups * 2);
+    const int o_n = r0 * (G * 32) + chunk * C::kNibRow;
+    const int o_h = r0 * (G * 16) + chunk * C::kHighRow;
+    const int o_s = r0 * (G * 2) + chunk * C::kScaleRow;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) { dma16(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
+    for (int q = 0; q < C::kNibDma; ++q) { dma16(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
 #pragma unroll
-    for (int q = 0; q < 2; ++q) { dma16(pl.h, st + kNibStage + q * 1024, d.h[q] + o_h, 0); }
-    dma4s(pl.s, st + kNibStage + kHighStage, d.s + o_s, 0);
+    for (int q = 0; q < C::kHighDma; ++q) { dma16(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
+    dma4s(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
 }
 
-template <int TP, int W>
+template <int TP, int W, int CG>
 __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
+    using CH = Chunk<CG>;
     extern __shared__ __attribute__((aligned(16))) char dsmem[];
     NMI_AS3 char* smem = (NMI_AS3 char*)dsmem;
     const int lane = threadIdx.x & 63;
@@ -141,7 +167,7 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     NMI_AS3 uint32_t* cmax = (NMI_AS3 uint32_t*)(smem + x_lds_bytes(TP, a.Kp)); // per column: max |x| (BF16 bits)
     NMI_AS3 float* cfac = (NMI_AS3 float*)(cmax + TP);                         // per column: power-of-two factor
     const size_t ring0 = (x_lds_bytes(TP, a.Kp) + static_cast<size_t>(TP) * 8 + 15) & ~static_cast<size_t>(15);
-    NMI_AS3 char* ring = smem + ring0 + static_cast<size_t>(wave) * 2 * kStageBytes;
+    NMI_AS3 char* ring = smem + ring0 + static_cast<size_t>(wave) * 2 * CH::kStage;
 
     // ---- x of this pass -> LDS as FP16, each 8-element block stored as (e0, e4, e1, e5, e2, e6, e3,
     // e7); columns past the pass and elements past K are zero. Two passes over x (it is small):
@@ -197,16 +223,16 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     __syncthreads();
 
     const int gw = blockIdx.x * W + wave; // wave index of the launch
-    const int nch = (G + kChunkGroups - 1) / kChunkGroups;
+    const int nch = (G + CG - 1) / CG;
     const int ntw = gw < a.ntiles ? (a.ntiles - gw + a.waves - 1) / a.waves : 0;
     const int items = ntw * nch;
     const Planes pl{raw_buffer(a.qdata, a.nib_bytes), raw_buffer(a.qhigh, a.high_bytes), raw_buffer(a.scales, a.scale_bytes)};
-    const LinDma dl = make_lin_dma(lane, G);
+    const LinDma<CG> dl = make_lin_dma<CG>(lane, G);
     const int c = lane & 15;  // MFMA column (x column) of this lane
     const int b = lane >> 4;  // 16-code block of a group / accumulator row block
 
-    if (items > 0) { issue_item(ring, pl, dl, gw, 0, G); }
-    if (items > 1) { issue_item(ring + kStageBytes, pl, dl, gw + (1 / nch) * a.waves, 1 % nch, G); }
+    if (items > 0) { issue_item<CG>(ring, pl, dl, gw, 0, G); }
+    if (items > 1) { issue_item<CG>(ring + CH::kStage, pl, dl, gw + (1 / nch) * a.waves, 1 % nch, G); }
 
     float tot[4] = {0.f, 0.f, 0.f, 0.f};
     uint64_t best = 0;
@@ -214,33 +240,39 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     for (int j = 0; j < items; ++j) {
         const int tile = gw + (j / nch) * a.waves;
         const int chunk = j % nch;
-        NMI_AS3 char* st = ring + (j & 1) * kStageBytes;
+        NMI_AS3 char* st = ring + (j & 1) * CH::kStage;
         if (j + 1 < items) {
-            __builtin_amdgcn_s_waitcnt((kDmaPerChunk & 0xf) | ((kDmaPerChunk >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+            __builtin_amdgcn_s_waitcnt((CH::kDma & 0xf) | ((CH::kDma >> 4) << 14) | (0x7 << 4) | (0xf << 8));
         } else {
             __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xf << 8));
         }
         // chunk j -> registers, then the stage takes chunk j + 2
-        uint64_t nib[kChunkGroups];
-        uint32_t hig[kChunkGroups];
-        i4 sc[4];
+        uint64_t nib[CG];
+        uint32_t hig[CG];
+        uint32_t sc[4][CG / 2];
         const int r = c; // A-operand row of this lane
 #pragma unroll
-        for (int gl = 0; gl < kChunkGroups; ++gl) {
-            nib[gl] = *(const NMI_AS3 uint64_t*)(st + r * 256 + 16 * ((2 * gl + (b >> 1)) ^ r) + 8 * (b & 1));
-            hig[gl] = *(const NMI_AS3 uint32_t*)(st + kNibStage + r * 128 + 16 * (gl ^ ((r >> 1) & 7)) + 4 * b);
+        for (int gl = 0; gl < CG; ++gl) {
+            nib[gl] = *(const NMI_AS3 uint64_t*)(st + r * CH::kNibRow + 16 * ((2 * gl + (b >> 1)) ^ swz<CH::kNibRow>(r)) +
+                                                 8 * (b & 1));
+            hig[gl] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + r * CH::kHighRow + 16 * (gl ^ swz<CH::kHighRow>(r)) + 4 * b);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { sc[i] = *(const NMI_AS3 i4*)(st + kNibStage + kHighStage + (4 * b + i) * 16); }
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int q = 0; q < CG / 2; ++q) {
+                sc[i][q] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + CH::kHigh + (4 * b + i) * CH::kScaleRow + 4 * q);
+            }
+        }
         if (j + 2 < items) {
             __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
-            issue_item(st, pl, dl, gw + ((j + 2) / nch) * a.waves, (j + 2) % nch, G);
+            issue_item<CG>(st, pl, dl, gw + ((j + 2) / nch) * a.waves, (j + 2) % nch, G);
         }
-        const int ng = min(kChunkGroups, G - chunk * kChunkGroups);
+        const int ng = min(CG, G - chunk * CG);
 #pragma unroll
-        for (int gl = 0; gl < kChunkGroups; ++gl) {
+        for (int gl = 0; gl < CG; ++gl) {
             if (gl < ng) {
-                const int ga = chunk * kChunkGroups + gl;
+                const int ga = chunk * CG + gl;
                 h8 a0, a1;
                 decode16(nib[gl], hig[gl], a0, a1);
                 i4 x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
@@ -254,7 +286,7 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint32_t w = static_cast<uint32_t>(sc[i][gl >> 1]);
+                    const uint32_t w = sc[i][gl >> 1];
                     const float s = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
                     tot[i] = fmaf(s, acc[i], tot[i]);
                 }
@@ -299,28 +331,40 @@ __global__ __launch_bounds__(256) void linear_argmax_reduce_kernel(const uint64_
     }
 }
 
-size_t lds_bytes(int TP, int W, int Kp, int G) {
-    (void)G;
+size_t lds_bytes(int TP, int W, int CG, int Kp) {
     const size_t x = static_cast<size_t>(TP) * (Kp * 2 + kXPad) + static_cast<size_t>(TP) * 8;
-    return ((x + 15) & ~static_cast<size_t>(15)) + static_cast<size_t>(W) * 2 * kStageBytes;
+    const size_t stage = CG == 8 ? Chunk<8>::kStage : Chunk<4>::kStage;
+    return ((x + 15) & ~static_cast<size_t>(15)) + static_cast<size_t>(W) * 2 * stage;
 }
 
 } // namespace
 
+// Built instances (columns per pass, waves per workgroup, groups per chunk), in order of preference
+// (measured on MI355X: 8 waves with 8-group chunks stream best; 4-group chunks free the LDS that
+// 16 columns of x need; fewer columns per pass re-stream the weight). The first whose LDS map fits
+// is taken, starting from the column class of T.
+struct LinearInstance {
+    int tp, waves, cg;
+};
+constexpr LinearInstance kInstances[] = {
+    {16, 8, 4}, {16, 4, 4},                                    // T > 8
+    {8, 8, 8}, {8, 8, 4}, {8, 4, 8}, {8, 4, 4},                // T in 5..8 (T > 8 when x is too large)
+    {4, 8, 8}, {4, 16, 4}, {4, 8, 4}, {4, 4, 4},               // T <= 4 (and the last resort)
+};
+constexpr int kInstanceCount = sizeof(kInstances) / sizeof(kInstances[0]);
+
 LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T) {
-    const int32_t G = Kp / 64;
     const int32_t ntiles = (N + kTileRows - 1) / kTileRows;
     constexpr size_t kLds = 160 * 1024;
-    // (columns per pass, waves) in order of preference; the first whose LDS map fits is taken.
-    static constexpr int kCand[4][2] = {{16, 4}, {8, 4}, {4, 8}, {4, 4}};
-    const int first = T <= 4 ? 2 : (T <= 8 ? 1 : 0);
+    const int first = T <= 4 ? 6 : (T <= 8 ? 2 : 0);
     LinearPlan p{};
-    for (int i = first; i < 4; ++i) {
-        p.tp = kCand[i][0];
-        p.waves = kCand[i][1];
-        if (lds_bytes(p.tp, p.waves, Kp, G) <= kLds) { break; }
+    for (int i = first; i < kInstanceCount; ++i) {
+        p.tp = kInstances[i].tp;
+        p.waves = kInstances[i].waves;
+        p.cg = kInstances[i].cg;
+        p.lds = lds_bytes(p.tp, p.waves, p.cg, Kp);
+        if (p.lds <= kLds) { break; }
     }
-    p.lds = lds_bytes(p.tp, p.waves, Kp, G);
     p.passes = (T + p.tp - 1) / p.tp;
     p.grid = std::max<int32_t>(1, std::min<int32_t>(kLinearGrid, (ntiles + p.waves - 1) / p.waves));
     return p;
@@ -330,37 +374,41 @@ size_t linear_argmax_workspace_bytes(int32_t T) {
     return static_cast<size_t>(T) * kLinearGrid * kLinearMaxWaves * sizeof(uint64_t);
 }
 
-template <int TP, int W>
-void allow_lds() {
-    static const bool done = [] {
-        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_kernel<TP, W>),
+template <int TP, int W, int CG>
+void launch_instance(const LinearArgs& a, const LinearPlan& p, hipStream_t stream) {
+    static const bool lds_raised = [] {
+        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_kernel<TP, W, CG>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         return true;
     }();
-    (void)done;
+    (void)lds_raised;
+    hipLaunchKernelGGL((linear_q6_kernel<TP, W, CG>), dim3(p.grid), dim3(64 * W), p.lds, stream, a);
 }
 
 void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream) {
     a.ntiles = (a.N + kTileRows - 1) / kTileRows;
     a.waves = p.grid * p.waves;
-    allow_lds<4, 8>();
-    allow_lds<4, 4>();
-    allow_lds<8, 4>();
-    allow_lds<16, 4>();
     for (int32_t pass = 0; pass < p.passes; ++pass) {
         a.t0 = pass * p.tp;
         a.tp = std::min(p.tp, a.T - a.t0);
-        const dim3 grid(p.grid), block(64 * p.waves);
-        if (p.tp == 4 && p.waves == 8) {
-            hipLaunchKernelGGL((linear_q6_kernel<4, 8>), grid, block, p.lds, stream, a);
-        } else if (p.tp == 4) {
-            hipLaunchKernelGGL((linear_q6_kernel<4, 4>), grid, block, p.lds, stream, a);
-        } else if (p.tp == 8) {
-            hipLaunchKernelGGL((linear_q6_kernel<8, 4>), grid, block, p.lds, stream, a);
-        } else {
-            hipLaunchKernelGGL((linear_q6_kernel<16, 4>), grid, block, p.lds, stream, a);
-        }
-        check_launch("linear_q6_kernel");
+#define NMI_LINEAR_CASE(TP, W, CG)                                                                            \
+    if (p.tp == TP && p.waves == W && p.cg == CG) {                                                           \
+        launch_instance<TP, W, CG>(a, p, stream);                                                             \
+        check_launch("linear_q6_kernel");                                                                     \
+        continue;                                                                                             \
+    }
+        NMI_LINEAR_CASE(16, 8, 4)
+        NMI_LINEAR_CASE(16, 4, 4)
+        NMI_LINEAR_CASE(8, 8, 8)
+        NMI_LINEAR_CASE(8, 8, 4)
+        NMI_LINEAR_CASE(8, 4, 8)
+        NMI_LINEAR_CASE(8, 4, 4)
+        NMI_LINEAR_CASE(4, 16, 4)
+        NMI_LINEAR_CASE(4, 8, 8)
+        NMI_LINEAR_CASE(4, 8, 4)
+        NMI_LINEAR_CASE(4, 4, 4)
+#undef NMI_LINEAR_CASE
+        throw Unsupported("linear: no built kernel instance for this plan");
     }
 }
 
