@@ -10,8 +10,10 @@ already resident in HBM.
 
 Also measured in the same run: the long-context layer (configs[2], "C3": context 260,096, 1%
 outliers at +-20), the top-20 stochastic sampler at batch 1 and batch 16 (configs[3] sampler
-shape: temperature 0.7, top-p 0.95, N(0, 3) logits), and the CPU oracle on the host as a reported
-baseline.
+shape: temperature 0.7, top-p 0.95, N(0, 3) logits), the configs[3] batch step ("C4": batched
+attention over 16 ragged contexts, rollback, prefix commit), the configs[4] tree verify ("C5":
+8 x 16-node trees, tree attention, longest-path selection, compaction), and the CPU oracle on the
+host as a reported baseline.
 
 Prints ONE JSON line. `value` is the C2 verify attention's achieved HBM bandwidth (algorithmic
 bytes / time, GB/s).
@@ -259,6 +261,150 @@ def general_launch(dev, stream):
                                    VOCAB, dev["cfg"].ptr, dev["ws"], stream)
 
 
+def fill_batch_cache(cache, L_max: int, seed: int, chunk: int = 2048) -> None:
+    """History rows [0, L_max) of every sequence of a batch cache: one generated block of BF16
+    N(0,1) K and V columns [D, Hkv, chunk, B], quantized into each run of `chunk` rows by the append
+    op (rows past a sequence's own length are never visible to it)."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, synchronize
+    B = cache.batch
+    rng = np.random.default_rng(seed)
+    n = D * HKV * chunk * B
+    kb = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32)), (D, HKV, chunk, B))
+    vb = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(n, dtype=np.float32)), (D, HKV, chunk, B))
+    for start in range(0, L_max, chunk):
+        rows = np.arange(start, start + chunk, dtype=np.int32)
+        rows[rows >= L_max] = -1  # skipped by the append
+        dp = DeviceArray.from_numpy(na.I32, np.tile(rows, B), (chunk, B))
+        ops.gqa_kv_append(kb.tensor(), vb.tensor(), dp.tensor(), cache.view())
+    synchronize()
+
+
+def batch_attn_bytes(Ls, T_: int) -> int:
+    """Algorithmic bytes of one batched layer: codes+scales of every sequence's L_b+T visible keys,
+    plus per sequence the Q read, output write, new BF16 K/V read and new codes+scales written."""
+    per_seq = D * HQ * T_ * 2 * 2 + D * HKV * T_ * 2 * 2 + T_ * HKV * 2 * (D + 2 * (D // 64))
+    return sum((int(L) + T_) * BYTES_PER_TOKEN for L in Ls) + len(Ls) * per_seq
+
+
+def c4_bench(stream, args) -> dict:
+    """B = 16, contexts uniform in [1K, 32K], q_len 4, INT8-G64 KV. One layer of batched
+    verify attention (A1, per-sequence positions), then the commit side: the rollback of rejected
+    rows and the INT8 prefix commit, each per call inside a graph. The stochastic acceptance of the
+    same batch is the sampler section (B = 16)."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    from ninfer_amd.kv_cache import KVCacheLayer
+    B = 16
+    rng = np.random.default_rng(404)
+    Ls = rng.integers(1024, 32768, size=B, endpoint=True)
+    max_ctx = int(Ls.max()) + T
+    t0 = time.perf_counter()
+    cache = KVCacheLayer(max_ctx, HKV, D, B)
+    fill_batch_cache(cache, int(Ls.max()), seed=405)
+    q = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * T * B, dtype=np.float32)), (D, HQ, T, B))
+    kn = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * T * B, dtype=np.float32)), (D, HKV, T, B))
+    vn = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * T * B, dtype=np.float32)), (D, HKV, T, B))
+    pos_host = (Ls[:, None] + np.arange(T)[None, :]).astype(np.int32)
+    pos = DeviceArray.from_numpy(na.I32, pos_host.reshape(-1), (T, B))
+    out = DeviceArray(na.BF16, (D, HQ, T, B))
+    env = (1, max_ctx)
+    ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, B, max_ctx))
+    view = cache.view()
+    log(f"C4: batch cache (B={B}, contexts {int(Ls.min())}..{int(Ls.max())}) generated in {time.perf_counter() - t0:.1f}s")
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+
+    def attn():
+        ops.gqa_attention(q.tensor(), kn.tensor(), vn.tensor(), pos.tensor(), scale, view, env, ws, out.tensor(), stream)
+    reps = 4
+    g = capture(stream, lambda: [attn() for _ in range(reps)])
+    ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)
+    attn_us = ms * 1e3 / reps
+    nbytes = batch_attn_bytes(Ls, T)
+    # commit side: keep A_b + 1 rows of the 4 written (seeded accept counts), roll back the rest
+    keep = DeviceArray.from_numpy(na.I32, rng.integers(1, T + 1, size=B).astype(np.int32), (B,))
+    g_rb = capture(stream, lambda: [ops.kv_cache_rollback(pos.tensor(), keep.tensor(), view, stream)
+                                    for _ in range(CALLS_PER_GRAPH)])
+    rb_us = time_graph(g_rb, stream, args.steps, args.warmup)[0] * 1e3 / CALLS_PER_GRAPH
+    g_cp = capture(stream, lambda: [ops.kv_cache_append_prefix(kn.tensor(), vn.tensor(), pos.tensor(), keep.tensor(),
+                                                               (0, T), view, stream) for _ in range(CALLS_PER_GRAPH)])
+    cp_us = time_graph(g_cp, stream, args.steps, args.warmup)[0] * 1e3 / CALLS_PER_GRAPH
+    del g, g_rb, g_cp, cache
+    return dict(attn_us=attn_us, attn_us_p95=p95 * 1e3 / reps, attn_bytes=nbytes,
+                attn_gbs=nbytes / (attn_us * 1e-6) / 1e9, attn_frac_of_peak=nbytes / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                rollback_us=rb_us, commit_prefix_us=cp_us, contexts=[int(x) for x in Ls])
+
+
+def c5_bench(stream, args) -> dict:
+    """B = 8 draft trees of 16 nodes (binary, depth 4, the first 16 nodes in BFS order),
+    contexts log-uniform in [1K, 128K]. Tree verify attention (A1 with the ancestor mask, new rows
+    written), greedy longest accepted root-to-leaf path, and compaction of that path's INT8 K/V into
+    contiguous rows, each per call inside a graph."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    from ninfer_amd.kv_cache import KVCacheLayer
+    B, N = 8, 16
+    rng = np.random.default_rng(505)
+    Ls = np.exp(rng.uniform(np.log(1024), np.log(131072), size=B)).astype(np.int64)
+    max_ctx = int(Ls.max()) + N
+    t0 = time.perf_counter()
+    cache = KVCacheLayer(max_ctx, HKV, D, B)
+    fill_batch_cache(cache, int(Ls.max()), seed=506)
+    parents = np.array([-1] + [(u - 1) // 2 for u in range(1, N)], np.int32)
+    q = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * N * B, dtype=np.float32)), (D, HQ, N, B))
+    kn = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * N * B, dtype=np.float32)), (D, HKV, N, B))
+    vn = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HKV * N * B, dtype=np.float32)), (D, HKV, N, B))
+    pos = DeviceArray.from_numpy(na.I32, (Ls[:, None] + np.arange(N)[None, :]).astype(np.int32).reshape(-1), (N, B))
+    par = DeviceArray.from_numpy(na.I32, np.tile(parents, B), (N, B))
+    out = DeviceArray(na.BF16, (D, HQ, N, B))
+    env = (1, max_ctx)
+    ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, N, B, max_ctx))
+    view = cache.view()
+    log(f"C5: batch cache (B={B}, contexts {int(Ls.min())}..{int(Ls.max())}) generated in {time.perf_counter() - t0:.1f}s")
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+
+    def attn():
+        ops.gqa_attention_tree(q.tensor(), kn.tensor(), vn.tensor(), pos.tensor(), par.tensor(), scale, view, env, True,
+                               ws, out.tensor(), stream)
+    reps = 4
+    g = capture(stream, lambda: [attn() for _ in range(reps)])
+    ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)
+    attn_us = ms * 1e3 / reps
+    nbytes = batch_attn_bytes(Ls, N)
+    # greedy path selection: node tokens agree with their parent's target w.p. 0.8
+    tt = rng.integers(0, VOCAB, size=(B, N)).astype(np.int32)
+    nt = np.zeros((B, N), np.int32)
+    for b in range(B):
+        for u in range(1, N):
+            nt[b, u] = tt[b, parents[u]] if rng.random() < 0.8 else int(rng.integers(0, VOCAB))
+    d_nt = DeviceArray.from_numpy(na.I32, nt.reshape(-1), (N, B))
+    d_tt = DeviceArray.from_numpy(na.I32, tt.reshape(-1), (N, B))
+    path, plen = DeviceArray(na.I32, (N, B)), DeviceArray(na.I32, (B,))
+    length = DeviceArray.from_numpy(na.I32, Ls.astype(np.int32), (B,))
+    token, so, ns, acc = DeviceArray(na.I32, (B,)), DeviceArray(na.I32, (N, B)), DeviceArray(na.I32, (B,)), DeviceArray(na.I32, (B,))
+    stats = DeviceArray.from_numpy(na.I64, np.zeros((B, 4 + N), np.int64), (4 + N, B))
+    base = DeviceArray.from_numpy(na.I32, Ls.astype(np.int32), (B,))
+
+    def accept():
+        ops.tree_accept_greedy(par.tensor(), d_nt.tensor(), d_tt.tensor(), path.tensor(), plen.tensor(), length.tensor(),
+                               token.tensor(), so.tensor(), ns.tensor(), acc.tensor(), stats.tensor(), stream)
+    g_acc = capture(stream, lambda: [accept() for _ in range(CALLS_PER_GRAPH)])
+    acc_us = time_graph(g_acc, stream, args.steps, args.warmup)[0] * 1e3 / CALLS_PER_GRAPH
+    accept()
+    stream.synchronize()
+    g_cp = capture(stream, lambda: [ops.kv_cache_compact_path(base.tensor(), path.tensor(), plen.tensor(), view, stream)
+                                    for _ in range(CALLS_PER_GRAPH)])
+    cp_us = time_graph(g_cp, stream, args.steps, args.warmup)[0] * 1e3 / CALLS_PER_GRAPH
+    path_lens = [int(x) for x in plen.numpy()]
+    del g, g_acc, g_cp, cache
+    return dict(attn_us=attn_us, attn_us_p95=p95 * 1e3 / reps, attn_bytes=nbytes,
+                attn_gbs=nbytes / (attn_us * 1e-6) / 1e9, attn_frac_of_peak=nbytes / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                tree_accept_us=acc_us, compact_us=cp_us, path_lengths=path_lens, contexts=[int(x) for x in Ls])
+
+
 def lm_head_bytes(N: int, K: int, T: int) -> int:
     """Bytes of one lm_head pass: the Q6 weight (32 + 16 + 2 B per 64 codes of every row), x, and
     the BF16 logits when they are written (the fused argmax writes T ids instead)."""
@@ -420,7 +566,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "gdn", "lm_head", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "c4", "c5", "gdn", "lm_head", "copy"], default=None,
                     help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
                          "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
@@ -575,6 +721,24 @@ def main():
         log(f"sampler: B=1 {sres['b1_us']:.1f} us, B=16 {sres['b16_us_per_seq']:.2f} us/seq; "
             f"Mode F B=1 {sres['mode_f_b1_us']:.1f} us, B=16 {sres['mode_f_b16_us_per_seq']:.2f} us/seq")
 
+    # ---- C4 batch step (attention over ragged contexts, commit side) and C5 tree verify ----------
+    if args.only in (None, "c4"):
+        r4 = c4_bench(stream, args)
+        log(f"C4: attention B=16 {r4['attn_us']:.1f} us ({r4['attn_gbs']:.0f} GB/s), rollback {r4['rollback_us']:.2f} us, "
+            f"prefix commit {r4['commit_prefix_us']:.2f} us")
+        if args.only:
+            return
+        result["c4"] = r4
+        device.synchronize()
+    if args.only in (None, "c5"):
+        r5 = c5_bench(stream, args)
+        log(f"C5: tree attention B=8 x 16 nodes {r5['attn_us']:.1f} us ({r5['attn_gbs']:.0f} GB/s), tree accept "
+            f"{r5['tree_accept_us']:.2f} us, compaction {r5['compact_us']:.2f} us, paths {r5['path_lengths']}")
+        if args.only:
+            return
+        result["c5"] = r5
+        device.synchronize()
+
     # ---- hybrid layers: GDN recurrent state over the verify tokens (snapshot per token) ----------
     if args.only in (None, "gdn"):
         gres = gdn_bench(stream, args)
@@ -648,6 +812,18 @@ def main():
         line["sampler"] = {"workload": "stochastic accept, K=3, vocab 248320, T=0.7, top-p 0.95: Mode R (top-20 cap) "
                                        "and Mode F (full vocabulary, draft logits correlated 0.9)",
                            **{k: round(v, 2) for k, v in result["sampler"].items()}}
+    def rounded(d):
+        return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+    if "c4" in result:
+        line["batch_stochastic"] = {
+            "workload": "C4: batch 16, contexts uniform in [1K, 32K], q_len 4, INT8-G64 KV: one batched verify "
+                        "attention layer (A1), rollback of rejected rows, INT8 prefix commit (acceptance: sampler b16)",
+            **rounded(result["c4"])}
+    if "c5" in result:
+        line["tree_verify"] = {
+            "workload": "C5: batch 8, 16-node draft trees (binary, depth 4), contexts log-uniform in [1K, 128K]: "
+                        "tree attention (ancestor mask, new rows written), greedy longest path, INT8 path compaction",
+            **rounded(result["c5"])}
     traffic = measured_traffic("c2")
     line["roofline"] = {
         "bound": "hbm",

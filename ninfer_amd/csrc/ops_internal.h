@@ -28,9 +28,12 @@ struct SplitPlan {
     int32_t tokens_per_chunk = 0; // tokens whose G rows fit one 32-row MFMA tile pair
     int32_t row_chunks = 0;
     int32_t nsplit = 0;           // key splits per (sequence, row chunk, KV head)
-    int32_t keys_per_split = 0;   // multiple of 128
+    int32_t keys_per_split = 0;   // multiple of 128 (B == 1)
+    int32_t split_slots = 0;      // partial slots per (row chunk, KV head)
+    int32_t split_budget = 0;     // B > 1: most splits per (row chunk, KV head) the device cuts the batch into
     size_t part_o_offset = 0;
     size_t part_ml_offset = 0;
+    size_t seq_table_offset = 0; // B > 1: per sequence (first slot, split count)
     size_t bytes = 0;
 };
 

@@ -101,8 +101,9 @@ struct AttnArgs {
     uint16_t* vs;
     const uint16_t* kb; // BF16 cache planes (BF16 kernel only)
     const uint16_t* vb;
-    float* part_o;  // [unit][nsplit][32][D]
-    float* part_ml; // [unit][nsplit][32][2]
+    float* part_o;  // [row chunk][KV head][split_slots][32][D]
+    float* part_ml; // [row chunk][KV head][split_slots][32][2]
+    int32_t* seq_table; // B > 1: per sequence (first slot, split count), written by the partial launch
     int64_t code_seq;
     int64_t scale_seq;
     int32_t P;
@@ -112,11 +113,130 @@ struct AttnArgs {
     int32_t G;
     int32_t tokens_per_chunk;
     int32_t row_chunks;
-    int32_t nsplit;
-    int32_t kps;
+    int32_t nsplit;      // B == 1: key splits (host plan)
+    int32_t kps;         // B == 1: keys per split (host plan)
+    int32_t B;
+    int32_t split_slots; // partial slots per (row chunk, KV head)
+    int32_t split_budget; // B > 1: most splits the batch's keys are cut into per (row chunk, KV head)
     int32_t max_keys; // envelope max_visible_keys (<= max_context <= P): clamps device positions
     float scale_log2; // softmax scale * log2(e)
 };
+
+// ---- split plan of a batch -----------------------------------------------------------------------
+// B == 1 keeps the host plan, so the first chunk DMAs need not wait for the positions. For B > 1 the
+// sequences' windows W_i (keys visible to their last token, from the device positions) are cut into
+// splits of kps keys (a multiple of 128, at least kAttnMinKeysPerSplit): sequence i owns
+// n_i = max(1, ceil(W_i / kps)) consecutive partial slots of its (row chunk, KV head), and kps is the
+// smallest value with sum n_i <= split_budget, so ragged contexts fill the resident workgroups
+// evenly. With budget <= B every sequence gets one split.
+struct SplitRange {
+    int b;     // owning sequence (-1: none)
+    int first; // its first slot
+    int count; // its number of splits
+    int kps;
+};
+
+__device__ __forceinline__ int seq_window(const int32_t* positions, int T, int max_keys, int i) {
+    return max(0, min(positions[static_cast<int64_t>(i) * T + T - 1] + 1, max_keys));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) { v += __shfl_xor(v, off, 64); }
+    return v;
+}
+
+// max(1, ceil(w / kps)) in 32-bit arithmetic (w >= 0, kps >= 128).
+__device__ __forceinline__ int splits_of(int w, unsigned kps) {
+    return max(1, static_cast<int>((static_cast<unsigned>(w) + kps - 1u) / kps));
+}
+
+// sum over the batch of max(1, ceil(W_i / kps)) (whole wave).
+__device__ int batch_split_count(const int32_t* positions, int T, int B, int max_keys, unsigned kps) {
+    const int lane = threadIdx.x & 63;
+    int n = 0;
+    for (int base = 0; base < B; base += 64) {
+        const int i = base + lane;
+        if (i < B) { n += splits_of(seq_window(positions, T, max_keys, i), kps); }
+    }
+    return wave_sum_i(n);
+}
+
+// Keys per split of the batch (whole wave; every lane returns the same).
+__device__ unsigned batch_kps(const int32_t* positions, int T, int B, int max_keys, int budget) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long total = 0;
+    int wmax = 0;
+    for (int base = 0; base < B; base += 64) {
+        const int i = base + lane;
+        const int w = i < B ? seq_window(positions, T, max_keys, i) : 0;
+        total += static_cast<unsigned>(w);
+        wmax = max(wmax, w);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        total += __shfl_xor(total, off, 64);
+        wmax = max(wmax, __shfl_xor(wmax, off, 64));
+    }
+    const auto up128 = [](unsigned long long x) { return ((x + 127ull) / 128ull) * 128ull; };
+    unsigned long long kps;
+    if (budget <= B) {
+        kps = up128(static_cast<unsigned long long>(max(wmax, 1)));
+    } else {
+        // count(k) >= total / k, so lo is a lower bound; count(hi) <= total / hi + B <= budget.
+        unsigned long long lo = up128((total + budget - 1) / budget);
+        unsigned long long hi = up128((total + (budget - B) - 1) / (budget - B));
+        lo = lo < kAttnMinKeysPerSplit ? kAttnMinKeysPerSplit : lo;
+        hi = hi < lo ? lo : hi;
+        while (lo < hi) {
+            const unsigned long long mid = lo + ((hi - lo) / 256ull) * 128ull;
+            if (batch_split_count(positions, T, B, max_keys, static_cast<unsigned>(mid)) <= budget) {
+                hi = mid;
+            } else {
+                lo = mid + 128ull;
+            }
+        }
+        kps = lo;
+    }
+    kps = kps < kAttnMinKeysPerSplit ? kAttnMinKeysPerSplit : kps;
+    kps = kps > 0x7FFFFF80ull ? 0x7FFFFF80ull : kps;
+    return static_cast<unsigned>(kps);
+}
+
+// The sequence owning partial slot `slot` (b = -1 past the last split), whole wave. With `table`,
+// also stores every sequence's (first slot, split count) there, for the merge.
+__device__ SplitRange batch_split_range(const int32_t* positions, int T, int B, int max_keys, int budget, int slot,
+                                        int32_t* table) {
+    const int lane = threadIdx.x & 63;
+    const unsigned kps = batch_kps(positions, T, B, max_keys, budget);
+    SplitRange r{-1, 0, 0, static_cast<int>(kps)};
+    int run = 0;
+    for (int base = 0; base < B; base += 64) {
+        const int i = base + lane;
+        const int n = i < B ? splits_of(seq_window(positions, T, max_keys, i), kps) : 0;
+        int incl = n;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(incl, off, 64);
+            if (lane >= off) { incl += o; }
+        }
+        const int excl = run + incl - n;
+        if (table != nullptr && i < B) {
+            table[2 * i] = excl;
+            table[2 * i + 1] = n;
+        }
+        const unsigned long long m = __ballot(i < B && slot >= excl && slot < excl + n);
+        if (m != 0ull && r.b < 0) {
+            const int src = __ffsll(static_cast<long long>(m)) - 1;
+            r.b = base + src;
+            r.first = __shfl(excl, src, 64);
+            r.count = __shfl(n, src, 64);
+            if (table == nullptr) { return r; }
+        }
+        run += __shfl(incl, 63, 64);
+    }
+    return r;
+}
 
 // Visibility of new node u (0 <= u < T) from query token t, as a bitmask over u.
 __device__ __forceinline__ uint32_t new_key_mask(const int32_t* parents, int32_t t) {
@@ -564,11 +684,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int split = blockIdx.x;
     const int h = blockIdx.y;
-    const int b = blockIdx.z / a.row_chunks;
-    const int rc = blockIdx.z - b * a.row_chunks;
-    const int k0 = split * a.kps;
+    const int rc = blockIdx.z;
+    int b = 0;
+    int split = blockIdx.x;
+    int kps = a.kps;
+    int slot0 = 0;
+    if (a.B > 1) {
+        // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
+        const bool recorder = blockIdx.x == 0 && h == 0 && rc == 0;
+        const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
+                                                recorder ? a.seq_table : nullptr);
+        if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
+        b = sr.b;
+        split = blockIdx.x - sr.first;
+        kps = sr.kps;
+        slot0 = sr.first;
+    }
+    const int k0 = split * kps;
 
     const int64_t head_code = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
     const int64_t head_scale = static_cast<int64_t>(b) * a.scale_seq + static_cast<int64_t>(h) * a.P * G;
@@ -699,14 +832,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 
     const int window = min(pos_last + 1, a.max_keys);
     const int L = max(0, min(pos_first, window));
-    const int k1 = min(k0 + a.kps, window);
+    const int k1 = min(k0 + kps, window);
     const bool fused = a.k_new != nullptr;
     // With the fused append the cache rows >= L are written by this launch: splits stream only the
     // history below L, and the split holding L attends to the new rows from its own registers.
     const int hend = fused ? min(k1, L) : k1;
-    const bool owner = fused && L >= k0 && L < k0 + a.kps && L < window;
-    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
-    const int64_t pidx = unit * a.nsplit + split;
+    const bool owner = fused && L >= k0 && L < k0 + kps && L < window;
+    const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
     float* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
 
@@ -1032,11 +1164,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int split = blockIdx.x;
     const int h = blockIdx.y;
-    const int b = blockIdx.z / a.row_chunks;
-    const int rc = blockIdx.z - b * a.row_chunks;
-    const int k0 = split * a.kps;
+    const int rc = blockIdx.z;
+    int b = 0;
+    int split = blockIdx.x;
+    int kps = a.kps;
+    int slot0 = 0;
+    if (a.B > 1) {
+        // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
+        const bool recorder = blockIdx.x == 0 && h == 0 && rc == 0;
+        const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
+                                                recorder ? a.seq_table : nullptr);
+        if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
+        b = sr.b;
+        split = blockIdx.x - sr.first;
+        kps = sr.kps;
+        slot0 = sr.first;
+    }
+    const int k0 = split * kps;
 
     const int64_t head = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
     const __amdgpu_buffer_rsrc_t rk = raw_buffer(a.kb + head, static_cast<int64_t>(a.P) * D * 2);
@@ -1103,9 +1248,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int pos_last = __builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]);
     const int window = min(pos_last + 1, a.max_keys);
     const int L = max(0, min(pos_first, window));
-    const int hend = min(k0 + a.kps, window); // the new rows are already in the cache
-    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
-    const int64_t pidx = unit * a.nsplit + split;
+    const int hend = min(k0 + kps, window); // the new rows are already in the cache
+    const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
     float* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
     if (k0 >= hend) {
@@ -1198,6 +1342,9 @@ struct MergeArgs {
     int32_t row_chunks;
     int32_t nsplit;
     int32_t out_f32;
+    const int32_t* seq_table;
+    int32_t B;
+    int32_t split_slots;
 };
 
 constexpr int kMergeThreads = 256;
@@ -1224,9 +1371,15 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int gi = qh - h * a.G;
     const int rc = t / a.tokens_per_chunk;
     const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
-    const int64_t unit = (static_cast<int64_t>(b) * a.row_chunks + rc) * a.Hkv + h;
-    const float* ml = a.part_ml + unit * a.nsplit * 64;
-    const float* po = a.part_o + unit * a.nsplit * (32 * D);
+    int first = 0;
+    int nsplit = a.nsplit;
+    if (a.B > 1) {
+        first = a.seq_table[2 * b];
+        nsplit = a.seq_table[2 * b + 1];
+    }
+    const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + first;
+    const float* ml = a.part_ml + slot0 * 64;
+    const float* po = a.part_o + slot0 * (32 * D);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -1237,10 +1390,10 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
 #pragma unroll
     for (int k = 0; k < kMergePre; ++k) {
         const int s = sg + kMergeGroups * k;
-        pre[k] = s < a.nsplit ? po[static_cast<int64_t>(s) * 32 * D + r * D + d] : 0.0f;
+        pre[k] = s < nsplit ? po[static_cast<int64_t>(s) * 32 * D + r * D + d] : 0.0f;
     }
     float M = -INFINITY;
-    for (int s = tid; s < a.nsplit; s += kMergeThreads) {
+    for (int s = tid; s < nsplit; s += kMergeThreads) {
         const float ls = ml[s * 64 + 2 * r + 1];
         const float ms = ml[s * 64 + 2 * r];
         wts[s] = ls > 0.0f ? ms : -INFINITY;
@@ -1253,7 +1406,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     __syncthreads();
     float lsum = 0.0f;
-    for (int s = tid; s < a.nsplit; s += kMergeThreads) {
+    for (int s = tid; s < nsplit; s += kMergeThreads) {
         const float w = (M != -INFINITY && wts[s] != -INFINITY) ? __builtin_amdgcn_exp2f(wts[s] - M) : 0.0f;
         wts[s] = w;
         lsum = fmaf(lw[s], w, lsum);
@@ -1270,10 +1423,10 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
 #pragma unroll
         for (int k = 0; k < kMergePre; ++k) {
             const int s = sg + kMergeGroups * k;
-            if (s < a.nsplit) { o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o; }
+            if (s < nsplit) { o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o; }
         }
 #pragma unroll 4
-        for (int s = sg + kMergeGroups * kMergePre; s < a.nsplit; s += kMergeGroups) {
+        for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
             const float v = po[static_cast<int64_t>(s) * 32 * D + r * D + d];
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
@@ -1370,18 +1523,25 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     // D = 256 runs one workgroup per CU (its LDS map), D = 128 two.
     const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
     const int64_t want = std::max<int64_t>(1, (target + units - 1) / units);
+    // B > 1: the device cuts the batch's actual keys into at most split_budget splits per (row
+    // chunk, KV head), sized so that every split workgroup is resident at once.
+    const int64_t cols = static_cast<int64_t>(Hkv) * p.row_chunks;
+    p.split_budget = static_cast<int32_t>(std::max<int64_t>(1, target / cols));
     int64_t kps = (static_cast<int64_t>(max_visible_keys) + want - 1) / want;
     kps = ((kps + 127) / 128) * 128;
     kps = std::max<int64_t>(kps, kAttnMinKeysPerSplit);
     p.keys_per_split = static_cast<int32_t>(kps);
     p.nsplit = static_cast<int32_t>((static_cast<int64_t>(max_visible_keys) + kps - 1) / kps);
     p.nsplit = std::max(p.nsplit, 1);
-    const size_t part_units = static_cast<size_t>(units) * p.nsplit;
+    p.split_slots = B == 1 ? p.nsplit : std::max(p.split_budget, B);
+    const size_t part_units = static_cast<size_t>(cols) * p.split_slots;
     p.part_o_offset = 0;
     const size_t o_bytes = part_units * 32 * static_cast<size_t>(D) * sizeof(float);
     p.part_ml_offset = (o_bytes + 255) & ~static_cast<size_t>(255);
     const size_t ml_bytes = part_units * 64 * sizeof(float);
-    p.bytes = ((p.part_ml_offset + ml_bytes + 255) & ~static_cast<size_t>(255));
+    p.seq_table_offset = (p.part_ml_offset + ml_bytes + 255) & ~static_cast<size_t>(255);
+    const size_t table_bytes = static_cast<size_t>(B) * 2 * sizeof(int32_t);
+    p.bytes = ((p.seq_table_offset + table_bytes + 255) & ~static_cast<size_t>(255));
     return p;
 }
 
@@ -1412,7 +1572,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
                              void* workspace, const SplitPlan& plan, void* out, bool out_f32,
                              hipStream_t stream) {
     if (c.D != 128 && c.D != 256) { throw Unsupported("verify attention: head_dim 128 and 256 are built"); }
-    if (plan.nsplit > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
+    if (plan.split_slots > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
     if (k_new != nullptr && (plan.row_chunks > 1 || c.kb != nullptr)) {
         // Several row-chunk workgroups read the new rows, or a BF16 cache (no in-kernel codec):
         // write them in a launch of their own.
@@ -1435,6 +1595,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.vs = c.vs;
     a.part_o = reinterpret_cast<float*>(ws + plan.part_o_offset);
     a.part_ml = reinterpret_cast<float*>(ws + plan.part_ml_offset);
+    a.seq_table = reinterpret_cast<int32_t*>(ws + plan.seq_table_offset);
     a.code_seq = c.code_seq;
     a.scale_seq = c.scale_seq;
     a.P = c.P;
@@ -1446,10 +1607,13 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.row_chunks = plan.row_chunks;
     a.nsplit = plan.nsplit;
     a.kps = plan.keys_per_split;
+    a.B = c.B;
+    a.split_slots = plan.split_slots;
+    a.split_budget = plan.split_budget;
     a.max_keys = static_cast<int32_t>(max_keys);
     a.scale_log2 = scale * 1.4426950408889634f;
     const int rows = plan.tokens_per_chunk * plan.G;
-    dim3 grid(plan.nsplit, c.Hkv, c.B * plan.row_chunks);
+    dim3 grid(plan.split_slots, c.Hkv, plan.row_chunks);
     if (c.kb != nullptr) {
         if (c.D == 128) {
             if (rows <= 16) {
@@ -1486,6 +1650,9 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.tokens_per_chunk = plan.tokens_per_chunk;
     mg.row_chunks = plan.row_chunks;
     mg.nsplit = plan.nsplit;
+    mg.seq_table = a.seq_table;
+    mg.B = c.B;
+    mg.split_slots = plan.split_slots;
     mg.out_f32 = out_f32 ? 1 : 0;
     if (c.D == 128) {
         hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
