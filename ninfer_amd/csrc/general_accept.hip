@@ -39,6 +39,8 @@ typedef unsigned __int128 u128;
 
 constexpr int kThreads = 256;
 constexpr int kPerThread = kGenTile / kThreads; // 16 consecutive tokens per thread in rescans
+constexpr int kDrawPerThread = kGenDrawTile / kThreads; // 4 tokens per thread in the draw passes
+constexpr int kMaxDrawTilesPerThread = (kGenMaxTiles * kGenTile / kGenDrawTile) / kThreads; // V <= 2^20
 
 struct ColDesc {
     float m;          // xmax / T
@@ -76,6 +78,7 @@ struct GenArgs {
     int32_t K;
     int32_t ncols;
     int32_t ntiles;
+    int32_t ndraw; // draw tiles of kGenDrawTile tokens
     float* tile_max;
     uint64_t* cmass;
     uint32_t* ccount;
@@ -84,7 +87,18 @@ struct GenArgs {
     uint32_t* fine_total;
     uint64_t* tile_res;
     uint64_t* tile_p;
+    struct DraftEntry* dtab;
 };
+
+// Inputs of draft i's accept test, gathered once per round by gen_coarse so that no later launch
+// waits on drafts -> logits: the BF16 bits of target column i and draft column i at token d_i
+// (xpq = xp | xq << 16, zero outside the token domain) and d_i itself (-1 outside the domain).
+struct DraftEntry {
+    uint32_t xpq;
+    int32_t d;
+};
+static_assert(sizeof(DraftEntry) == kGenDraftEntryBytes, "draft entry size");
+constexpr int kMaxCols = 2 * kMaxColumns; // 2K + 1 <= 31 descriptors per sequence
 
 __device__ __forceinline__ const uint16_t* column_ptr(const GenArgs& a, int b, int c) {
     if (c <= a.K) { return a.logits + b * a.logit_seq + c * a.logit_col; }
@@ -161,6 +175,20 @@ __device__ __forceinline__ void load16(const uint16_t* col, int v0, int V, float
     }
 }
 
+// The 4 tokens [v0, v0 + 4) of a column as floats (tokens >= V read as -inf).
+__device__ __forceinline__ void load4(const uint16_t* col, int v0, int V, float (&x)[4]) {
+    if (v0 + 4 <= V && (reinterpret_cast<uintptr_t>(col + v0) & 7u) == 0) {
+        const uint2 r = *reinterpret_cast<const uint2*>(col + v0);
+        x[0] = bf16_to_f32(static_cast<uint16_t>(r.x & 0xffffu));
+        x[1] = bf16_to_f32(static_cast<uint16_t>(r.x >> 16));
+        x[2] = bf16_to_f32(static_cast<uint16_t>(r.y & 0xffffu));
+        x[3] = bf16_to_f32(static_cast<uint16_t>(r.y >> 16));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[e] = bf16_to_f32(v0 + e < V ? col[v0 + e] : static_cast<uint16_t>(0xff80u)); }
+    }
+}
+
 // Smallest thread index with `pred`, or kThreads.
 __device__ int block_first(bool pred, int* sh) {
     if (threadIdx.x == 0) { *sh = kThreads; }
@@ -224,6 +252,14 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
     __shared__ float red[kThreads / 64];
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
+    if (t == 0 && c == 0 && static_cast<int>(threadIdx.x) < a.K) {
+        const int i = threadIdx.x;
+        const int d = a.drafts[b * a.K + i];
+        const bool in_domain = d >= 0 && d < a.V;
+        const uint32_t xp = in_domain ? column_ptr(a, b, i)[d] : 0u;
+        const uint32_t xq = in_domain ? column_ptr(a, b, a.K + 1 + i)[d] : 0u;
+        a.dtab[static_cast<int64_t>(b) * a.K + i] = DraftEntry{xp | (xq << 16), in_domain ? d : -1};
+    }
     cnt[threadIdx.x] = 0;
     mass[threadIdx.x] = 0;
     // The tile's tokens load while the column maximum is reduced.
@@ -379,29 +415,42 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     }
 }
 
-// Accept decisions of sequence b (identical in every block that evaluates them): thread i < K
-// tests draft i, and the first failing draft is the rejection. Returns a; sets *rejected to the
+// Accept decisions of sequence b (identical in every block that evaluates them), from the
+// sequence's descriptors in LDS (sd) and thread i's draft entry e and accept uniform ua: thread
+// i < K tests draft i, and the first failing draft is the rejection. Returns a; sets *rejected to the
 // rejected column (or -1 when all K drafts are accepted).
-__device__ int decide(const GenArgs& a, int b, int* rejected, int* sh) {
+__device__ int decide(const GenArgs& a, const ColDesc* sd, const DraftEntry& e, float ua, int* rejected, int* sh) {
     bool fail = false;
     const int i = static_cast<int>(threadIdx.x);
     if (i < a.K) {
-        const int d = a.drafts[b * a.K + i];
-        const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + i];
-        const ColDesc q = a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + i];
+        const ColDesc& p = sd[i];
+        const ColDesc& q = sd[a.K + 1 + i];
         // A draft id outside the token domain has no mass under either distribution: rejected.
-        const bool in_domain = d >= 0 && d < a.V;
-        const float xp = in_domain ? bf16_to_f32(column_ptr(a, b, i)[d]) : 0.0f;
-        const float xq = in_domain ? bf16_to_f32(column_ptr(a, b, a.K + 1 + i)[d]) : 0.0f;
-        const uint64_t wp = in_domain ? member_weight(p, xp, d) : 0ull;
-        const uint64_t wq = in_domain ? member_weight(q, xq, d) : 0ull;
-        const u128 lhs = static_cast<u128>(fixed_u24(a.u_accept[b * (a.K + 1) + i])) * wq * p.zs;
+        const bool in_domain = e.d >= 0;
+        const float xp = in_domain ? bf16_to_f32(static_cast<uint16_t>(e.xpq & 0xffffu)) : 0.0f;
+        const float xq = in_domain ? bf16_to_f32(static_cast<uint16_t>(e.xpq >> 16)) : 0.0f;
+        const uint64_t wp = in_domain ? member_weight(p, xp, e.d) : 0ull;
+        const uint64_t wq = in_domain ? member_weight(q, xq, e.d) : 0ull;
+        const u128 lhs = static_cast<u128>(fixed_u24(ua)) * wq * p.zs;
         const u128 rhs = (static_cast<u128>(wp) * q.zs) << 24;
         fail = !(lhs < rhs);
     }
     const int f = block_first(fail, sh);
     *rejected = f < a.K ? f : -1;
     return f < a.K ? f : a.K;
+}
+
+// The sequence's descriptors into LDS and thread i's draft entry and accept uniform (one round trip
+// for everything decide() reads).
+__device__ __forceinline__ void load_decision_inputs(const GenArgs& a, int b, ColDesc* sd, DraftEntry* e, float* ua) {
+    const int i = static_cast<int>(threadIdx.x);
+    *e = DraftEntry{0u, -1};
+    *ua = 0.0f;
+    if (i < a.K) {
+        *e = a.dtab[static_cast<int64_t>(b) * a.K + i];
+        *ua = a.u_accept[b * (a.K + 1) + i];
+    }
+    if (i < a.ncols) { sd[i] = a.desc[static_cast<int64_t>(b) * a.ncols + i]; }
 }
 
 // Draw weights of token v: residual (column pair i) or p (column i); both from one read.
@@ -429,21 +478,26 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
     __shared__ u128 shr[kThreads / 64];
     __shared__ uint64_t shp[kThreads / 64];
     __shared__ int first;
+    __shared__ ColDesc sd[kMaxCols];
     const int t = blockIdx.x, b = blockIdx.y;
+    DraftEntry e;
+    float ua;
+    load_decision_inputs(a, b, sd, &e, &ua);
+    __syncthreads();
     int rejected;
-    const int acc = decide(a, b, &rejected, &first);
+    const int acc = decide(a, sd, e, ua, &rejected, &first);
     const int col_p = rejected >= 0 ? rejected : a.K;
-    const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
-    const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
+    const ColDesc p = sd[col_p];
+    const ColDesc q = rejected >= 0 ? sd[a.K + 1 + rejected] : p;
     (void)acc;
     u128 res = 0;
     uint64_t pm = 0;
-    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
-    float xp[16], xq[16] = {};
-    load16(column_ptr(a, b, col_p), v0, a.V, xp);
-    if (rejected >= 0) { load16(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
+    const int v0 = t * kGenDrawTile + kDrawPerThread * static_cast<int>(threadIdx.x);
+    float xp[kDrawPerThread], xq[kDrawPerThread] = {};
+    load4(column_ptr(a, b, col_p), v0, a.V, xp);
+    if (rejected >= 0) { load4(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
+    for (int k = 0; k < kDrawPerThread; ++k) {
         if (v0 + k < a.V) {
             const DrawMass dm = draw_mass_x(rejected, p, q, xp[k], xq[k], v0 + k);
             res += dm.res;
@@ -453,9 +507,9 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
     const u128 rtot = block_scan<u128>(res, shr);
     const uint64_t ptot = block_scan<uint64_t>(pm, shp);
     if (threadIdx.x == kThreads - 1) {
-        a.tile_res[(static_cast<int64_t>(b) * a.ntiles + t) * 2] = static_cast<uint64_t>(rtot);
-        a.tile_res[(static_cast<int64_t>(b) * a.ntiles + t) * 2 + 1] = static_cast<uint64_t>(rtot >> 64);
-        a.tile_p[static_cast<int64_t>(b) * a.ntiles + t] = ptot;
+        a.tile_res[(static_cast<int64_t>(b) * a.ndraw + t) * 2] = static_cast<uint64_t>(rtot);
+        a.tile_res[(static_cast<int64_t>(b) * a.ndraw + t) * 2 + 1] = static_cast<uint64_t>(rtot >> 64);
+        a.tile_p[static_cast<int64_t>(b) * a.ndraw + t] = ptot;
     }
 }
 
@@ -466,56 +520,104 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     __shared__ int first;
     __shared__ int last_tile;
     __shared__ int result;
+    __shared__ u128 tile_before;
+    __shared__ int crossing_tile;
+    __shared__ ColDesc sd[kMaxCols];
+    __shared__ int32_t sdrafts[kMaxColumns];
+    __shared__ int64_t sstats[4 + kMaxColumns];
+    __shared__ int32_t slength;
     const int b = blockIdx.x;
-    int rejected;
-    const int acc = decide(a, b, &rejected, &first);
-    const int col_p = rejected >= 0 ? rejected : a.K;
-    const ColDesc p = a.desc[static_cast<int64_t>(b) * a.ncols + col_p];
-    const ColDesc q = rejected >= 0 ? a.desc[static_cast<int64_t>(b) * a.ncols + a.K + 1 + rejected] : p;
-    // Tile totals of the chosen weights (residual, or p when there is no residual mass).
-    u128 rtot = 0;
-    if (static_cast<int>(threadIdx.x) < a.ntiles) {
-        const int64_t ti = static_cast<int64_t>(b) * a.ntiles + threadIdx.x;
-        rtot = (static_cast<u128>(a.tile_res[ti * 2 + 1]) << 64) | a.tile_res[ti * 2];
+    const int tid = static_cast<int>(threadIdx.x);
+    // Thread tid owns draw tiles [tid * tpt, tid * tpt + tpt) (ids ascending across threads).
+    const int tpt = (a.ndraw + kThreads - 1) / kThreads;
+    const int tile0 = tid * tpt;
+    // Everything this block reads except the crossing tile's tokens, requested at once.
+    DraftEntry e;
+    float ua;
+    load_decision_inputs(a, b, sd, &e, &ua);
+    u128 rt[kMaxDrawTilesPerThread];
+    uint64_t pt[kMaxDrawTilesPerThread];
+#pragma unroll
+    for (int j = 0; j < kMaxDrawTilesPerThread; ++j) {
+        rt[j] = 0;
+        pt[j] = 0;
+        if (j < tpt && tile0 + j < a.ndraw) {
+            const int64_t ti = static_cast<int64_t>(b) * a.ndraw + tile0 + j;
+            rt[j] = (static_cast<u128>(a.tile_res[ti * 2 + 1]) << 64) | a.tile_res[ti * 2];
+            pt[j] = a.tile_p[ti];
+        }
     }
-    const u128 rincl = block_scan<u128>(rejected >= 0 ? rtot : u128(0), sh);
+    if (tid < a.K) { sdrafts[tid] = a.drafts[b * a.K + tid]; }
+    if (tid < 4 + a.K) { sstats[tid] = a.stats[static_cast<int64_t>(b) * a.stats_stride + tid]; }
+    if (tid == 0) { slength = a.length[b]; }
+    const float u_res = a.u_residual[b];
+    const float u_bonus = a.u_accept[b * (a.K + 1) + a.K];
+    __syncthreads();
+    int rejected;
+    const int acc = decide(a, sd, e, ua, &rejected, &first);
+    const int col_p = rejected >= 0 ? rejected : a.K;
+    const ColDesc p = sd[col_p];
+    const ColDesc q = rejected >= 0 ? sd[a.K + 1 + rejected] : p;
+    // Totals of the chosen weights (residual, or p when there is no residual mass).
+    u128 rsum = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxDrawTilesPerThread; ++j) { rsum += rt[j]; }
+    const u128 rincl = block_scan<u128>(rejected >= 0 ? rsum : u128(0), sh);
     __shared__ u128 rall;
-    if (threadIdx.x == kThreads - 1) { rall = rincl; }
+    if (tid == kThreads - 1) { rall = rincl; }
     __syncthreads();
     const bool use_res = rejected >= 0 && rall != 0;
-    u128 tt = 0;
-    if (static_cast<int>(threadIdx.x) < a.ntiles) {
-        tt = use_res ? rtot : static_cast<u128>(a.tile_p[static_cast<int64_t>(b) * a.ntiles + threadIdx.x]);
+    u128 tt[kMaxDrawTilesPerThread];
+    u128 tsum = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxDrawTilesPerThread; ++j) {
+        tt[j] = use_res ? rt[j] : static_cast<u128>(pt[j]);
+        tsum += tt[j];
     }
-    const u128 incl = block_scan<u128>(tt, sh);
+    const u128 incl = block_scan<u128>(tsum, sh);
     __shared__ u128 total;
-    if (threadIdx.x == kThreads - 1) { total = incl; }
+    if (tid == kThreads - 1) { total = incl; }
     __syncthreads();
-    const float u = rejected >= 0 ? a.u_residual[b] : a.u_accept[b * (a.K + 1) + a.K];
+    const float u = rejected >= 0 ? u_res : u_bonus;
     const u128 goal = (total * fixed_u24(u)) >> 24;
-    int ts = block_first(static_cast<int>(threadIdx.x) < a.ntiles && tt != 0 && incl > goal, &first);
-    const bool crossing = ts < kThreads;
+    // The first tile whose running mass exceeds goal lies in the first thread whose inclusive sum
+    // does (a tile that moves the running mass past goal has nonzero mass).
+    const int owner = block_first(tsum != 0 && incl > goal, &first);
+    const bool crossing = owner < kThreads;
+    if (tid == 0) {
+        last_tile = -1;
+        crossing_tile = 0;
+    }
+    __syncthreads();
+    if (crossing && tid == owner) {
+        u128 run = incl - tsum;
+        for (int j = 0; j < tpt; ++j) {
+            if (tt[j] != 0 && run + tt[j] > goal) {
+                crossing_tile = tile0 + j;
+                tile_before = run;
+                break;
+            }
+            run += tt[j];
+        }
+    }
     if (!crossing) {
         // goal >= total: the draw is the last id with nonzero mass.
-        if (threadIdx.x == 0) { last_tile = 0; }
-        __syncthreads();
-        if (static_cast<int>(threadIdx.x) < a.ntiles && tt != 0) { atomicMax(&last_tile, static_cast<int>(threadIdx.x)); }
-        __syncthreads();
-        ts = last_tile;
+        int lt = -1;
+        for (int j = 0; j < tpt; ++j) { if (tt[j] != 0) { lt = tile0 + j; } }
+        if (lt >= 0) { atomicMax(&last_tile, lt); }
     }
-    __shared__ u128 tile_before;
-    if (static_cast<int>(threadIdx.x) == ts) { tile_before = incl - tt; }
-    if (threadIdx.x == 0) { result = -1; }
+    if (tid == 0) { result = -1; }
     __syncthreads();
-    // Rescan the tile: thread i owns tokens [16 i, 16 i + 16).
-    const int v0 = ts * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
-    float xp[16], xq[16] = {};
-    load16(column_ptr(a, b, col_p), v0, a.V, xp);
-    if (rejected >= 0) { load16(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
-    uint64_t w[kPerThread];
+    const int ts = crossing ? crossing_tile : max(last_tile, 0);
+    // Rescan the tile: thread i owns tokens [4 i, 4 i + 4) of it.
+    const int v0 = ts * kGenDrawTile + kDrawPerThread * tid;
+    float xp[kDrawPerThread], xq[kDrawPerThread] = {};
+    load4(column_ptr(a, b, col_p), v0, a.V, xp);
+    if (rejected >= 0) { load4(column_ptr(a, b, a.K + 1 + rejected), v0, a.V, xq); }
+    uint64_t w[kDrawPerThread];
     u128 mine = 0;
 #pragma unroll
-    for (int k = 0; k < kPerThread; ++k) {
+    for (int k = 0; k < kDrawPerThread; ++k) {
         const int v = v0 + k;
         w[k] = 0;
         if (v < a.V) {
@@ -524,11 +626,11 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
         }
         mine += w[k];
     }
-    const u128 mincl = block_scan<u128>(mine, sh) + tile_before;
+    const u128 mincl = block_scan<u128>(mine, sh) + (crossing ? tile_before : u128(0));
     if (crossing) {
         if (mine != 0 && mincl > goal && mincl - mine <= goal) {
             u128 run = mincl - mine;
-            for (int k = 0; k < kPerThread; ++k) {
+            for (int k = 0; k < kDrawPerThread; ++k) {
                 if (w[k] == 0) { continue; }
                 run += w[k];
                 if (goal < run) {
@@ -538,19 +640,24 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
             }
         }
     } else {
-        const int lastk = [&] {
-            int r = -1;
-            for (int k = 0; k < kPerThread; ++k) { if (w[k] != 0) { r = k; } }
-            return r;
-        }();
+        int lastk = -1;
+        for (int k = 0; k < kDrawPerThread; ++k) { if (w[k] != 0) { lastk = k; } }
         if (lastk >= 0) { atomicMax(&result, v0 + lastk); }
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const int tstar = result < 0 ? 0 : result;
-        commit_round(a.drafts + b * a.K, a.K, acc, tstar, a.length[b], a.length + b, a.token + b,
-                     a.sampled_out + b * (a.K + 1), a.num_sampled + b, a.accepted + b,
-                     a.stats + static_cast<int64_t>(b) * a.stats_stride);
+    // Commit the round (the reference's commit, src/ops/kernel/speculative_round.cuh:145-166), from
+    // the values read at entry: stores only.
+    const int tstar = result < 0 ? 0 : result;
+    if (tid <= a.K) { a.sampled_out[b * (a.K + 1) + tid] = tid < acc ? sdrafts[tid] : (tid == acc ? tstar : 0); }
+    if (tid < 4 + a.K) {
+        const int64_t add = tid == 0 ? a.K : tid == 1 ? acc : tid == 2 ? 1 : (tid >= kStatsPerPositionOffset && tid - kStatsPerPositionOffset < acc) ? 1 : 0;
+        if (add != 0) { a.stats[static_cast<int64_t>(b) * a.stats_stride + tid] = sstats[tid] + add; }
+    }
+    if (tid == 0) {
+        a.num_sampled[b] = acc + 1;
+        a.accepted[b] = acc;
+        a.token[b] = tstar;
+        a.length[b] = slength + acc + 1;
     }
 }
 
@@ -560,6 +667,7 @@ GenPlan plan_general(int32_t token_domain, int32_t K, int32_t B) {
     GenPlan p;
     p.ncols = 2 * K + 1;
     p.ntiles = (token_domain + kGenTile - 1) / kGenTile;
+    p.ndraw = (token_domain + kGenDrawTile - 1) / kGenDrawTile;
     const auto align = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
     size_t at = 0;
     const size_t cols = static_cast<size_t>(B) * p.ncols;
@@ -576,9 +684,11 @@ GenPlan plan_general(int32_t token_domain, int32_t K, int32_t B) {
     p.fine_total_offset = at;
     at = align(at + cols * kGenBins * sizeof(uint32_t));
     p.tile_res_offset = at;
-    at = align(at + static_cast<size_t>(B) * p.ntiles * 2 * sizeof(uint64_t));
+    at = align(at + static_cast<size_t>(B) * p.ndraw * 2 * sizeof(uint64_t));
     p.tile_p_offset = at;
-    at = align(at + static_cast<size_t>(B) * p.ntiles * sizeof(uint64_t));
+    at = align(at + static_cast<size_t>(B) * p.ndraw * sizeof(uint64_t));
+    p.dtab_offset = at;
+    at = align(at + static_cast<size_t>(B) * K * kGenDraftEntryBytes);
     p.bytes = at;
     return p;
 }
@@ -607,6 +717,7 @@ void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* worksp
     a.K = l.K;
     a.ncols = plan.ncols;
     a.ntiles = plan.ntiles;
+    a.ndraw = plan.ndraw;
     a.tile_max = reinterpret_cast<float*>(ws + plan.tile_max_offset);
     a.cmass = reinterpret_cast<uint64_t*>(ws + plan.cmass_offset);
     a.ccount = reinterpret_cast<uint32_t*>(ws + plan.ccount_offset);
@@ -615,6 +726,7 @@ void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* worksp
     a.fine_total = reinterpret_cast<uint32_t*>(ws + plan.fine_total_offset);
     a.tile_res = reinterpret_cast<uint64_t*>(ws + plan.tile_res_offset);
     a.tile_p = reinterpret_cast<uint64_t*>(ws + plan.tile_p_offset);
+    a.dtab = reinterpret_cast<DraftEntry*>(ws + plan.dtab_offset);
     const dim3 tiles(plan.ntiles, plan.ncols, l.B);
     const dim3 cols(plan.ncols, l.B);
     hipLaunchKernelGGL(gen_max_kernel, tiles, dim3(kThreads), 0, stream, a);
@@ -627,7 +739,7 @@ void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* worksp
     check_launch("gen_fine_kernel");
     hipLaunchKernelGGL(gen_nucleus_kernel, cols, dim3(kThreads), 0, stream, a);
     check_launch("gen_nucleus_kernel");
-    hipLaunchKernelGGL(gen_totals_kernel, dim3(plan.ntiles, l.B), dim3(kThreads), 0, stream, a);
+    hipLaunchKernelGGL(gen_totals_kernel, dim3(plan.ndraw, l.B), dim3(kThreads), 0, stream, a);
     check_launch("gen_totals_kernel");
     hipLaunchKernelGGL(gen_pick_kernel, dim3(l.B), dim3(kThreads), 0, stream, a);
     check_launch("gen_pick_kernel");

@@ -5,15 +5,18 @@
 
 namespace nmi {
 
-inline constexpr int32_t kGenTile = 4096;       // tokens per tile
+inline constexpr int32_t kGenTile = 4096;       // tokens per tile (histogram passes)
+inline constexpr int32_t kGenDrawTile = 1024;   // tokens per tile of the draw passes
 inline constexpr int32_t kGenBins = 256;        // histogram bins per level
 inline constexpr int32_t kGenMaxTiles = 256;    // one tile per thread in the per-column scans
 inline constexpr int32_t kGenDescBytes = 64;    // per-column nucleus descriptor
+inline constexpr int32_t kGenDraftEntryBytes = 8; // per-draft accept-test inputs
 
 // Workspace layout, shared by the size query and the launch.
 struct GenPlan {
     int32_t ncols = 0;  // K + 1 target columns then K draft columns
     int32_t ntiles = 0;
+    int32_t ndraw = 0;  // draw tiles
     size_t tile_max_offset = 0;
     size_t cmass_offset = 0;
     size_t ccount_offset = 0;
@@ -22,6 +25,7 @@ struct GenPlan {
     size_t fine_total_offset = 0; // per column: fine counts summed over tiles
     size_t tile_res_offset = 0;
     size_t tile_p_offset = 0;
+    size_t dtab_offset = 0;   // per draft: BF16 bits of its target/draft logits, its id
     size_t bytes = 0;
 };
 

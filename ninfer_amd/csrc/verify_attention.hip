@@ -1371,13 +1371,8 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int gi = qh - h * a.G;
     const int rc = t / a.tokens_per_chunk;
     const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
-    int first = 0;
-    int nsplit = a.nsplit;
-    if (a.B > 1) {
-        first = a.seq_table[2 * b];
-        nsplit = a.seq_table[2 * b + 1];
-    }
-    const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + first;
+    const int nsplit = a.nsplit; // B == 1 (batches use verify_attn_merge_rows_kernel)
+    const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots;
     const float* ml = a.part_ml + slot0 * 64;
     const float* po = a.part_o + slot0 * (32 * D);
     const int tid = threadIdx.x;
@@ -1444,6 +1439,64 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
         } else {
             static_cast<uint16_t*>(a.out)[oi] = f32_to_bf16_bits(val);
         }
+    }
+}
+
+// Batched form of the merge (B > 1, a few splits per sequence): a block serves 8 output rows
+// (b, t, qh) x 32 dims, and each thread merges its (row, dim) over the sequence's splits in split
+// order with a running log-sum-exp, eight splits' loads in flight. Same result contract as above.
+constexpr int kMergeRowsPerBlock = kMergeThreads / kMergeDims;
+
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(MergeArgs a) {
+    const int tid = threadIdx.x;
+    const int row_id = blockIdx.x * kMergeRowsPerBlock + tid / kMergeDims; // (b, t, qh)
+    if (row_id >= a.B * a.T * a.Hq) { return; }
+    const int qh = row_id % a.Hq;
+    const int t = (row_id / a.Hq) % a.T;
+    const int b = row_id / (a.Hq * a.T);
+    const int h = qh / a.G;
+    const int gi = qh - h * a.G;
+    const int rc = t / a.tokens_per_chunk;
+    const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
+    const int d = blockIdx.y * kMergeDims + (tid & (kMergeDims - 1));
+    const int first = a.seq_table[2 * b];
+    const int nsplit = a.seq_table[2 * b + 1];
+    const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + first;
+    const float* ml = a.part_ml + slot0 * 64 + 2 * r;
+    const float* po = a.part_o + slot0 * (32 * D) + r * D + d;
+    float M = -INFINITY;
+    float lsum = 0.0f;
+    float o = 0.0f;
+    constexpr int kBatch = 8;
+#pragma unroll 1
+    for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
+        float2 mlv[kBatch];
+        float ov[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int s = s0 + k;
+            mlv[k] = s < nsplit ? *reinterpret_cast<const float2*>(ml + static_cast<int64_t>(s) * 64) : float2{-INFINITY, 0.0f};
+            ov[k] = s < nsplit ? po[static_cast<int64_t>(s) * 32 * D] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            // A split with no visible key never wrote its partial rows: skip it.
+            if (!(mlv[k].y > 0.0f)) { continue; }
+            const float mn = fmaxf(M, mlv[k].x);
+            const float alpha = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+            const float beta = __builtin_amdgcn_exp2f(mlv[k].x - mn);
+            o = fmaf(o, alpha, ov[k] * beta);
+            lsum = fmaf(lsum, alpha, mlv[k].y * beta);
+            M = mn;
+        }
+    }
+    const float val = lsum > 0.0f ? o / lsum : 0.0f;
+    const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
+    if (a.out_f32) {
+        static_cast<float*>(a.out)[oi] = val;
+    } else {
+        static_cast<uint16_t*>(a.out)[oi] = f32_to_bf16_bits(val);
     }
 }
 
@@ -1654,7 +1707,12 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.B = c.B;
     mg.split_slots = plan.split_slots;
     mg.out_f32 = out_f32 ? 1 : 0;
-    if (c.D == 128) {
+    const dim3 rows_grid((c.B * T * Hq + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock, c.D / kMergeDims);
+    if (c.B > 1 && c.D == 128) {
+        hipLaunchKernelGGL(verify_attn_merge_rows_kernel<128>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
+    } else if (c.B > 1) {
+        hipLaunchKernelGGL(verify_attn_merge_rows_kernel<256>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
+    } else if (c.D == 128) {
         hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else {
         hipLaunchKernelGGL(verify_attn_merge_kernel<256>, dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
