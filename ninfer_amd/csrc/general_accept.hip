@@ -17,14 +17,16 @@
 // last included token among equal values (ids ascending). The nucleus collapses to one 64-bit
 // key threshold: token v is a member iff sort_key(x_v, v) >= kstar.
 //
-// Launches (tiles of 4096 tokens, all columns and sequences in one grid each):
+// Launches (histogram passes over tiles of 4096 tokens, draw passes over tiles of 1024; all
+// columns and sequences in one grid each):
 //   1 gen_max      tile maxima; zero the coarse histograms and the column fine counts
-//   2 gen_coarse   per-token weights -> coarse counts and masses (LDS, then global atomics)
-//   3 gen_cross    per column: total mass, top-p target, crossing coarse bin
-//   4 gen_fine     per tile: counts of the 256 values inside the crossing bin (also summed per column)
-//   5 gen_nucleus  per column: crossing value, rank cut, kstar and nucleus mass
-//   6 gen_totals   per tile: accept decision (recomputed per block), masses of the draw
-//   7 gen_pick     per sequence: locate the draw, commit the round
+//   2 gen_coarse   per-token weights -> coarse counts and masses (replicated LDS histograms, then
+//                  global atomics); block 0 of a sequence gathers the drafts' accept-test inputs
+//   3 gen_fine     per tile: total mass, top-p target and crossing coarse bin (every block; block 0
+//                  writes the column descriptor), then counts of the 256 values inside that bin
+//   4 gen_nucleus  per column: crossing value, rank cut, kstar and nucleus mass
+//   5 gen_totals   per draw tile: accept decision (recomputed per block), masses of the draw
+//   6 gen_pick     per sequence: locate the draw, commit the round
 #include "common.h"
 #include "device_utils.h"
 #include "general_internal.h"
@@ -246,9 +248,14 @@ __device__ void column_scale(const GenArgs& a, int64_t cb, float* red, float* m,
 }
 
 // ---- 2: coarse histogram of counts and masses ----------------------------------------------------
+// Lanes of a wave mostly fall into a few bins, so lane l adds into replica l % kCoarseReplicas; the
+// replica stride of kGenBins + 1 words puts the replicas of one bin in different LDS banks.
+constexpr int kCoarseReplicas = 16;
+constexpr int kReplicaStride = kGenBins + 1;
+
 __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
-    __shared__ uint32_t cnt[kGenBins];
-    __shared__ uint64_t mass[kGenBins];
+    __shared__ uint32_t cnt[kCoarseReplicas * kReplicaStride];
+    __shared__ uint64_t mass[kCoarseReplicas * kReplicaStride];
     __shared__ float red[kThreads / 64];
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
@@ -260,8 +267,10 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
         const uint32_t xq = in_domain ? column_ptr(a, b, a.K + 1 + i)[d] : 0u;
         a.dtab[static_cast<int64_t>(b) * a.K + i] = DraftEntry{xp | (xq << 16), in_domain ? d : -1};
     }
-    cnt[threadIdx.x] = 0;
-    mass[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < kCoarseReplicas * kReplicaStride; i += kThreads) {
+        cnt[i] = 0;
+        mass[i] = 0;
+    }
     // The tile's tokens load while the column maximum is reduced.
     const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
     float x[16];
@@ -271,43 +280,54 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         if (v0 + e < a.V) {
-            const uint32_t bin = ordered16(x[e]) >> 8;
-            atomicAdd(&cnt[bin], 1u);
-            atomicAdd(reinterpret_cast<unsigned long long*>(&mass[bin]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
+            const uint32_t slot = (threadIdx.x % kCoarseReplicas) * kReplicaStride + (ordered16(x[e]) >> 8);
+            atomicAdd(&cnt[slot], 1u);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&mass[slot]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
         }
     }
     __syncthreads();
-    if (cnt[threadIdx.x] != 0) {
-        atomicAdd(&a.ccount[cb * kGenBins + threadIdx.x], cnt[threadIdx.x]);
+    uint32_t ct = 0;
+    uint64_t ms = 0;
+#pragma unroll
+    for (int r = 0; r < kCoarseReplicas; ++r) {
+        ct += cnt[r * kReplicaStride + threadIdx.x];
+        ms += mass[r * kReplicaStride + threadIdx.x];
+    }
+    if (ct != 0) {
+        atomicAdd(&a.ccount[cb * kGenBins + threadIdx.x], ct);
         atomicAdd(reinterpret_cast<unsigned long long*>(&a.cmass[cb * kGenBins + threadIdx.x]),
-                  static_cast<unsigned long long>(mass[threadIdx.x]));
+                  static_cast<unsigned long long>(ms));
     }
 }
 
-// ---- 3: total mass, top-p target, crossing coarse bin ------------------------------------------
-__global__ __launch_bounds__(kThreads) void gen_cross_kernel(GenArgs a) {
+// ---- 3: crossing coarse bin (every block of the column finds it), then the fine counts inside it,
+// per tile. Block t == 0 writes the column's descriptor: total mass, top-p target, crossing bin.
+__global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
+    __shared__ uint32_t cnt[kGenBins];
     __shared__ uint64_t sh[kThreads];
     __shared__ float red[kThreads / 64];
     __shared__ int first;
-    const int c = blockIdx.x, b = blockIdx.y;
+    __shared__ uint64_t total;
+    const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
-    float m, inv_temp;
-    column_scale(a, cb, red, &m, &inv_temp);
+    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
+    float x[16];
+    load16(column_ptr(a, b, c), v0, a.V, x); // issued before the histogram arrives
     const int bin = kGenBins - 1 - static_cast<int>(threadIdx.x); // descending value order
     const uint32_t count = a.ccount[cb * kGenBins + bin];
     const uint64_t mass = a.cmass[cb * kGenBins + bin];
+    const float top_p = a.config->top_p;
     const uint64_t incl = block_scan<uint64_t>(mass, sh);
-    __shared__ uint64_t total;
     if (threadIdx.x == kThreads - 1) { total = incl; }
     __syncthreads();
     const uint64_t Z = total;
-    const float top_p = a.config->top_p;
     ColDesc d{};
-    d.m = m;
-    d.inv_temp = inv_temp;
-    d.z = Z;
+    if (t == 0) {
+        column_scale(a, cb, red, &d.m, &d.inv_temp);
+        d.z = Z;
+    }
     if (!(top_p < 1.0f)) {
-        if (threadIdx.x == 0) {
+        if (t == 0 && threadIdx.x == 0) {
             d.c1 = -1;
             d.nucleus = 0;
             d.zs = Z;
@@ -318,31 +338,21 @@ __global__ __launch_bounds__(kThreads) void gen_cross_kernel(GenArgs a) {
     }
     const uint64_t target = static_cast<uint64_t>((static_cast<u128>(Z) * fixed_u24(top_p)) >> 24);
     const int f = block_first(count != 0 && incl >= target, &first);
-    if (static_cast<int>(threadIdx.x) == f) {
+    if (t == 0 && static_cast<int>(threadIdx.x) == f) {
         d.c1 = bin;
         d.nucleus = 1;
         d.cum1 = incl - mass;
         d.target = target;
         a.desc[cb] = d;
     }
-}
-
-// ---- 4: fine counts inside the crossing coarse bin, per tile -----------------------------------
-__global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
-    __shared__ uint32_t cnt[kGenBins];
-    const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
-    const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
-    const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
-    float x[16];
-    load16(column_ptr(a, b, c), v0, a.V, x); // issued before the descriptor arrives
-    const ColDesc d = a.desc[cb];
-    if (!d.nucleus) { return; }
+    if (f >= kThreads) { return; }
+    const int c1 = kGenBins - 1 - f;
     cnt[threadIdx.x] = 0;
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const uint32_t o = ordered16(x[e]);
-        if (v0 + e < a.V && static_cast<int>(o >> 8) == d.c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
+        if (v0 + e < a.V && static_cast<int>(o >> 8) == c1) { atomicAdd(&cnt[o & 0xffu], 1u); }
     }
     __syncthreads();
     a.fine[(cb * a.ntiles + t) * kGenBins + threadIdx.x] = cnt[threadIdx.x];
@@ -733,8 +743,6 @@ void launch_general_accept(const GenLaunch& l, const GenPlan& plan, void* worksp
     check_launch("gen_max_kernel");
     hipLaunchKernelGGL(gen_coarse_kernel, tiles, dim3(kThreads), 0, stream, a);
     check_launch("gen_coarse_kernel");
-    hipLaunchKernelGGL(gen_cross_kernel, cols, dim3(kThreads), 0, stream, a);
-    check_launch("gen_cross_kernel");
     hipLaunchKernelGGL(gen_fine_kernel, tiles, dim3(kThreads), 0, stream, a);
     check_launch("gen_fine_kernel");
     hipLaunchKernelGGL(gen_nucleus_kernel, cols, dim3(kThreads), 0, stream, a);
