@@ -120,6 +120,29 @@ def test_batch_ragged(gpu):
     _check_out(out, ref, REL_L2_F32)
 
 
+def test_batch_one_long_many_short(gpu):
+    """The batch split plan gives the long sequence most of the workgroups and every short (or
+    empty) sequence one split; each sequence's splits merge in order."""
+    case = AttnCase([60000, 5, 0, 300, 1, 2000, 17, 128, 0, 9, 4000, 33], T=4, seed=22)
+    print("case batch B=12 one long", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def test_batch_more_sequences_than_split_budget(gpu):
+    """72 sequences over 8 KV heads exceed the 64 splits per KV head the plan targets: every
+    sequence then gets exactly one split."""
+    rng = np.random.default_rng(23)
+    case = AttnCase([int(x) for x in rng.integers(0, 150, size=72)], T=4, seed=23)
+    print("case batch B=72", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
 def _bfs_tree(n):
     """Binary tree in BFS order pruned to n nodes: parent(u) = (u - 1) // 2."""
     return [-1] + [(u - 1) // 2 for u in range(1, n)]
