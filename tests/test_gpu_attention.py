@@ -143,6 +143,19 @@ def test_batch_more_sequences_than_split_budget(gpu):
     _check_out(out, ref, REL_L2_F32)
 
 
+@pytest.mark.parametrize("T,Hq,Hkv,Ls", [(16, 40, 8, [3000]), (8, 64, 8, [2500]), (32, 40, 8, [1900]),
+                                          (7, 40, 8, [4100]), (12, 16, 2, [2222]), (16, 40, 8, [700, 5000, 0])])
+def test_many_query_rows(gpu, T, Hq, Hkv, Ls):
+    """More than 32 query rows per KV head: several row-chunk workgroups per (split, KV head), the
+    new rows appended by their own launch first."""
+    case = AttnCase(Ls, T=T, Hq=Hq, Hkv=Hkv, seed=2000 + T + Hq + len(Ls))
+    print(f"case rows T={T} Hq={Hq} Hkv={Hkv} Ls={Ls}", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
 def _bfs_tree(n):
     """Binary tree in BFS order pruned to n nodes: parent(u) = (u - 1) // 2."""
     return [-1] + [(u - 1) // 2 for u in range(1, n)]
