@@ -32,16 +32,35 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) { v = fmaxf(v, __shfl_xor(v, off, 64)); }
-    return v;
+// Wave-wide reductions by DPP: shifts by 1, 2, 4, 8 inside each 16-lane row, then lane 15 of rows
+// 0 and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31), so lane 63
+// ends with the whole wave's result, which every lane then reads. A lane whose DPP source is
+// outside its row (or masked off) combines with `identity`. No LDS round trip, unlike ds_bpermute
+// shuffles.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_from(float v, float identity) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
 }
 
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_from<0x111, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_from<0x112, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_from<0x114, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_from<0x118, 0xf>(v, -INFINITY));
+    v = fmaxf(v, dpp_from<0x142, 0xa>(v, -INFINITY));
+    v = fmaxf(v, dpp_from<0x143, 0xc>(v, -INFINITY));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// The lanes' values summed in one fixed order (the same bits on every run).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) { v += __shfl_xor(v, off, 64); }
-    return v;
+    v += dpp_from<0x111, 0xf>(v, 0.0f);
+    v += dpp_from<0x112, 0xf>(v, 0.0f);
+    v += dpp_from<0x114, 0xf>(v, 0.0f);
+    v += dpp_from<0x118, 0xf>(v, 0.0f);
+    v += dpp_from<0x142, 0xa>(v, 0.0f);
+    v += dpp_from<0x143, 0xc>(v, 0.0f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 // Reduction across the four 16-lane groups that share one MFMA column (lanes c, c+16, c+32, c+48).

@@ -87,13 +87,28 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
     return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
 }
 
+// One DPP step of the wave-wide maximum: the value of the lane that CTRL selects (0, the smallest
+// key, where that lane lies outside the row or is masked off).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp_max_u64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v & 0xffffffffu), CTRL, ROW_MASK, 0xf, false));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v >> 32), CTRL, ROW_MASK, 0xf, false));
+    const uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    return o > v ? o : v;
+}
+
+// Wave-wide maximum (row shifts 1, 2, 4, 8, then row broadcasts 15 and 31: lane 63 holds it, and
+// every lane reads it back). The whole wave must be active.
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint64_t o = shfl_xor_u64(v, off);
-        v = o > v ? o : v;
-    }
-    return v;
+    v = dpp_max_u64<0x111, 0xf>(v);
+    v = dpp_max_u64<0x112, 0xf>(v);
+    v = dpp_max_u64<0x114, 0xf>(v);
+    v = dpp_max_u64<0x118, 0xf>(v);
+    v = dpp_max_u64<0x142, 0xa>(v);
+    v = dpp_max_u64<0x143, 0xc>(v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v & 0xffffffffu), 63));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), 63));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
 
