@@ -206,13 +206,14 @@ __device__ __forceinline__ void load4(const uint16_t* col, int v0, int V, float 
     }
 }
 
-// Smallest thread index with `pred`, or kThreads.
+// Smallest thread index with `pred`, or kThreads: a ballot per wave, then the four waves' firsts
+// through LDS (sh: kThreads / 64 entries).
 __device__ int block_first(bool pred, int* sh) {
-    if (threadIdx.x == 0) { *sh = kThreads; }
+    const unsigned long long m = __ballot(pred);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sh[wave] = m != 0ull ? 64 * wave + __ffsll(static_cast<long long>(m)) - 1 : kThreads; }
     __syncthreads();
-    if (pred) { atomicMin(sh, static_cast<int>(threadIdx.x)); }
-    __syncthreads();
-    const int r = *sh;
+    const int r = min(min(sh[0], sh[1]), min(sh[2], sh[3]));
     __syncthreads();
     return r;
 }
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
     __shared__ uint32_t cnt[kGenBins];
     __shared__ uint64_t sh[kThreads];
     __shared__ float red[kThreads / 64];
-    __shared__ int first;
+    __shared__ int first[kThreads / 64];
     __shared__ uint64_t total;
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
@@ -352,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
         return;
     }
     const uint64_t target = static_cast<uint64_t>((static_cast<u128>(Z) * fixed_u24(top_p)) >> 24);
-    const int f = block_first(count != 0 && incl >= target, &first);
+    const int f = block_first(count != 0 && incl >= target, first);
     if (t == 0 && static_cast<int>(threadIdx.x) == f) {
         d.c1 = bin;
         d.nucleus = 1;
@@ -377,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void gen_fine_kernel(GenArgs a) {
 // ---- 5: crossing value, rank cut among equal values, kstar --------------------------------------
 __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     __shared__ uint64_t sh[kThreads];
-    __shared__ int first;
+    __shared__ int first[kThreads / 64];
     __shared__ uint64_t bcast[4];
     const int c = blockIdx.x, b = blockIdx.y;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
@@ -393,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     const uint64_t w = gen_weight(x, d.inv_temp, d.m);
     const uint64_t mass = count * w;
     const uint64_t incl = block_scan<uint64_t>(mass, sh);
-    const int fs = block_first(count != 0 && d.cum1 + incl >= d.target, &first);
+    const int fs = block_first(count != 0 && d.cum1 + incl >= d.target, first);
     if (static_cast<int>(threadIdx.x) == fs) {
         const uint64_t before = d.cum1 + incl - mass;
         // smallest j >= 1 with before + j * w >= target (w > 0 at the crossing)
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(kThreads) void gen_nucleus_kernel(GenArgs a) {
     uint64_t tc = 0;
     if (static_cast<int>(threadIdx.x) < a.ntiles) { tc = a.fine[(cb * a.ntiles + threadIdx.x) * kGenBins + fstar]; }
     const uint64_t tincl = block_scan<uint64_t>(tc, sh);
-    const int ts = block_first(static_cast<int>(threadIdx.x) < a.ntiles && tincl >= j, &first);
+    const int ts = block_first(static_cast<int>(threadIdx.x) < a.ntiles && tincl >= j, first);
     if (static_cast<int>(threadIdx.x) == ts) { bcast[3] = j - (tincl - tc); } // 1-based rank in tile
     __syncthreads();
     const uint64_t rank = bcast[3];
@@ -502,7 +503,7 @@ __device__ __forceinline__ DrawMass draw_mass_x(int rejected, const ColDesc& p, 
 __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
     __shared__ u128 shr[kThreads / 64];
     __shared__ uint64_t shp[kThreads / 64];
-    __shared__ int first;
+    __shared__ int first[kThreads / 64];
     __shared__ ColDesc sd[kMaxCols];
     const int t = blockIdx.x, b = blockIdx.y;
     DraftEntry e;
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
     load_decision_inputs(a, b, sd, &e, &ua);
     __syncthreads();
     int rejected;
-    const int acc = decide(a, sd, e, ua, &rejected, &first);
+    const int acc = decide(a, sd, e, ua, &rejected, first);
     const int col_p = rejected >= 0 ? rejected : a.K;
     const ColDesc p = sd[col_p];
     const ColDesc q = rejected >= 0 ? sd[a.K + 1 + rejected] : p;
@@ -542,7 +543,7 @@ __global__ __launch_bounds__(kThreads) void gen_totals_kernel(GenArgs a) {
 // last id with mass) and commit the round --------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     __shared__ u128 sh[kThreads / 64];
-    __shared__ int first;
+    __shared__ int first[kThreads / 64];
     __shared__ int last_tile;
     __shared__ int result;
     __shared__ u128 tile_before;
@@ -579,7 +580,7 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     const float u_bonus = a.u_accept[b * (a.K + 1) + a.K];
     __syncthreads();
     int rejected;
-    const int acc = decide(a, sd, e, ua, &rejected, &first);
+    const int acc = decide(a, sd, e, ua, &rejected, first);
     const int col_p = rejected >= 0 ? rejected : a.K;
     const ColDesc p = sd[col_p];
     const ColDesc q = rejected >= 0 ? sd[a.K + 1 + rejected] : p;
@@ -607,7 +608,7 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     const u128 goal = (total * fixed_u24(u)) >> 24;
     // The first tile whose running mass exceeds goal lies in the first thread whose inclusive sum
     // does (a tile that moves the running mass past goal has nonzero mass).
-    const int owner = block_first(tsum != 0 && incl > goal, &first);
+    const int owner = block_first(tsum != 0 && incl > goal, first);
     const bool crossing = owner < kThreads;
     if (tid == 0) {
         last_tile = -1;
