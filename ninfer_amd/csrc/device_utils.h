@@ -63,6 +63,37 @@ __device__ __forceinline__ float wave_sum(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// One step of a wave-wide inclusive scan of an integer: add the value that DPP control CTRL
+// brings from another lane (zero where that lane lies outside the row or is masked off), word by
+// word with carries.
+template <int CTRL, int ROW_MASK, typename T>
+__device__ __forceinline__ T dpp_scan_step(T v) {
+    constexpr int kWords = sizeof(T) / 4;
+    uint32_t w[kWords];
+    __builtin_memcpy(w, &v, sizeof(T));
+#pragma unroll
+    for (int i = 0; i < kWords; ++i) {
+        w[i] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(w[i]), CTRL, ROW_MASK, 0xf, true));
+    }
+    T o;
+    __builtin_memcpy(&o, w, sizeof(T));
+    return v + o;
+}
+
+// Inclusive scan over the 64 lanes of a wave: shifts by 1, 2, 4, 8 inside each 16-lane row, then
+// lane 15 of rows 0 and 2 into rows 1 and 3 (row_bcast:15), then lane 31 into rows 2 and 3
+// (row_bcast:31).
+template <typename T>
+__device__ __forceinline__ T wave_inclusive_scan(T v) {
+    v = dpp_scan_step<0x111, 0xf>(v);
+    v = dpp_scan_step<0x112, 0xf>(v);
+    v = dpp_scan_step<0x114, 0xf>(v);
+    v = dpp_scan_step<0x118, 0xf>(v);
+    v = dpp_scan_step<0x142, 0xa>(v);
+    v = dpp_scan_step<0x143, 0xc>(v);
+    return v;
+}
+
 // Reduction across the four 16-lane groups that share one MFMA column (lanes c, c+16, c+32, c+48).
 // v_permlane32_swap / v_permlane16_swap exchange half-waves and odd/even 16-lane rows in the VALU,
 // so each step is a register swap plus one op (no LDS round trip as with ds_bpermute). Both lanes

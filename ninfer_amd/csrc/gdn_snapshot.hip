@@ -24,12 +24,21 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-// Sum over the 16 lanes that own one state row (lanes 16i .. 16i+15 of the wave).
+// The value of the lane that DPP control CTRL selects inside the lane's 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes that own one state row (lanes 16i .. 16i+15 of the wave), all in the VALU:
+// swap neighbours (quad_perm 1,0,3,2), then pairs (quad_perm 2,3,0,1), then quads (row_half_mirror),
+// then half-rows (row_mirror). Each step adds a lane and its partner in either order, so every lane
+// of the row ends with the same bits.
 __device__ __forceinline__ float row_sum16(float x) {
-    x += __shfl_xor(x, 1, 16);
-    x += __shfl_xor(x, 2, 16);
-    x += __shfl_xor(x, 4, 16);
-    x += __shfl_xor(x, 8, 16);
+    x += dpp_row<0xB1>(x);
+    x += dpp_row<0x4E>(x);
+    x += dpp_row<0x141>(x);
+    x += dpp_row<0x140>(x);
     return x;
 }
 

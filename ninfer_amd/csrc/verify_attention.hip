@@ -140,10 +140,21 @@ __device__ __forceinline__ int seq_window(const int32_t* positions, int T, int m
     return max(0, min(positions[static_cast<int64_t>(i) * T + T - 1] + 1, max_keys));
 }
 
+// Wave-wide integer sum by DPP (row shifts 1, 2, 4, 8, then row broadcasts 15 and 31; lane 63
+// holds the total, which every lane reads back). The whole wave must be active.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_from_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+
 __device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) { v += __shfl_xor(v, off, 64); }
-    return v;
+    v += dpp_from_i<0x111, 0xf>(v);
+    v += dpp_from_i<0x112, 0xf>(v);
+    v += dpp_from_i<0x114, 0xf>(v);
+    v += dpp_from_i<0x118, 0xf>(v);
+    v += dpp_from_i<0x142, 0xa>(v);
+    v += dpp_from_i<0x143, 0xc>(v);
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 // max(1, ceil(w / kps)) in 32-bit arithmetic (w >= 0, kps >= 128).
@@ -214,12 +225,7 @@ __device__ SplitRange batch_split_range(const int32_t* positions, int T, int B, 
     for (int base = 0; base < B; base += 64) {
         const int i = base + lane;
         const int n = i < B ? splits_of(seq_window(positions, T, max_keys, i), kps) : 0;
-        int incl = n;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int o = __shfl_up(incl, off, 64);
-            if (lane >= off) { incl += o; }
-        }
+        const int incl = wave_inclusive_scan(n);
         const int excl = run + incl - n;
         if (table != nullptr && i < B) {
             table[2 * i] = excl;
@@ -233,7 +239,7 @@ __device__ SplitRange batch_split_range(const int32_t* positions, int T, int B, 
             r.count = __shfl(n, src, 64);
             if (table == nullptr) { return r; }
         }
-        run += __shfl(incl, 63, 64);
+        run += __builtin_amdgcn_readlane(incl, 63);
     }
     return r;
 }
