@@ -795,7 +795,7 @@ def main():
     if "c3_bf16" in result:
         line["long_context_bf16"] = {
             "workload": "C3 shape over a BF16 KV cache: context 260096, 1% outliers +-20, one layer "
-                        "(new rows copied into the cache by their own launch, then attention)",
+                        "(the attention launch copies the new rows into the cache itself)",
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3_bf16"].items()}}
     if "lm_head" in result:
         line["lm_head"] = {

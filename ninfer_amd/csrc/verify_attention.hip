@@ -99,8 +99,8 @@ struct AttnArgs {
     int8_t* vc;
     uint16_t* ks;
     uint16_t* vs;
-    const uint16_t* kb; // BF16 cache planes (BF16 kernel only)
-    const uint16_t* vb;
+    uint16_t* kb; // BF16 cache planes (BF16 kernel only)
+    uint16_t* vb;
     float* part_o;  // [row chunk][KV head][split_slots][32][D]
     float* part_ml; // [row chunk][KV head][split_slots][32][2]
     int32_t* seq_table; // B > 1: per sequence (first slot, split count), written by the partial launch
@@ -982,7 +982,11 @@ struct GeoB {
     static constexpr int kRingBytes = kWaves * STAGES * kStageBytes;
     static constexpr int kQTile = kRingBytes;       // Q tile: 32 rows x 2D B
     static constexpr int kPosLds = kQTile + 64 * D;
-    static constexpr int kSmemBytes = kPosLds + 128; // D=128: 139,392 B; D=256: 147,584 B
+    // D = 128: the new rows of A1 (32 rows of K and V) get a stage of their own; D = 256 has no room
+    // for one, and its A1 copies the new rows into the cache in a launch of their own.
+    static constexpr bool kFusedAppend = D == 128;
+    static constexpr int kNewStage = kPosLds + 128;
+    static constexpr int kSmemBytes = kFusedAppend ? kNewStage + kStageBytes : kPosLds + 128; // 155,776 B / 147,584 B
 };
 
 // Lane -> (row lane / PB, slot lane % PB) of each 1 KB DMA (512 / D rows); K slot s of row r holds
@@ -1254,17 +1258,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int pos_last = __builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]);
     const int window = min(pos_last + 1, a.max_keys);
     const int L = max(0, min(pos_first, window));
-    const int hend = min(k0 + kps, window); // the new rows are already in the cache
+    const int k1 = min(k0 + kps, window);
+    // With the fused append (D = 128) the new rows are copied into the cache by this launch: splits
+    // stream only the history below L, and the split holding L attends to the new rows from a stage
+    // built from the inputs. Otherwise they are already in the cache.
+    const bool fused = GB::kFusedAppend && a.k_new != nullptr;
+    const int hend = fused ? min(k1, L) : k1;
+    const bool owner = fused && L >= k0 && L < k0 + kps && L < window;
     const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
     float* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
-    if (k0 >= hend) {
+    if (k0 >= hend && !owner) {
         __builtin_amdgcn_s_waitcnt(0);
         if (threadIdx.x < 32) {
             out_ml[2 * threadIdx.x] = -INFINITY;
             out_ml[2 * threadIdx.x + 1] = 0.0f;
         }
         return;
+    }
+
+    if constexpr (GB::kFusedAppend) {
+        if (owner) {
+            // Every thread copies 16-byte pieces of the T new K/V rows into cache rows pos[t] and
+            // into the stage (K piece p of row r at slot p ^ (r % PB), V in natural order; rows
+            // without a new token, or whose position lies outside the cache, stay zero).
+            NMI_AS3 char* ns = (NMI_AS3 char*)smem + GB::kNewStage;
+            constexpr int PB = GB::PB;
+            for (int i = threadIdx.x; i < 32 * PB; i += blockDim.x) {
+                const int r = i / PB;
+                const int pc = i - r * PB;
+                i4 kv = {0, 0, 0, 0};
+                i4 vv = {0, 0, 0, 0};
+                const int pr = r < a.T ? pos_lds[r] : -1;
+                if (pr >= 0 && pr < a.P) {
+                    const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(a.Hkv) * (r + static_cast<int64_t>(a.T) * b)) + 8 * pc;
+                    kv = *reinterpret_cast<const i4*>(a.k_new + src);
+                    vv = *reinterpret_cast<const i4*>(a.v_new + src);
+                    *reinterpret_cast<i4*>(a.kb + head + static_cast<int64_t>(pr) * D + 8 * pc) = kv;
+                    *reinterpret_cast<i4*>(a.vb + head + static_cast<int64_t>(pr) * D + 8 * pc) = vv;
+                }
+                *(NMI_AS3 i4*)(ns + GB::kStageK + r * 2 * D + 16 * (pc ^ (r % PB))) = kv;
+                *(NMI_AS3 i4*)(ns + GB::kStageV + r * 2 * D + 16 * pc) = vv;
+            }
+            __syncthreads();
+            if (wave == 0) {
+                ChunkRegsB<D> r;
+                read_k_b<D>(ns, r, c, g);
+                read_v_b<D>(ns, r, c, g);
+                const KeyRange nk{L, L, min(window, L + a.T)};
+                f4 sacc[2][NT];
+                qk_chunk_b<NT, D>(r, qtile, c, g, R, sacc);
+                float p[NT][8];
+                softmax_probs<NT, D>(sacc, L, true, s, nk, g, p);
+                pv_chunk_b<NT, D>(p, r, L, true, s, nk, g);
+            }
+        }
     }
 
     const KeyRange hk{min(L, hend), L, hend};
@@ -1632,9 +1680,9 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
                              hipStream_t stream) {
     if (c.D != 128 && c.D != 256) { throw Unsupported("verify attention: head_dim 128 and 256 are built"); }
     if (plan.split_slots > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
-    if (k_new != nullptr && (plan.row_chunks > 1 || c.kb != nullptr)) {
-        // Several row-chunk workgroups read the new rows, or a BF16 cache (no in-kernel codec):
-        // write them in a launch of their own.
+    if (k_new != nullptr && (plan.row_chunks > 1 || (c.kb != nullptr && c.D != 128))) {
+        // Several row-chunk workgroups read the new rows, or a BF16 cache of head_dim 256 (no room
+        // for a new-row stage): write them in a launch of their own.
         launch_kv_append(k_new, v_new, positions, nullptr, T, c, stream);
         k_new = nullptr;
         v_new = nullptr;
