@@ -325,7 +325,9 @@ __device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers&
                                             int c0, int lane) {
     using G = Geo<D>;
     constexpr int NDMA = D / 32; // 1 KB code DMAs per plane
-    const int so = c0 * D;
+    // c0 is wave-uniform; lane 0's copy puts the DMA soffset in an SGPR (a VGPR soffset would make
+    // the compiler wrap every DMA in a readfirstlane loop).
+    const int so = __builtin_amdgcn_readfirstlane(c0) * D;
 #pragma unroll
     for (int r8 = 0; r8 < NDMA; ++r8) { dma16(hb.k, st + G::kStageK + r8 * 1024, dl.k[r8 % kvar<D>()], so + r8 * 1024); }
 #pragma unroll
@@ -1012,7 +1014,7 @@ template <int D>
 __device__ __forceinline__ void issue_k_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc_t rk, const DmaLanesB& dl, int c0) {
     using G = GeoB<D>;
     constexpr int ROWS = 512 / D; // rows per 1 KB DMA
-    const int so = c0 * 2 * D;
+    const int so = __builtin_amdgcn_readfirstlane(c0) * 2 * D; // wave-uniform, in an SGPR
 #pragma unroll
     for (int r = 0; r < D / 16; ++r) {
         const int koff = dl.row * 2 * D + 16 * (dl.slot ^ ((ROWS * r + dl.row) % G::PB));
@@ -1024,7 +1026,7 @@ __device__ __forceinline__ void issue_k_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc
 template <int D>
 __device__ __forceinline__ void issue_v_b(NMI_AS3 char* st, __amdgpu_buffer_rsrc_t rv, const DmaLanesB& dl, int c0) {
     using G = GeoB<D>;
-    const int so = c0 * 2 * D;
+    const int so = __builtin_amdgcn_readfirstlane(c0) * 2 * D; // wave-uniform, in an SGPR
 #pragma unroll
     for (int r = 0; r < D / 16; ++r) { dma16(rv, st + G::kStageV + r * 1024, dl.v, so + r * 1024); }
 }
