@@ -205,7 +205,7 @@ const char* nmi_last_error(void) { return g_last_error.c_str(); }
 const char* nmi_build_info(void) {
     return "ninfer_amd gfx950: verify_attn_partial<{1,2},{128,256}> fp16-MFMA 16x16x32 (INT8-G64 KV), "
            "verify_attn_partial_bf16<{1,2},{128,256}> bf16-MFMA 16x16x32 (BF16 KV), "
-           "verify_attn_merge, kv_quant_append, bf16_kv_append, argmax, speculative accept (greedy, top-20 "
+           "verify_attn_merge (B = 1) and verify_attn_merge_rows (batches), kv_quant_append, bf16_kv_append, argmax, speculative accept (greedy, top-20 "
            "stochastic, general fixed-point), kv commit/rollback/compaction, gdn_recurrent<{16,32,64,128}> "
            "(snapshot), conv1d_silu (snapshot), device scalars, linear_q6<{4,8,16} cols> f16-MFMA (Q6G64 lm_head, "
            "fused argmax)";
