@@ -1,6 +1,6 @@
 // CPU oracle for the MTP verify step. TEST INFRASTRUCTURE ONLY (see oracle.h).
 //
-// Built with -O2 -ffp-contract=off -fno-fast-math so every float operation is the one written
+// Built with -O3 -ffp-contract=off -fno-fast-math so every float operation is the one written
 // here; fused multiply-adds appear only where std::fma is called explicitly.
 #include "oracle.h"
 
@@ -257,35 +257,59 @@ void attention_core(const uint16_t* q, const int32_t* positions, const int32_t* 
         const size_t n = rows.size();
         std::vector<double> kd(n * D), vd(n * D);
         for (size_t r = 0; r < n; ++r) { decode(b, h, rows[r], &kd[r * D], &vd[r * D]); }
-        std::vector<double> sc(n), pr(n);
+        // Query rows (t, gi) of this KV head as doubles, transposed to [D][R] so the score loop runs
+        // keys outermost (each decoded key row is read once per job) while every dot product keeps
+        // its own d = 0..D-1 summation order; likewise the value loop keeps the r = 0..n-1 order of
+        // every output element.
+        const int32_t R = T * G;
+        std::vector<double> qt(static_cast<size_t>(D) * R);
         for (int32_t t = 0; t < T; ++t) {
             for (int32_t gi = 0; gi < G; ++gi) {
                 const int32_t qh = h * G + gi;
                 const uint16_t* qv = q + static_cast<size_t>(D) * (qh + static_cast<size_t>(Hq) * (t + static_cast<size_t>(T) * b));
-                double mx = -std::numeric_limits<double>::infinity();
-                for (size_t r = 0; r < n; ++r) {
-                    const bool visible = r < static_cast<size_t>(L) || vis[static_cast<size_t>(t) * T + (r - L)];
-                    if (!visible) {
-                        sc[r] = -std::numeric_limits<double>::infinity();
-                        continue;
-                    }
-                    double dot = 0.0;
-                    for (int32_t d = 0; d < D; ++d) { dot += static_cast<double>(bf16(qv[d])) * kd[r * D + d]; }
-                    sc[r] = dot * scale;
-                    mx = std::max(mx, sc[r]);
-                }
-                double den = 0.0;
-                for (size_t r = 0; r < n; ++r) {
-                    pr[r] = std::isinf(sc[r]) && sc[r] < 0 ? 0.0 : std::exp(sc[r] - mx);
-                    den += pr[r];
-                }
-                double* o = out + static_cast<size_t>(D) * (qh + static_cast<size_t>(Hq) * (t + static_cast<size_t>(T) * b));
-                for (int32_t d = 0; d < D; ++d) {
-                    double acc = 0.0;
-                    for (size_t r = 0; r < n; ++r) { acc += pr[r] * vd[r * D + d]; }
-                    o[d] = acc / den;
-                }
+                for (int32_t d = 0; d < D; ++d) { qt[static_cast<size_t>(d) * R + t * G + gi] = static_cast<double>(bf16(qv[d])); }
             }
+        }
+        std::vector<double> sc(static_cast<size_t>(R) * n), dot(R);
+        std::vector<double> mx(R, -std::numeric_limits<double>::infinity());
+        for (size_t r = 0; r < n; ++r) {
+            std::fill(dot.begin(), dot.end(), 0.0);
+            const double* kr = &kd[r * D];
+            for (int32_t d = 0; d < D; ++d) {
+                const double kv = kr[d];
+                const double* qd = &qt[static_cast<size_t>(d) * R];
+                for (int32_t i = 0; i < R; ++i) { dot[i] += qd[i] * kv; }
+            }
+            for (int32_t i = 0; i < R; ++i) {
+                const int32_t t = i / G;
+                const bool visible = r < static_cast<size_t>(L) || vis[static_cast<size_t>(t) * T + (r - L)];
+                double& s = sc[static_cast<size_t>(i) * n + r];
+                if (!visible) {
+                    s = -std::numeric_limits<double>::infinity();
+                    continue;
+                }
+                s = dot[i] * scale;
+                mx[i] = std::max(mx[i], s);
+            }
+        }
+        std::vector<double> acc(D);
+        for (int32_t i = 0; i < R; ++i) {
+            double* si = &sc[static_cast<size_t>(i) * n];
+            double den = 0.0;
+            for (size_t r = 0; r < n; ++r) {
+                si[r] = std::isinf(si[r]) && si[r] < 0 ? 0.0 : std::exp(si[r] - mx[i]);
+                den += si[r];
+            }
+            std::fill(acc.begin(), acc.end(), 0.0);
+            for (size_t r = 0; r < n; ++r) {
+                const double p = si[r];
+                const double* vr = &vd[r * D];
+                for (int32_t d = 0; d < D; ++d) { acc[d] += p * vr[d]; }
+            }
+            const int32_t t = i / G, gi = i % G;
+            const int32_t qh = h * G + gi;
+            double* o = out + static_cast<size_t>(D) * (qh + static_cast<size_t>(Hq) * (t + static_cast<size_t>(T) * b));
+            for (int32_t d = 0; d < D; ++d) { o[d] = acc[d] / den; }
         }
     };
 

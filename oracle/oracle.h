@@ -172,6 +172,12 @@ void orc_kv_compact_path(int32_t base, const int32_t* path, int32_t count, int32
 int32_t orc_tree_longest_path(const int32_t* parents, const int32_t* node_tokens,
                               const int32_t* target_tokens, int32_t nodes, int32_t* path);
 
+// ---- test-input generation (synth.cpp; not a restatement) ----------------------------------------
+// n seeded N(0, std_dev^2) values as BF16 bits, each replaced by +-outlier_value with probability
+// outlier_frac; the result depends on (seed, i) only, not on the thread count.
+void orc_fill_normal_bf16(uint64_t seed, size_t n, float std_dev, float outlier_frac,
+                          float outlier_value, uint16_t* out, int32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,12 @@ def lib() -> C.CDLL:
     return _lib
 
 
+def _threads(threads: int) -> int:
+    """Worker threads for the FP64 kernels: the caller's count, else the host's cores capped at 16
+    (the CPU share of one GPU box)."""
+    return threads if threads > 0 else max(1, min(16, os.cpu_count() or 1))
+
+
 def _ptr(a: np.ndarray | None):
     return None if a is None else a.ctypes.data_as(C.c_void_p)
 
@@ -86,6 +92,16 @@ def splitmix64(x: int) -> int:
 
 def sampling_uniform(seed: int, pos: int, purpose: int, sub: int = 0) -> float:
     return float(lib().orc_sampling_uniform(seed, pos, purpose, sub))
+
+
+def fill_normal_bf16(seed: int, n: int, std: float = 1.0, outlier_frac: float = 0.0,
+                     outlier_value: float = 20.0, threads: int = 0) -> np.ndarray:
+    """Seeded BF16 normals for workload-sized test inputs (synth.cpp)."""
+    out = np.empty(n, dtype=np.uint16)
+    lib().orc_fill_normal_bf16(C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), C.c_size_t(n), C.c_float(std),
+                               C.c_float(outlier_frac), C.c_float(outlier_value), _ptr(out),
+                               C.c_int32(_threads(threads)))
+    return out
 
 
 def quantize_group(src_bf16: np.ndarray):
@@ -112,7 +128,7 @@ def attention(q, kc, vc, ks, vs, positions, parents, T, B, Hq, Hkv, D, P, scale,
     out = np.zeros(D * Hq * T * B, dtype=np.float64)
     lib().orc_attention(_ptr(q), _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs), _ptr(positions), _ptr(par),
                         C.c_int32(T), C.c_int32(B), C.c_int32(Hq), C.c_int32(Hkv), C.c_int32(D),
-                        C.c_int32(P), C.c_double(scale), _ptr(out), C.c_int32(threads))
+                        C.c_int32(P), C.c_double(scale), _ptr(out), C.c_int32(_threads(threads)))
     return out
 
 
@@ -126,7 +142,7 @@ def attention_bf16(q, kb, vb, positions, parents, T, B, Hq, Hkv, D, P, scale, th
     out = np.zeros(D * Hq * T * B, dtype=np.float64)
     lib().orc_attention_bf16(_ptr(q), _ptr(kb), _ptr(vb), _ptr(positions), _ptr(par), C.c_int32(T),
                              C.c_int32(B), C.c_int32(Hq), C.c_int32(Hkv), C.c_int32(D), C.c_int32(P),
-                             C.c_double(scale), _ptr(out), C.c_int32(threads))
+                             C.c_double(scale), _ptr(out), C.c_int32(_threads(threads)))
     return out
 
 
@@ -138,7 +154,7 @@ def linear_q6(qdata, qhigh, scales, N, K, x, T, threads=0):
     x = np.ascontiguousarray(x, dtype=np.uint16)
     out = np.zeros(N * T, dtype=np.float64)
     lib().orc_linear_q6(_ptr(qdata), _ptr(qhigh), _ptr(scales), C.c_int32(N), C.c_int32(K), _ptr(x), C.c_int32(T),
-                        _ptr(out), C.c_int32(threads))
+                        _ptr(out), C.c_int32(_threads(threads)))
     return out.reshape(T, N)
 
 

@@ -36,12 +36,19 @@ def reference_composite_ok(got: np.ndarray, ref: np.ndarray, tol=ATTENTION_BF16)
     return ok, f"viol_frac={frac:.2e} worst={worst:.2f} rel_l2={l2:.3e}"
 
 
+def fast_normal_bf16(seed: int, n: int, std: float = 1.0, outliers: bool = False) -> np.ndarray:
+    """n N(0, std^2) values as BF16 bits from the oracle library's threaded generator; with
+    `outliers`, a seeded 1% of entries become +-20 (the long-context configuration's statistics)."""
+    from oracle import pyoracle
+    return pyoracle.fill_normal_bf16(seed, n, std, 0.01 if outliers else 0.0, 20.0)
+
+
 class AttnCase:
     """One verify-attention problem: BF16 history K/V quantized into INT8-G64 planes (or stored
     as BF16 when kv="bf16"), T new K/V columns, BF16 Q, positions L..L+T-1 per sequence."""
 
     def __init__(self, Ls, T=4, Hq=40, Hkv=8, D=128, seed=0, outliers=False, parents=None,
-                 max_context=None, qstd=1.0, kv="i8", dist="normal"):
+                 max_context=None, qstd=1.0, kv="i8", dist="normal", gen="splitmix"):
         self.Ls = list(Ls)
         self.B = len(self.Ls)
         self.T, self.Hq, self.Hkv, self.D = T, Hq, Hkv, D
@@ -50,9 +57,15 @@ class AttnCase:
         self.parents = parents
         self.kv = kv
         B, P, G = self.B, self.P, D // 64
-        gen = syn.normal_bf16_with_outliers if outliers else syn.normal_bf16
+        if gen == "pcg":
+            # workload-sized histories (10^8+ values): the same distributions from a threaded
+            # generator, at a fraction of the numpy SplitMix64/Box-Muller generator's cost
+            gen = (lambda sd, n: fast_normal_bf16(sd, n, outliers=True)) if outliers else fast_normal_bf16
+            gen_q = lambda sd, n: fast_normal_bf16(sd, n, qstd)  # noqa: E731
+        else:
+            gen = syn.normal_bf16_with_outliers if outliers else syn.normal_bf16
+            gen_q = lambda sd, n: syn.normal_bf16(sd, n, qstd)  # noqa: E731
         gen_k = gen_v = gen
-        gen_q = lambda sd, n: syn.normal_bf16(sd, n, qstd)  # noqa: E731
         if dist == "uniform":
             # the reference's op-test inputs: Q, K in [-0.25, 0.25), V in [-1, 1)
             # (tests/ops/test_gqa_attention.cpp:778-782)

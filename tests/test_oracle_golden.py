@@ -634,6 +634,146 @@ def test_general_emitted_distribution_equals_target(oracle):
     assert chi2 < 20.0, (chi2, counts / n, p)
 
 
+# Mode F against the mathematics (numpy float64, independent of the oracle's fixed-point code):
+# weights, the top-p nucleus, the emitted distribution at the C4 temperature and top-p, and the
+# reduction to Mode R when the draft distribution is one-hot.
+
+def _np_probs(x, temperature, top_p):
+    """float64 restatement: w = exp((x - max) / T); nucleus = shortest prefix in (value desc, id asc)
+    order whose mass reaches top_p * sum(w); p = w / mass on the nucleus, else 0."""
+    x = np.asarray(x, dtype=np.float64)
+    w = np.exp((x - x.max()) / temperature)
+    order = np.lexsort((np.arange(x.size), -x))
+    cum = np.cumsum(w[order])
+    n = x.size if top_p >= 1.0 else int(np.searchsorted(cum, top_p * cum[-1], side="left")) + 1
+    p = np.zeros_like(w)
+    keep = order[:n]
+    p[keep] = w[keep] / w[keep].sum()
+    return p, n, cum, order
+
+
+@pytest.mark.parametrize("temperature", [0.5, 0.7, 1.3])
+def test_general_weights_match_exp(oracle, temperature):
+    """Weights / 2^40 equal exp((x - max) / T) within the error of the FP32 evaluation: det_expf
+    (<= 1 ulp, 2^-23 relative), the FP32 reciprocal of T and the rounded products x / T and max / T
+    (each 2^-24 relative to the argument), then the 2^40 fixed-point rounding (2^-41 absolute). A
+    temperature applied the wrong way or a wrong maximum shift is off by orders of magnitude."""
+    V = 50000
+    col = syn.normal_bf16(60 + int(temperature * 10), V, np.sqrt(3.0))
+    x = syn.bf16_bits_to_f32(col).astype(np.float64)
+    n, w, member, zs, z = oracle.general_column(col, V, _gcfg(oracle, temperature, 1.0))
+    assert n == V and member.all() and zs == z == sum(int(v) for v in w)
+    exact = np.exp((x - x.max()) / temperature)
+    arg = (np.abs(x) + abs(x.max())) / temperature
+    bound = exact * (2.0 ** -22 + 4.0 * 2.0 ** -24 * arg) + 2.0 ** -41
+    got = w.astype(np.float64) / 2.0 ** 40
+    assert np.all(np.abs(got - exact) <= bound), float(np.max(np.abs(got - exact) / bound))
+    # the maximum's weight is exp(e) with e the FP32 rounding error of max / T (at most 2^-24 relative)
+    assert abs(int(w[int(np.argmax(x))]) / 2.0 ** 40 - 1.0) <= 2.0 ** -22 * (1.0 + abs(x.max()) / temperature)
+
+
+@pytest.mark.parametrize("temperature,top_p", [(0.7, 0.95), (0.5, 0.9), (1.3, 0.5), (0.7, 0.999)])
+def test_general_nucleus_matches_numpy(oracle, temperature, top_p):
+    """The nucleus is the float64 nucleus: the same size, except +-1 where the float64 cumulative
+    mass lies within 1e-6 of top_p * sum (the fixed-point sums may then round either way)."""
+    V = 20000
+    for seed in range(3):
+        col = syn.normal_bf16(700 + seed, V, np.sqrt(3.0))
+        x = syn.bf16_bits_to_f32(col).astype(np.float64)
+        n, w, member, zs, z = oracle.general_column(col, V, _gcfg(oracle, temperature, top_p))
+        _, n_np, cum, order = _np_probs(x, temperature, top_p)
+        if n != n_np:
+            edge = cum[min(n, n_np) - 1]
+            assert abs(n - n_np) == 1 and abs(edge - top_p * cum[-1]) <= 1e-6 * cum[-1], (n, n_np)
+        assert member[order[:n]].all() and member.sum() == n
+
+
+def test_general_emitted_distribution_t07_top_p(oracle):
+    """configs[3]'s temperature 0.7 and top-p 0.95: the first emitted token is distributed as the
+    float64 nucleus distribution of the target column (chi-square, 9 degrees of freedom at most),
+    with the draft token drawn from the float64 draft distribution."""
+    rows = 12
+    t = BF(np.array([1.9, 1.4, 1.2, 0.9, 0.7, 0.5, 0.1, -0.2, -0.6, -1.0, -1.5, -2.5], np.float32))
+    d = BF(np.array([0.4, 1.8, 0.3, 1.1, -0.5, 0.9, 0.6, -0.1, 0.2, -1.2, -0.4, 0.0], np.float32))
+    p, _, _, _ = _np_probs(syn.bf16_bits_to_f32(t), 0.7, 0.95)
+    q, _, _, _ = _np_probs(syn.bf16_bits_to_f32(d), 0.7, 0.95)
+    assert 0 < (p == 0).sum() and 0 < (q == 0).sum()  # both nuclei cut something off
+    logits = np.concatenate([t, t])
+    n = 30000
+    counts = np.zeros(rows)
+    us = syn.uniforms(1234, 3 * n)
+    cq = np.cumsum(q)
+    for i in range(n):
+        dr = min(int(np.searchsorted(cq, us[3 * i] * cq[-1], side="right")), rows - 1)
+        r = oracle.general_accept(logits, d, rows, [dr], 10, [0] * 5, rows, _gcfg(oracle, 0.7, 0.95),
+                                  np.array([us[3 * i + 1], 0.5], np.float32), float(us[3 * i + 2]))
+        counts[r["sampled_out"][0]] += 1
+    assert counts[p == 0].sum() == 0, "a token outside the target nucleus was emitted"
+    sel = p > 0
+    expected = p[sel] * n
+    chi2 = float(((counts[sel] - expected) ** 2 / expected).sum())
+    assert chi2 < 27.9, (chi2, counts / n, p)  # p = 0.001 quantile of chi2(9)
+
+
+def test_general_one_hot_q_reproduces_mode_r(oracle):
+    """With a one-hot draft distribution q = e_d, min(1, p/q) accepts iff u < p(d), and the residual
+    max(0, p - q) is p without d: Mode R's rule. Fed Mode R's own uniforms (accept, correction and
+    bonus streams at positions L+i+1 / L+K+1) and target columns whose nucleus is ordered by id
+    (logits strictly decreasing in id, so both inverse CDFs walk the same order), Mode F returns
+    Mode R's accept count and token. Trials with a uniform within 1e-5 of a float64 decision or CDF
+    boundary are skipped (FP32 versus fixed-point rounding may decide those either way)."""
+    V, K, L = 64, 3, 100
+    rng = np.random.default_rng(77)
+    compared = 0
+    trials = 300
+    for trial in range(trials):
+        cols, ps = [], []
+        for i in range(K + 1):
+            while True:
+                head = np.sort(rng.uniform(-1.0, 3.0, 8))[::-1].astype(np.float32)
+                x = np.full(V, -30.0, np.float32)
+                x[:8] = head
+                xb = BF(x)
+                xf = syn.bf16_bits_to_f32(xb)
+                if np.all(np.diff(xf[:8]) < 0):
+                    p, n_np, cum, _ = _np_probs(xf, 0.7, 0.95)
+                    if np.min(np.abs(cum[:8] - 0.95 * cum[-1])) > 1e-4 * cum[-1]:
+                        break
+            cols.append(xb)
+            ps.append(p)
+        target = np.concatenate(cols)
+        drafts = [int(v) for v in rng.integers(0, 8, K)]
+        seed = 1000 + trial
+        cfg = _cfg(oracle, 0.7, top_p=0.95, seed=seed)
+        r_mode = oracle.speculative_accept(None, target, V, drafts, L, [0] * (4 + K), V, cfg)
+        a = r_mode["accepted"]
+        u_acc = [oracle.sampling_uniform(seed, L + i + 1, 2) for i in range(K)]
+        u_bonus = oracle.sampling_uniform(seed, L + K + 1, 4)
+        u_corr = oracle.sampling_uniform(seed, L + a + 1, 3) if a < K else 0.5
+        # margins of every decision Mode R took
+        near = any(abs(u_acc[i] - ps[i][drafts[i]]) < 1e-5 for i in range(min(a + 1, K)))
+        if a < K:
+            rest = ps[a].copy()
+            rest[drafts[a]] = 0.0
+            u_pick, edges = u_corr, np.cumsum(rest) / max(rest.sum(), 1e-300)
+        else:
+            u_pick, edges = u_bonus, np.cumsum(ps[K])
+        near = near or np.min(np.abs(edges - u_pick)) < 1e-5
+        if near:
+            continue
+        one_hot = np.full((K, V), BF(np.array([-100.0], np.float32))[0], np.uint16)
+        for i, dr in enumerate(drafts):
+            one_hot[i, dr] = BF(np.array([0.0], np.float32))[0]
+        r_gen = oracle.general_accept(target, one_hot.reshape(-1), V, drafts, L, [0] * (4 + K), V,
+                                      _gcfg(oracle, 0.7, 0.95), np.array(u_acc + [u_bonus], np.float32),
+                                      float(u_corr))
+        assert r_gen["accepted"] == a, (trial, r_gen, r_mode)
+        assert r_gen["token"] == r_mode["token"], (trial, r_gen, r_mode)
+        assert list(r_gen["sampled_out"]) == list(r_mode["sampled_out"])
+        compared += 1
+    assert compared >= 0.9 * trials
+
+
 # ---- commit / rollback / compaction / tree ---------------------------------------------------------
 
 def _planes(P=256, H=2, D=128, seed=0):
