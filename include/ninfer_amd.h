@@ -150,6 +150,16 @@ int nmi_gqa_attention(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor
                       nmi_gqa_envelope envelope, void* workspace, size_t workspace_bytes,
                       nmi_tensor* out, nmi_stream_t stream);
 
+/* No counterpart in the reference: A1 exactly as nmi_gqa_attention (same validation, kernels and
+ * results), for callers that cannot allocate or pass a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The split-K partials go to a static
+ * 16 MiB per-device scratch array instead of a workspace, so the call allocates nothing; a plan
+ * needing more (NMI_UNSUPPORTED) must use nmi_gqa_attention. Calls that overlap on one GPU (two
+ * streams at once) race on that scratch; consecutive calls need no clearing in between. */
+int nmi_gqa_attention_noalloc(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                              const nmi_tensor* positions, float scale, const nmi_kv_layer_view* cache,
+                              nmi_gqa_envelope envelope, nmi_tensor* out, nmi_stream_t stream);
+
 /* A2, replaces gqa_kv_append (include/ninfer/ops/gqa_attention.h:80-81). */
 int nmi_gqa_kv_append(const nmi_tensor* k, const nmi_tensor* v, const nmi_tensor* positions,
                       const nmi_kv_layer_view* cache, nmi_stream_t stream);

@@ -153,6 +153,17 @@ inline void gqa_attention(const Tensor& q, const Tensor& k, const Tensor& v, con
     detail::check(nmi_gqa_attention(&cq, &ck, &cv, &cp, scale, &cc, envelope, ws, need, &co, detail::st(stream)));
 }
 
+// No reference counterpart: A1 for callers that cannot allocate or pass a workspace (graph capture,
+// serving loops); the split partials use the library's static per-device scratch (16 MiB).
+inline void gqa_attention_noalloc(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& positions,
+                                  float scale, KVCacheLayerView cache, GqaExecutionEnvelope envelope, Tensor& out,
+                                  hipStream_t stream) {
+    const nmi_tensor cq = q.c(), ck = k.c(), cv = v.c(), cp = positions.c();
+    nmi_tensor co = out.c();
+    const nmi_kv_layer_view cc = cache.c();
+    detail::check(nmi_gqa_attention_noalloc(&cq, &ck, &cv, &cp, scale, &cc, envelope, &co, detail::st(stream)));
+}
+
 // A2, include/ninfer/ops/gqa_attention.h:80-81.
 inline void gqa_kv_append(const Tensor& k, const Tensor& v, const Tensor& positions,
                           KVCacheLayerView cache, hipStream_t stream) {

@@ -126,6 +126,7 @@ _SIGNATURES = {
     "nmi_build_info": (C.c_char_p, []),
     "nmi_gqa_attention_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_uint32]),
     "nmi_gqa_attention": (C.c_int, [_T, _T, _T, _T, C.c_float, P(KVLayerView), GqaEnvelope, C.c_void_p, C.c_size_t, _T, _STREAM]),
+    "nmi_gqa_attention_noalloc": (C.c_int, [_T, _T, _T, _T, C.c_float, P(KVLayerView), GqaEnvelope, _T, _STREAM]),
     "nmi_gqa_kv_append": (C.c_int, [_T, _T, _T, P(KVLayerView), _STREAM]),
     "nmi_gqa_attention_cached": (C.c_int, [_T, _T, C.c_float, P(KVLayerView), GqaEnvelope, C.c_void_p, C.c_size_t, _T, _STREAM]),
     "nmi_gqa_attention_tree": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, P(KVLayerView), GqaEnvelope, C.c_int32, C.c_void_p, C.c_size_t, _T, _STREAM]),

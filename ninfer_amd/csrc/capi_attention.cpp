@@ -163,11 +163,13 @@ void require_workspace(void* ws, size_t bytes, size_t need, const std::string& o
     require((reinterpret_cast<uintptr_t>(ws) & 255u) == 0, op, "workspace must be 256-byte aligned");
 }
 
+// static_ws: the split partials go to the device's static scratch (the allocation-free entry
+// point); ws/ws_bytes are then ignored.
 int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
                    const nmi_tensor* positions, const nmi_tensor* parents, float scale,
                    const nmi_kv_layer_view* cache, nmi_gqa_envelope env, bool write_cache,
                    void* ws, size_t ws_bytes, nmi_tensor* out, hipStream_t stream,
-                   const std::string& op) {
+                   const std::string& op, bool static_ws = false) {
     return guarded([&] {
         const AttnShape s = validate_attention(q, positions, out, cache, env, scale, op);
         if (write_cache) { validate_new_kv(k, v, s.D, s.Hkv, s.T, s.B, op); }
@@ -179,6 +181,10 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
         }
         require_built(c, op);
         const SplitPlan plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys);
+        if (static_ws) {
+            ws = static_scratch(plan.bytes, op);
+            ws_bytes = plan.bytes;
+        }
         require_workspace(ws, ws_bytes, plan.bytes, op);
         launch_verify_attention(static_cast<const uint16_t*>(q->data),
                                 write_cache ? static_cast<const uint16_t*>(k->data) : nullptr,
@@ -228,6 +234,13 @@ int nmi_gqa_attention(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor
     return attention_impl(q, k, v, positions, nullptr, scale, cache, envelope, true, workspace,
                           workspace_bytes, out, reinterpret_cast<hipStream_t>(stream),
                           "gqa_attention");
+}
+
+int nmi_gqa_attention_noalloc(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
+                              const nmi_tensor* positions, float scale, const nmi_kv_layer_view* cache,
+                              nmi_gqa_envelope envelope, nmi_tensor* out, nmi_stream_t stream) {
+    return attention_impl(q, k, v, positions, nullptr, scale, cache, envelope, true, nullptr, 0, out,
+                          reinterpret_cast<hipStream_t>(stream), "gqa_attention_noalloc", true);
 }
 
 int nmi_gqa_attention_cached(const nmi_tensor* q, const nmi_tensor* positions, float scale,

@@ -45,6 +45,16 @@ inline constexpr int32_t kAttnMaxTokens = 32;
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
                          uint32_t max_visible_keys);
 
+// Size of the per-device static split scratch of nmi_gqa_attention_noalloc. 16 MiB holds every plan
+// of one sequence (T <= 32, any context, head_dim 128 or 256: at most 8.4 MiB) and of batches up to
+// ~100 sequences at T <= 6 (64 sequences at T = 4: 8.1 MiB); larger batches with several row chunks
+// need more and are rejected.
+inline constexpr size_t kStaticScratchBytes = size_t{16} << 20;
+
+// The calling device's static scratch (resolved on first use per device); throws Unsupported when
+// `need` exceeds kStaticScratchBytes.
+void* static_scratch(size_t need, const std::string& op);
+
 // Quantize-append: columns t (< *count when count != nullptr) of k/v BF16 [D, Hkv, T, B] into
 // rows positions[t + T*b].
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,

@@ -42,6 +42,13 @@ def gqa_attention(q, k, v, positions, scale, cache, envelope, workspace, out, st
                                   GqaEnvelope(*envelope), ws, nb, _p(out), _s(stream)))
 
 
+def gqa_attention_noalloc(q, k, v, positions, scale, cache, envelope, out, stream=None) -> None:
+    """A1 with the split partials in the library's static per-device scratch: allocates nothing,
+    takes no workspace (no reference counterpart; for callers that cannot allocate)."""
+    check(lib().nmi_gqa_attention_noalloc(_p(q), _p(k), _p(v), _p(positions), float(scale), C.byref(cache),
+                                          GqaEnvelope(*envelope), _p(out), _s(stream)))
+
+
 def gqa_kv_append(k, v, positions, cache, stream=None) -> None:
     """A2 (gqa_attention.h:80-81)."""
     check(lib().nmi_gqa_kv_append(_p(k), _p(v), _p(positions), C.byref(cache), _s(stream)))
