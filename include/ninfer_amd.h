@@ -72,6 +72,21 @@ typedef struct nmi_kv_layer_view {
     int32_t quant_group;
 } nmi_kv_layer_view;
 
+/* src/core/kv_cache.h:32-43 — cyclic K/V storage: absolute position p lives in row p % capacity.
+ * Planes as in nmi_kv_layer_view with P = padded_capacity. */
+typedef struct nmi_cyclic_kv_layer_view {
+    nmi_tensor k;
+    nmi_tensor v;
+    nmi_tensor k_scale;
+    nmi_tensor v_scale;
+    uint32_t capacity;
+    uint32_t padded_capacity;
+    int32_t num_kv_heads;
+    int32_t head_dim;
+    int32_t dtype; /* NMI_BF16 (the reference's) or NMI_I8 (INT8-G64) */
+    int32_t quant_group;
+} nmi_cyclic_kv_layer_view;
+
 /* include/ninfer/ops/gqa_attention.h:13-16 */
 typedef struct nmi_gqa_envelope {
     uint32_t min_visible_keys;
@@ -141,6 +156,13 @@ size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int3
                                          int32_t tokens, int32_t batch,
                                          uint32_t max_visible_keys);
 
+/* Replaces gqa_attention_workspace_bytes(q_heads, tokens) with its reference signature
+ * (include/ninfer/ops/gqa_attention.h:50; src/ops/wrapper/gqa_attention.cpp:229-245), as a status
+ * plus the size: the geometry follows from q_heads (24 -> 4 KV heads and 16 -> 2 at head_dim 256,
+ * the reference's registered ones; 40 -> 8 at head_dim 128), and the size covers every execution
+ * envelope of one sequence. tokens <= 0 or above 32 give 0; other q_heads NMI_INVALID_ARGUMENT. */
+int nmi_gqa_attention_workspace_bound(int32_t q_heads, int32_t tokens, size_t* bytes);
+
 /* A1, replaces gqa_attention (include/ninfer/ops/gqa_attention.h:71-73): quantize-append the T
  * new K/V columns at rows positions[t] and compute causal GQA over rows [0, positions[t]].
  * q/out BF16 [D, Hq, T(, B)]; k/v BF16 [D, Hkv, T(, B)]; positions I32 [T(, B)] sequential;
@@ -172,8 +194,9 @@ int nmi_gqa_attention_cached(const nmi_tensor* q, const nmi_tensor* positions, f
 
 /* EXTENSION (tree verification): A1/A3 with an ancestor mask. parents I32 [T(, B)], parents[0] =
  * -1, parents[u] < u. Node u occupies row positions[u]; query t sees history rows
- * [0, positions[0]) and the new rows of its ancestors-or-self. write_cache = 0 gives A3
- * (k and v may then be NULL). */
+ * [0, positions[0]) and the new rows of its ancestors-or-self. A parent outside [0, u) ends the
+ * ancestor walk there (nmi_tree_accept_greedy treats it the same way). write_cache = 0 gives A3
+ * (k and v may then be NULL). T above 32 returns NMI_UNSUPPORTED, as for A1 and A3. */
 int nmi_gqa_attention_tree(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
                            const nmi_tensor* positions, const nmi_tensor* parents, float scale,
                            const nmi_kv_layer_view* cache, nmi_gqa_envelope envelope,
@@ -237,12 +260,22 @@ int nmi_mtp_prepare_alignment_ids(const nmi_tensor* verify_ids, const nmi_tensor
 /* ---------------------------------------------------------------- commit / rollback (part c) */
 
 /* Replaces kv_cache_append_prefix (include/ninfer/ops/kv_cache_append_prefix.h:34-37) and
- * extends it to INT8-G64 caches: columns i < *commit_count are quantized (INT8) or copied (BF16)
- * into row positions[i]; no byte of a rejected column is written. */
+ * extends it to INT8-G64 caches and a trailing batch dimension (k/v [D, Hkv, T, B], positions
+ * [T, B], commit_count [B]): columns i < commit_count[b] are quantized (INT8) or copied (BF16)
+ * into row positions[i]; no byte of a rejected column is written, and a device count outside
+ * [envelope.min_count, envelope.max_count] writes nothing. */
 int nmi_kv_cache_append_prefix(const nmi_tensor* k, const nmi_tensor* v,
                                const nmi_tensor* positions, const nmi_tensor* commit_count,
                                nmi_commit_envelope envelope, const nmi_kv_layer_view* cache,
                                nmi_stream_t stream);
+
+/* Replaces the cyclic kv_cache_append_prefix overload (include/ninfer/ops/kv_cache_append_prefix.h:
+ * 40-51): the same commit into row positions[i] % capacity. The reference fixes capacity at 4096;
+ * any power of two from 128 up is accepted, and envelope.max_count must not exceed it. */
+int nmi_kv_cache_append_prefix_cyclic(const nmi_tensor* k, const nmi_tensor* v,
+                                      const nmi_tensor* positions, const nmi_tensor* commit_count,
+                                      nmi_commit_envelope envelope, const nmi_cyclic_kv_layer_view* cache,
+                                      nmi_stream_t stream);
 
 /* EXTENSION: explicit rollback — zero codes and scales of rows positions[i] for
  * i in [*keep_count, T). */

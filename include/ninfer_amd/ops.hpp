@@ -89,6 +89,32 @@ struct KVCacheLayerView {
     }
 };
 
+// src/core/kv_cache.h:32-43 — cyclic storage, absolute position p in row p % capacity.
+struct CyclicKVCacheLayerView {
+    Tensor k, v, k_scale, v_scale;
+    uint32_t capacity = 0;
+    uint32_t padded_capacity = 0;
+    int32_t num_kv_heads = 0;
+    int32_t head_dim = 0;
+    DType dtype = DType::BF16;
+    int32_t quant_group = 0;
+
+    nmi_cyclic_kv_layer_view c() const {
+        nmi_cyclic_kv_layer_view r{};
+        r.k = k.c();
+        r.v = v.c();
+        r.k_scale = k_scale.c();
+        r.v_scale = v_scale.c();
+        r.capacity = capacity;
+        r.padded_capacity = padded_capacity;
+        r.num_kv_heads = num_kv_heads;
+        r.head_dim = head_dim;
+        r.dtype = static_cast<int32_t>(dtype);
+        r.quant_group = quant_group;
+        return r;
+    }
+};
+
 using GqaExecutionEnvelope = nmi_gqa_envelope;
 using KVCacheAppendPrefixExecutionEnvelope = nmi_commit_envelope;
 using SamplingConfig = nmi_sampling_config; // same 40-byte device layout as the reference
@@ -131,7 +157,15 @@ inline nmi_stream_t st(hipStream_t s) { return reinterpret_cast<nmi_stream_t>(s)
 
 namespace ops {
 
-// include/ninfer/ops/gqa_attention.h:50 (geometry and envelope are explicit here).
+// include/ninfer/ops/gqa_attention.h:50, the reference signature: enough for every envelope of one
+// sequence at the geometry q_heads implies (24|4 and 16|2 at head_dim 256, 40|8 at 128).
+[[nodiscard]] inline std::size_t gqa_attention_workspace_bytes(int32_t q_heads, int32_t tokens) {
+    std::size_t n = 0;
+    detail::check(nmi_gqa_attention_workspace_bound(q_heads, tokens, &n));
+    return n;
+}
+
+// The exact size for one geometry, batch and envelope (what the ops below take from the arena).
 [[nodiscard]] inline std::size_t gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads,
                                                                int32_t head_dim, int32_t tokens,
                                                                int32_t batch,
@@ -279,6 +313,15 @@ inline void kv_cache_append_prefix(const Tensor& k, const Tensor& v, const Tenso
     const nmi_tensor ck = k.c(), cv = v.c(), cp = positions.c(), cc = commit_count.c();
     const nmi_kv_layer_view view = cache.c();
     detail::check(nmi_kv_cache_append_prefix(&ck, &cv, &cp, &cc, envelope, &view, detail::st(stream)));
+}
+
+// include/ninfer/ops/kv_cache_append_prefix.h:40-51 (cyclic cache).
+inline void kv_cache_append_prefix(const Tensor& k, const Tensor& v, const Tensor& positions,
+                                   const Tensor& commit_count, KVCacheAppendPrefixExecutionEnvelope envelope,
+                                   CyclicKVCacheLayerView cache, hipStream_t stream) {
+    const nmi_tensor ck = k.c(), cv = v.c(), cp = positions.c(), cc = commit_count.c();
+    const nmi_cyclic_kv_layer_view view = cache.c();
+    detail::check(nmi_kv_cache_append_prefix_cyclic(&ck, &cv, &cp, &cc, envelope, &view, detail::st(stream)));
 }
 
 // Extension: explicit rollback of rejected rows.

@@ -9,11 +9,12 @@ Layers:
 from __future__ import annotations
 
 from . import _capi
-from ._capi import (BF16, FP16, FP32, I8, I32, I64, U8, CommitEnvelope, GeneralConfig, GqaEnvelope,
-                    KVLayerView, SamplingConfig, Tensor, Weight, lib)
+from ._capi import (BF16, FP16, FP32, I8, I32, I64, U8, CommitEnvelope, CyclicKVLayerView, GeneralConfig,
+                    GqaEnvelope, KVLayerView, SamplingConfig, Tensor, Weight, lib)
 
 __all__ = [
-    "BF16", "FP16", "FP32", "I8", "I32", "I64", "Tensor", "KVLayerView", "GqaEnvelope", "Weight",
+    "BF16", "FP16", "FP32", "I8", "I32", "I64", "Tensor", "KVLayerView", "CyclicKVLayerView", "GqaEnvelope",
+    "Weight",
     "CommitEnvelope", "SamplingConfig", "GeneralConfig", "lib", "build_info",
 ]
 

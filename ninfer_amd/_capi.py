@@ -88,6 +88,23 @@ class KVLayerView(C.Structure):
     ]
 
 
+class CyclicKVLayerView(C.Structure):
+    """nmi_cyclic_kv_layer_view (src/core/kv_cache.h:32-43)."""
+
+    _fields_ = [
+        ("k", Tensor),
+        ("v", Tensor),
+        ("k_scale", Tensor),
+        ("v_scale", Tensor),
+        ("capacity", C.c_uint32),
+        ("padded_capacity", C.c_uint32),
+        ("num_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("dtype", C.c_int32),
+        ("quant_group", C.c_int32),
+    ]
+
+
 class GqaEnvelope(C.Structure):
     _fields_ = [("min_visible_keys", C.c_uint32), ("max_visible_keys", C.c_uint32)]
 
@@ -125,6 +142,7 @@ _SIGNATURES = {
     "nmi_last_error": (C.c_char_p, []),
     "nmi_build_info": (C.c_char_p, []),
     "nmi_gqa_attention_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_uint32]),
+    "nmi_gqa_attention_workspace_bound": (C.c_int, [C.c_int32, C.c_int32, P(C.c_size_t)]),
     "nmi_gqa_attention": (C.c_int, [_T, _T, _T, _T, C.c_float, P(KVLayerView), GqaEnvelope, C.c_void_p, C.c_size_t, _T, _STREAM]),
     "nmi_gqa_attention_noalloc": (C.c_int, [_T, _T, _T, _T, C.c_float, P(KVLayerView), GqaEnvelope, _T, _STREAM]),
     "nmi_gqa_kv_append": (C.c_int, [_T, _T, _T, P(KVLayerView), _STREAM]),
@@ -151,6 +169,7 @@ _SIGNATURES = {
     "nmi_increment_i32_scalar": (C.c_int, [_T, _STREAM]),
     "nmi_increment_i64_scalar": (C.c_int, [_T, _STREAM]),
     "nmi_kv_cache_append_prefix": (C.c_int, [_T, _T, _T, _T, CommitEnvelope, P(KVLayerView), _STREAM]),
+    "nmi_kv_cache_append_prefix_cyclic": (C.c_int, [_T, _T, _T, _T, CommitEnvelope, P(CyclicKVLayerView), _STREAM]),
     "nmi_kv_cache_rollback": (C.c_int, [_T, _T, P(KVLayerView), _STREAM]),
     "nmi_kv_cache_compact_path": (C.c_int, [_T, _T, _T, P(KVLayerView), _STREAM]),
     "nmi_tree_accept_greedy": (C.c_int, [_T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _T, _STREAM]),

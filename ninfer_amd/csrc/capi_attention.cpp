@@ -42,15 +42,18 @@ int32_t checked_i32(uint32_t v, const std::string& op, const char* name) {
 
 // Cache view checks (reference validate_cache, src/ops/wrapper/gqa_attention.cpp:59-99) with a
 // runtime geometry and an optional trailing batch dimension.
+// `attention`: the attention kernels also need padded_context to be a multiple of 128 (the
+// reference's plan_kv_cache alignment); the commit ops take any padded_context >= max_context, as the
+// reference's append validation does (src/ops/wrapper/kv_cache_append_prefix.cpp:62-80).
 CacheRef validate_cache(const nmi_kv_layer_view* cache, int32_t kv_heads, int32_t batch,
-                        const std::string& op) {
+                        const std::string& op, bool attention = true) {
     require(cache != nullptr, op, "cache must be non-null");
     require(cache->dtype == NMI_I8 || cache->dtype == NMI_BF16, op, "invalid KV cache dtype");
     require(cache->num_kv_heads == kv_heads, op, "invalid KV cache geometry or dtype");
     require(cache->head_dim > 0 && cache->head_dim % kQuantGroup == 0, op, "invalid KV cache head_dim");
     require(cache->max_context != 0 && cache->padded_context >= cache->max_context, op,
             "invalid KV cache capacity");
-    require(cache->padded_context % 128 == 0, op, "padded_context must be a multiple of 128");
+    require(!attention || cache->padded_context % 128 == 0, op, "padded_context must be a multiple of 128");
     if (cache->dtype == NMI_BF16) {
         require(cache->quant_group == 0, op, "BF16 KV cache must not have quant_group");
     } else {
@@ -58,6 +61,10 @@ CacheRef validate_cache(const nmi_kv_layer_view* cache, int32_t kv_heads, int32_
     }
     const int32_t P = checked_i32(cache->padded_context, op, "padded_context");
     const int32_t D = cache->head_dim;
+    // The kernels address one KV head's plane through 32-bit buffer offsets.
+    if (static_cast<int64_t>(P) * D * (cache->dtype == NMI_I8 ? 1 : 2) >= (int64_t{1} << 31)) {
+        throw Unsupported(op + ": a KV head plane of 2^31 bytes or more (padded_context * head_dim) is not built");
+    }
     const int32_t code_dtype = cache->dtype == NMI_I8 ? NMI_I8 : NMI_BF16;
     require(cache->k.dtype == code_dtype && cache->v.dtype == code_dtype, op, "invalid KV cache code dtype");
     require_shape(cache->k, D, P, kv_heads, batch, op, "cache k");
@@ -125,7 +132,10 @@ AttnShape validate_attention(const nmi_tensor* q, const nmi_tensor* positions,
     s.Hkv = cache->num_kv_heads;
     s.out_f32 = out->dtype == NMI_FP32;
     require(s.T > 0, op, "T must be positive");
-    require(s.T <= kAttnMaxTokens, op, "T exceeds 32 verify tokens");
+    if (s.T > kAttnMaxTokens) {
+        // the reference serves larger T by its prompt route; this build serves verify rounds only
+        throw Unsupported(op + ": T above 32 query tokens (the prompt route) is not built");
+    }
     require(s.B > 0, op, "batch must be positive");
     require(s.Hkv > 0 && s.Hq > 0 && s.Hq % s.Hkv == 0, op, "unsupported Q/KV head geometry");
     require(s.Hq / s.Hkv <= kAttnRowsPerTile, op, "unsupported Q/KV head geometry");
@@ -196,6 +206,51 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
     });
 }
 
+// reference kv_cache_append_prefix, both overloads (src/ops/wrapper/kv_cache_append_prefix.cpp:40-123;
+// contract include/ninfer/ops/kv_cache_append_prefix.h:22-51), extended to INT8-G64 caches and to a
+// trailing batch dimension (k/v [D, Hkv, T, B], positions [T, B], commit_count [B]). A device count
+// outside the envelope writes nothing, as in the reference kernel. `slot_mask` selects the cyclic
+// form (row = position mod capacity).
+void append_prefix_impl(const nmi_tensor* k, const nmi_tensor* v, const nmi_tensor* positions,
+                        const nmi_tensor* commit_count, nmi_commit_envelope envelope,
+                        const nmi_kv_layer_view* cache, uint32_t capacity, int32_t slot_mask,
+                        hipStream_t stream, const std::string& op) {
+    require_tensor(k, op, "k");
+    require_tensor(v, op, "v");
+    require_tensor(positions, op, "positions");
+    require_tensor(commit_count, op, "commit_count");
+    require(k->dtype == NMI_BF16 && v->dtype == NMI_BF16, op, "k/v must be BF16");
+    require(positions->dtype == NMI_I32 && commit_count->dtype == NMI_I32, op,
+            "positions/commit_count must be I32");
+    const int32_t D = k->ne[0];
+    const int32_t Hkv = k->ne[1];
+    const int32_t T = k->ne[2];
+    const int32_t B = k->ne[3];
+    require(T > 0, op, "T must be positive");
+    require(Hkv == cache->num_kv_heads && D == cache->head_dim, op, "k/v do not match the cache");
+    validate_new_kv(k, v, D, Hkv, T, B, op);
+    require((reinterpret_cast<uintptr_t>(k->data) & 15u) == 0 && (reinterpret_cast<uintptr_t>(v->data) & 15u) == 0,
+            op, "k/v must be 16-byte aligned");
+    require_shape(*positions, T, B, 1, 1, op, "positions");
+    require_shape(*commit_count, B, 1, 1, 1, op, "commit_count");
+    require_contiguous_nonnull(*positions, op, "positions");
+    require_contiguous_nonnull(*commit_count, op, "commit_count");
+    require(envelope.min_count <= envelope.max_count && envelope.max_count <= static_cast<uint32_t>(T) &&
+                envelope.max_count <= capacity,
+            op, "invalid execution envelope");
+    const CacheRef c = validate_cache(cache, Hkv, B, op, false);
+    if (c.kc != nullptr) { require_built(c, op); }
+    require(c.kc != nullptr || D % 8 == 0, op, "BF16 head_dim must be a multiple of 8");
+    if (envelope.max_count == 0) { return; }
+    CommitBounds bounds;
+    bounds.min_count = static_cast<int32_t>(envelope.min_count);
+    bounds.max_count = static_cast<int32_t>(envelope.max_count);
+    bounds.slot_mask = slot_mask;
+    launch_kv_append(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
+                     static_cast<const int32_t*>(positions->data), static_cast<const int32_t*>(commit_count->data),
+                     bounds, T, c, stream);
+}
+
 } // namespace
 
 void set_last_error(const std::string& msg) { g_last_error = msg; }
@@ -220,11 +275,33 @@ const char* nmi_build_info(void) {
 size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                                          int32_t tokens, int32_t batch,
                                          uint32_t max_visible_keys) {
-    if (tokens <= 0 || batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 ||
-        head_dim <= 0 || max_visible_keys == 0 || q_heads / kv_heads > kAttnRowsPerTile) {
+    // 0 for invalid shapes and for T above 32 (no built route: the op itself reports NMI_UNSUPPORTED)
+    if (tokens <= 0 || tokens > kAttnMaxTokens || batch <= 0 || kv_heads <= 0 || q_heads <= 0 ||
+        q_heads % kv_heads != 0 || head_dim <= 0 || max_visible_keys == 0 || q_heads / kv_heads > kAttnRowsPerTile) {
         return 0;
     }
     return plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys).bytes;
+}
+
+// reference gqa_attention_workspace_bytes(q_heads, tokens) (src/ops/wrapper/gqa_attention.cpp:229-245):
+// the registered geometries keyed by query heads (kv_heads_for_q_heads, :24-28) plus the 40/8/128
+// verify geometry; the size covers every execution envelope of one sequence.
+int nmi_gqa_attention_workspace_bound(int32_t q_heads, int32_t tokens, size_t* bytes) {
+    const std::string op = "gqa_attention_workspace_bytes";
+    return guarded([&] {
+        require(bytes != nullptr, op, "bytes must be non-null");
+        *bytes = 0;
+        // T <= 0 needs nothing (as in the reference); T above 32 runs no route of this build.
+        if (tokens <= 0 || tokens > kAttnMaxTokens) { return; }
+        int32_t kv_heads = 0, head_dim = 0;
+        switch (q_heads) {
+        case 24: kv_heads = 4; head_dim = 256; break;
+        case 16: kv_heads = 2; head_dim = 256; break;
+        case 40: kv_heads = 8; head_dim = 128; break;
+        default: throw InvalidArgument(op + ": unsupported Q/KV head geometry");
+        }
+        *bytes = attention_workspace_bound(q_heads, kv_heads, head_dim, tokens);
+    });
 }
 
 int nmi_gqa_attention(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
@@ -287,59 +364,52 @@ int nmi_gqa_kv_append(const nmi_tensor* k, const nmi_tensor* v, const nmi_tensor
         validate_new_kv(k, v, D, Hkv, T, B, op);
         require_shape(*positions, T, B, 1, 1, op, "positions");
         require_contiguous_nonnull(*positions, op, "positions");
-        const CacheRef c = validate_cache(cache, Hkv, B, op);
+        const CacheRef c = validate_cache(cache, Hkv, B, op, false);
         require(static_cast<uint32_t>(T) <= cache->max_context, op, "T exceeds KV cache capacity");
         require_built(c, op);
         launch_kv_append(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                         static_cast<const int32_t*>(positions->data), nullptr, T, c,
+                         static_cast<const int32_t*>(positions->data), nullptr, CommitBounds{}, T, c,
                          reinterpret_cast<hipStream_t>(stream));
     });
 }
 
-// reference kv_cache_append_prefix (src/ops/wrapper/kv_cache_append_prefix.cpp; contract
-// include/ninfer/ops/kv_cache_append_prefix.h:22-37), extended to INT8-G64 caches and to a
-// trailing batch dimension (k/v [D, Hkv, T, B], positions [T, B], commit_count [B]).
 int nmi_kv_cache_append_prefix(const nmi_tensor* k, const nmi_tensor* v,
                                const nmi_tensor* positions, const nmi_tensor* commit_count,
                                nmi_commit_envelope envelope, const nmi_kv_layer_view* cache,
                                nmi_stream_t stream) {
     const std::string op = "kv_cache_append_prefix";
     return guarded([&] {
-        require_tensor(k, op, "k");
-        require_tensor(v, op, "v");
-        require_tensor(positions, op, "positions");
-        require_tensor(commit_count, op, "commit_count");
         require(cache != nullptr, op, "cache must be non-null");
-        require(k->dtype == NMI_BF16 && v->dtype == NMI_BF16, op, "k/v must be BF16");
-        require(positions->dtype == NMI_I32 && commit_count->dtype == NMI_I32, op,
-                "positions/commit_count must be I32");
-        const int32_t D = k->ne[0];
-        const int32_t Hkv = k->ne[1];
-        const int32_t T = k->ne[2];
-        const int32_t B = k->ne[3];
-        require(T > 0, op, "T must be positive");
-        require(Hkv == cache->num_kv_heads && D == cache->head_dim, op, "k/v do not match the cache");
-        validate_new_kv(k, v, D, Hkv, T, B, op);
-        require_shape(*positions, T, B, 1, 1, op, "positions");
-        require_shape(*commit_count, B, 1, 1, 1, op, "commit_count");
-        require_contiguous_nonnull(*positions, op, "positions");
-        require_contiguous_nonnull(*commit_count, op, "commit_count");
-        require(envelope.min_count <= envelope.max_count && envelope.max_count <= static_cast<uint32_t>(T),
-                op, "invalid execution envelope");
-        const CacheRef c = validate_cache(cache, Hkv, B, op);
-        const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-        if (cache->dtype == NMI_BF16) {
-            require(B == 1, op, "BF16 prefix commit takes one sequence");
-            launch_bf16_append_prefix(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                                      static_cast<const int32_t*>(positions->data),
-                                      static_cast<const int32_t*>(commit_count->data), T, Hkv, D, c.P,
-                                      static_cast<uint16_t*>(cache->k.data), static_cast<uint16_t*>(cache->v.data), st);
-            return;
-        }
-        require_built(c, op);
-        launch_kv_append(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                         static_cast<const int32_t*>(positions->data),
-                         static_cast<const int32_t*>(commit_count->data), T, c, st);
+        append_prefix_impl(k, v, positions, commit_count, envelope, cache, cache->max_context, 0x7FFFFFFF,
+                           reinterpret_cast<hipStream_t>(stream), op);
+    });
+}
+
+int nmi_kv_cache_append_prefix_cyclic(const nmi_tensor* k, const nmi_tensor* v,
+                                      const nmi_tensor* positions, const nmi_tensor* commit_count,
+                                      nmi_commit_envelope envelope, const nmi_cyclic_kv_layer_view* cache,
+                                      nmi_stream_t stream) {
+    const std::string op = "kv_cache_append_prefix";
+    return guarded([&] {
+        require(cache != nullptr, op, "cache must be non-null");
+        // reference validate_cyclic_cache (src/ops/wrapper/kv_cache_append_prefix.cpp:82-101) fixes
+        // the ring at 4096 slots; any power of two from 128 up is accepted here.
+        const uint32_t cap = cache->capacity;
+        require(cap >= 128 && cap <= (1u << 30) && (cap & (cap - 1)) == 0, op, "invalid cyclic cache");
+        require(cache->padded_capacity >= cap, op, "invalid cyclic cache");
+        nmi_kv_layer_view linear{};
+        linear.k = cache->k;
+        linear.v = cache->v;
+        linear.k_scale = cache->k_scale;
+        linear.v_scale = cache->v_scale;
+        linear.max_context = cap;
+        linear.padded_context = cache->padded_capacity;
+        linear.num_kv_heads = cache->num_kv_heads;
+        linear.head_dim = cache->head_dim;
+        linear.dtype = cache->dtype;
+        linear.quant_group = cache->quant_group;
+        append_prefix_impl(k, v, positions, commit_count, envelope, &linear, cap, static_cast<int32_t>(cap - 1),
+                           reinterpret_cast<hipStream_t>(stream), op);
     });
 }
 
@@ -359,7 +429,7 @@ int nmi_kv_cache_rollback(const nmi_tensor* positions, const nmi_tensor* keep_co
         require_shape(*keep_count, B, 1, 1, 1, op, "keep_count");
         require_contiguous_nonnull(*positions, op, "positions");
         require_contiguous_nonnull(*keep_count, op, "keep_count");
-        const CacheRef c = validate_cache(cache, cache->num_kv_heads, B, op);
+        const CacheRef c = validate_cache(cache, cache->num_kv_heads, B, op, false);
         require(c.kc != nullptr, op, "rollback is defined for INT8-G64 caches");
         launch_kv_rollback(static_cast<const int32_t*>(positions->data),
                            static_cast<const int32_t*>(keep_count->data), T, c,
@@ -388,7 +458,7 @@ int nmi_kv_cache_compact_path(const nmi_tensor* base_position, const nmi_tensor*
         require_contiguous_nonnull(*path, op, "path");
         require_contiguous_nonnull(*path_len, op, "path_len");
         require_contiguous_nonnull(*base_position, op, "base_position");
-        const CacheRef c = validate_cache(cache, cache->num_kv_heads, B, op);
+        const CacheRef c = validate_cache(cache, cache->num_kv_heads, B, op, false);
         require(c.kc != nullptr, op, "compaction is defined for INT8-G64 caches");
         launch_kv_compact_path(static_cast<const int32_t*>(base_position->data),
                                static_cast<const int32_t*>(path->data),

@@ -107,28 +107,6 @@ __global__ __launch_bounds__(256) void kv_compact_path_kernel(const int32_t* bas
     }
 }
 
-// BF16 cache prefix commit (reference kv_cache_append_prefix_flat_kernel semantics): column i <
-// *count is copied bit-for-bit into row positions[i].
-__global__ __launch_bounds__(256) void bf16_append_prefix_kernel(const uint16_t* k, const uint16_t* v,
-                                                                 const int32_t* positions,
-                                                                 const int32_t* count, int32_t Hkv,
-                                                                 int32_t D, int32_t P, uint16_t* kc,
-                                                                 uint16_t* vc) {
-    const int t = blockIdx.x;
-    if (t >= *count) { return; }
-    const int pos = positions[t];
-    if (pos < 0 || pos >= P) { return; }
-    const int vec_per_row = D / 8; // 8 BF16 per 16 bytes
-    for (int i = threadIdx.x; i < Hkv * vec_per_row; i += blockDim.x) {
-        const int h = i / vec_per_row;
-        const int part = i - h * vec_per_row;
-        const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(Hkv) * t) + 8 * part;
-        const int64_t dst = static_cast<int64_t>(D) * (pos + static_cast<int64_t>(P) * h) + 8 * part;
-        *reinterpret_cast<i4*>(kc + dst) = *reinterpret_cast<const i4*>(k + src);
-        *reinterpret_cast<i4*>(vc + dst) = *reinterpret_cast<const i4*>(v + src);
-    }
-}
-
 } // namespace
 
 void launch_kv_rollback(const int32_t* positions, const int32_t* keep_count, int32_t T,
@@ -148,14 +126,6 @@ void launch_kv_compact_path(const int32_t* base_position, const int32_t* path,
                        path, path_len, T, c.Hkv, c.D, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq,
                        c.scale_seq);
     check_launch("kv_compact_path_kernel");
-}
-
-void launch_bf16_append_prefix(const uint16_t* k, const uint16_t* v, const int32_t* positions,
-                               const int32_t* count, int32_t T, int32_t Hkv, int32_t D,
-                               int32_t P, uint16_t* kc, uint16_t* vc, hipStream_t stream) {
-    hipLaunchKernelGGL(bf16_append_prefix_kernel, dim3(T), dim3(256), 0, stream, k, v, positions,
-                       count, Hkv, D, P, kc, vc);
-    check_launch("bf16_append_prefix_kernel");
 }
 
 } // namespace nmi

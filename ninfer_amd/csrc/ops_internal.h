@@ -45,6 +45,9 @@ inline constexpr int32_t kAttnMaxTokens = 32;
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
                          uint32_t max_visible_keys);
 
+// The largest plan_attention(Hq, Hkv, D, T, 1, keys).bytes over every envelope (keys >= 1).
+size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T);
+
 // Size of the per-device static split scratch of nmi_gqa_attention_noalloc. 16 MiB holds every plan
 // of one sequence (T <= 32, any context, head_dim 128 or 256: at most 8.4 MiB) and of batches up to
 // ~100 sequences at T <= 6 (64 sequences at T = 4: 8.1 MiB); larger batches with several row chunks
@@ -55,10 +58,20 @@ inline constexpr size_t kStaticScratchBytes = size_t{16} << 20;
 // `need` exceeds kStaticScratchBytes.
 void* static_scratch(size_t need, const std::string& op);
 
-// Quantize-append: columns t (< *count when count != nullptr) of k/v BF16 [D, Hkv, T, B] into
-// rows positions[t + T*b].
+// Device-side bounds of a prefix commit: a device count outside [min_count, max_count] writes
+// nothing (the reference's launch-resource envelope, kv_cache_append_prefix.cuh), and position p
+// lands in row p & slot_mask (every bit for a linear cache, capacity - 1 for a cyclic ring).
+struct CommitBounds {
+    int32_t min_count = 0;
+    int32_t max_count = 0x7FFFFFFF;
+    int32_t slot_mask = 0x7FFFFFFF;
+};
+
+// Quantize-append (INT8-G64) or copy (BF16): columns t (< count[b] when count != nullptr, and only
+// when count[b] is inside the bounds) of k/v BF16 [D, Hkv, T, B] into rows positions[t + T*b].
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
-                      const int32_t* count, int32_t T, const CacheRef& cache, hipStream_t stream);
+                      const int32_t* count, CommitBounds bounds, int32_t T, const CacheRef& cache,
+                      hipStream_t stream);
 
 // Split-K verify attention over cache rows; parents == nullptr is the causal mask. With k_new/v_new
 // (A1) the new columns are quantized into rows positions[t] first, by the owning split.
@@ -74,8 +87,5 @@ void launch_kv_rollback(const int32_t* positions, const int32_t* keep_count, int
 void launch_kv_compact_path(const int32_t* base_position, const int32_t* path,
                             const int32_t* path_len, int32_t T, const CacheRef& cache,
                             hipStream_t stream);
-void launch_bf16_append_prefix(const uint16_t* k, const uint16_t* v, const int32_t* positions,
-                               const int32_t* count, int32_t T, int32_t Hkv, int32_t D,
-                               int32_t P, uint16_t* kc, uint16_t* vc, hipStream_t stream);
 
 } // namespace nmi

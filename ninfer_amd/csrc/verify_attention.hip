@@ -245,14 +245,19 @@ __device__ SplitRange batch_split_range(const int32_t* positions, int T, int B, 
 }
 
 // Visibility of new node u (0 <= u < T) from query token t, as a bitmask over u.
+// The ancestor walk follows parents[u] only while it lies in [0, u) (the tree contract; the greedy
+// tree acceptance treats any other parent the same way), so every read stays inside the T-entry
+// parents row and a malformed tree cannot make a later node visible.
 __device__ __forceinline__ uint32_t new_key_mask(const int32_t* parents, int32_t t) {
     if (parents == nullptr) { return t >= 31 ? 0xffffffffu : ((2u << t) - 1u); }
-    uint32_t m = 0;
+    uint32_t m = 1u << t;
     int32_t u = t;
 #pragma unroll 1
-    for (int guard = 0; guard < 32 && u >= 0 && u < 32; ++guard) {
-        m |= 1u << u;
-        u = parents[u];
+    for (int guard = 0; guard < 32; ++guard) {
+        const int32_t p = parents[u];
+        if (p < 0 || p >= u) { break; }
+        m |= 1u << p;
+        u = p;
     }
     return m;
 }
@@ -1563,19 +1568,24 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
 template <int D>
 __global__ __launch_bounds__(256) void kv_quant_append_kernel(const uint16_t* k, const uint16_t* v,
                                                               const int32_t* positions,
-                                                              const int32_t* count, int32_t T,
-                                                              int32_t Hkv, int32_t P, int8_t* kc,
-                                                              int8_t* vc, uint16_t* ks,
+                                                              const int32_t* count, CommitBounds cb,
+                                                              int32_t T, int32_t Hkv, int32_t P,
+                                                              int8_t* kc, int8_t* vc, uint16_t* ks,
                                                               uint16_t* vs, int64_t code_seq,
                                                               int64_t scale_seq) {
     constexpr int G = D / 64;
     const int t = blockIdx.x;
     const int b = blockIdx.y;
     const int h = blockIdx.z;
-    if (count != nullptr && t >= count[b]) { return; }
+    if (count != nullptr) {
+        const int n = count[b];
+        if (n < cb.min_count || n > cb.max_count || t >= n) { return; }
+    }
     const int lane = threadIdx.x & 63;
-    const int pos = positions[static_cast<int64_t>(b) * T + t];
-    if (pos < 0 || pos >= P) { return; }
+    const int p = positions[static_cast<int64_t>(b) * T + t];
+    if (p < 0) { return; }
+    const int pos = p & cb.slot_mask;
+    if (pos >= P) { return; }
     for (int unit = threadIdx.x >> 6; unit < 2 * G; unit += blockDim.x / 64) {
         const int which = unit / G;
         const int grp = unit - which * G;
@@ -1603,20 +1613,41 @@ __global__ __launch_bounds__(256) void kv_quant_append_kernel(const uint16_t* k,
 // BF16 cache append (A2, and A1 on a BF16 cache): column t of sequence b is copied bit for bit into
 // row positions[t] (reference gqa_kv_append on a BF16 cache). Block (t, b, h).
 __global__ __launch_bounds__(64) void bf16_kv_append_kernel(const uint16_t* k, const uint16_t* v, const int32_t* positions,
-                                                            const int32_t* count, int32_t T, int32_t Hkv, int32_t P,
-                                                            int32_t D, uint16_t* kb, uint16_t* vb, int64_t seq) {
+                                                            const int32_t* count, CommitBounds cb, int32_t T,
+                                                            int32_t Hkv, int32_t P, int32_t D, uint16_t* kb,
+                                                            uint16_t* vb, int64_t seq) {
     const int t = blockIdx.x;
     const int b = blockIdx.y;
     const int h = blockIdx.z;
-    if (count != nullptr && t >= count[b]) { return; }
-    const int pos = positions[static_cast<int64_t>(b) * T + t];
-    if (pos < 0 || pos >= P) { return; }
+    if (count != nullptr) {
+        const int n = count[b];
+        if (n < cb.min_count || n > cb.max_count || t >= n) { return; }
+    }
+    const int p = positions[static_cast<int64_t>(b) * T + t];
+    if (p < 0) { return; }
+    const int pos = p & cb.slot_mask;
+    if (pos >= P) { return; }
     const int64_t src = static_cast<int64_t>(D) * (h + static_cast<int64_t>(Hkv) * (t + static_cast<int64_t>(T) * b));
     const int64_t dst = static_cast<int64_t>(b) * seq + static_cast<int64_t>(D) * (pos + static_cast<int64_t>(P) * h);
     for (int i = threadIdx.x; i < D / 8; i += blockDim.x) {
         *reinterpret_cast<i4*>(kb + dst + 8 * i) = *reinterpret_cast<const i4*>(k + src + 8 * i);
         *reinterpret_cast<i4*>(vb + dst + 8 * i) = *reinterpret_cast<const i4*>(v + src + 8 * i);
     }
+}
+
+} // namespace
+
+namespace {
+
+// Splits per (sequence, row chunk, KV head) a batch-1 plan aims for: about 512 workgroups at
+// head_dim 128 (two per CU), 256 at head_dim 256 (its LDS map holds one workgroup per CU).
+int64_t wanted_splits(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B) {
+    const int32_t G = Hq / Hkv;
+    const int32_t per_chunk = std::min<int32_t>(std::max<int32_t>(1, kAttnRowsPerTile / G), T);
+    const int64_t row_chunks = (T + per_chunk - 1) / per_chunk;
+    const int64_t units = static_cast<int64_t>(Hkv) * B * row_chunks;
+    const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
+    return std::max<int64_t>(1, (target + units - 1) / units);
 }
 
 } // namespace
@@ -1628,10 +1659,8 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     p.tokens_per_chunk = std::max<int32_t>(1, kAttnRowsPerTile / p.G);
     p.tokens_per_chunk = std::min(p.tokens_per_chunk, T);
     p.row_chunks = (T + p.tokens_per_chunk - 1) / p.tokens_per_chunk;
-    const int64_t units = static_cast<int64_t>(Hkv) * B * p.row_chunks;
-    // D = 256 runs one workgroup per CU (its LDS map), D = 128 two.
     const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
-    const int64_t want = std::max<int64_t>(1, (target + units - 1) / units);
+    const int64_t want = wanted_splits(Hq, Hkv, D, T, B);
     // B > 1: the device cuts the batch's actual keys into at most split_budget splits per (row
     // chunk, KV head), sized so that every split workgroup is resident at once.
     const int64_t cols = static_cast<int64_t>(Hkv) * p.row_chunks;
@@ -1654,21 +1683,29 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     return p;
 }
 
+size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T) {
+    // A batch-1 plan never has more than wanted_splits() splits (at least that many keys per split
+    // cover any context), and it reaches that count once every split holds the minimum 256 keys.
+    const int64_t want = wanted_splits(Hq, Hkv, D, T, 1);
+    return plan_attention(Hq, Hkv, D, T, 1, static_cast<uint32_t>(want * kAttnMinKeysPerSplit)).bytes;
+}
+
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
-                      const int32_t* count, int32_t T, const CacheRef& c, hipStream_t stream) {
+                      const int32_t* count, CommitBounds bounds, int32_t T, const CacheRef& c,
+                      hipStream_t stream) {
     dim3 grid(T, c.B, c.Hkv);
     if (c.kb != nullptr) {
-        hipLaunchKernelGGL(bf16_kv_append_kernel, grid, dim3(64), 0, stream, k, v, positions, count, T, c.Hkv, c.P, c.D,
-                           c.kb, c.vb, c.code_seq);
+        hipLaunchKernelGGL(bf16_kv_append_kernel, grid, dim3(64), 0, stream, k, v, positions, count, bounds, T, c.Hkv,
+                           c.P, c.D, c.kb, c.vb, c.code_seq);
         check_launch("bf16_kv_append_kernel");
         return;
     }
     if (c.D == 128) {
         hipLaunchKernelGGL(kv_quant_append_kernel<128>, grid, dim3(256), 0, stream, k, v, positions,
-                           count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
+                           count, bounds, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
     } else if (c.D == 256) {
         hipLaunchKernelGGL(kv_quant_append_kernel<256>, grid, dim3(256), 0, stream, k, v, positions,
-                           count, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
+                           count, bounds, T, c.Hkv, c.P, c.kc, c.vc, c.ks, c.vs, c.code_seq, c.scale_seq);
     } else {
         throw Unsupported("kv append: head_dim 128 and 256 are built");
     }
@@ -1685,7 +1722,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     if (k_new != nullptr && (plan.row_chunks > 1 || (c.kb != nullptr && c.D != 128))) {
         // Several row-chunk workgroups read the new rows, or a BF16 cache of head_dim 256 (no room
         // for a new-row stage): write them in a launch of their own.
-        launch_kv_append(k_new, v_new, positions, nullptr, T, c, stream);
+        launch_kv_append(k_new, v_new, positions, nullptr, CommitBounds{}, T, c, stream);
         k_new = nullptr;
         v_new = nullptr;
     }

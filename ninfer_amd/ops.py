@@ -35,6 +35,14 @@ def gqa_attention_workspace_bytes(q_heads: int, kv_heads: int, head_dim: int, to
     return int(lib().nmi_gqa_attention_workspace_bytes(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys))
 
 
+def gqa_attention_workspace_bound(q_heads: int, tokens: int) -> int:
+    """gqa_attention_workspace_bytes(q_heads, tokens) with the reference signature
+    (gqa_attention.h:50): enough for every envelope of one sequence."""
+    n = C.c_size_t(0)
+    check(lib().nmi_gqa_attention_workspace_bound(int(q_heads), int(tokens), C.byref(n)))
+    return int(n.value)
+
+
 def gqa_attention(q, k, v, positions, scale, cache, envelope, workspace, out, stream=None) -> None:
     """A1: quantize-append k/v at `positions`, then causal GQA (gqa_attention.h:71-73)."""
     ws, nb = _ws(workspace)
@@ -203,6 +211,12 @@ def increment_i64_scalar(scalar, stream=None) -> None:
 def kv_cache_append_prefix(k, v, positions, commit_count, envelope, cache, stream=None) -> None:
     check(lib().nmi_kv_cache_append_prefix(_p(k), _p(v), _p(positions), _p(commit_count),
                                            CommitEnvelope(*envelope), C.byref(cache), _s(stream)))
+
+
+def kv_cache_append_prefix_cyclic(k, v, positions, commit_count, envelope, cache, stream=None) -> None:
+    """The cyclic overload (kv_cache_append_prefix.h:40-51): row = position % capacity."""
+    check(lib().nmi_kv_cache_append_prefix_cyclic(_p(k), _p(v), _p(positions), _p(commit_count),
+                                                  CommitEnvelope(*envelope), C.byref(cache), _s(stream)))
 
 
 def kv_cache_rollback(positions, keep_count, cache, stream=None) -> None:

@@ -241,12 +241,14 @@ void attention_core(const uint16_t* q, const int32_t* positions, const int32_t* 
             if (parents == nullptr) {
                 for (int32_t u = 0; u <= t; ++u) { vis[static_cast<size_t>(t) * T + u] = 1; }
             } else {
+                // ancestors-or-self; a parent outside [0, u) ends the walk (tree contract)
                 int32_t u = t;
-                int32_t guard = 0;
-                while (u >= 0 && guard <= T) {
-                    vis[static_cast<size_t>(t) * T + u] = 1;
-                    u = parents[static_cast<size_t>(b) * T + u];
-                    ++guard;
+                vis[static_cast<size_t>(t) * T + u] = 1;
+                while (true) {
+                    const int32_t p = parents[static_cast<size_t>(b) * T + u];
+                    if (p < 0 || p >= u) { break; }
+                    vis[static_cast<size_t>(t) * T + p] = 1;
+                    u = p;
                 }
             }
         }

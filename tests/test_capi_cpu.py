@@ -84,12 +84,20 @@ def _attention_args(**over):
     (dict(envelope=(1, 3)), "execution envelope is shorter than T"),
     (dict(k=_t(na.BF16, (128, 4, 4))), "invalid shape for k"),
     (dict(q=_t(na.BF16, (128, 36, 4))), "unsupported Q/KV head geometry"),
-    (dict(q=_t(na.BF16, (128, 40, 33)), out=_t(na.BF16, (128, 40, 33)), k=_t(na.BF16, (128, 8, 33)),
-          v=_t(na.BF16, (128, 8, 33)), positions=_t(na.I32, (33,))), "T exceeds 32"),
 ])
 def test_gqa_attention_validation(override, needle):
     a, ws = _attention_args(**override)
     with pytest.raises(ValueError, match=re.escape(needle)):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], a["cache"], a["envelope"], ws,
+                          a["out"])
+
+
+def test_gqa_attention_prompt_route_is_unsupported():
+    """T above 32 is valid for the reference (its prompt route, gqa_attention.h:59-60) but not built
+    here: NMI_UNSUPPORTED (NotImplementedError), not an invalid argument."""
+    a, ws = _attention_args(q=_t(na.BF16, (128, 40, 33)), out=_t(na.BF16, (128, 40, 33)),
+                            k=_t(na.BF16, (128, 8, 33)), v=_t(na.BF16, (128, 8, 33)), positions=_t(na.I32, (33,)))
+    with pytest.raises(NotImplementedError, match="T above 32"):
         ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], a["cache"], a["envelope"], ws,
                           a["out"])
 
@@ -372,3 +380,90 @@ def test_general_accept_limits():
         _call_general(_general_args(V=big), V=big, ws=_WS(1 << 20))
     assert ops.general_accept_workspace_bytes(248320, 3, 16) > 0
     assert ops.general_accept_workspace_bytes(big, 3, 1) == 0
+
+
+# ---- reference-signature workspace query, plane limits, cyclic commit validation -------------------
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(40, 8, 128), (24, 4, 256), (16, 2, 256)])
+def test_workspace_bound_covers_every_envelope(q_heads, kv_heads, head_dim):
+    """gqa_attention_workspace_bytes(q_heads, tokens) (gqa_attention.h:50) is at least the exact size of
+    every batch-1 envelope, and equals the largest of them."""
+    for T in (1, 2, 4, 6, 7, 16, 32):
+        bound = ops.gqa_attention_workspace_bound(q_heads, T)
+        sizes = [ops.gqa_attention_workspace_bytes(q_heads, kv_heads, head_dim, T, 1, keys)
+                 for keys in list(range(1, 4096, 61)) + [2 ** k + d for k in range(12, 31) for d in (-1, 0, 77)]]
+        assert max(sizes) <= bound and bound in sizes, (T, bound, max(sizes))
+
+
+def test_workspace_bound_reference_call_shapes():
+    """The reference sizes its arenas with gqa_attention_workspace_bytes(query_heads, tokens)
+    (src/targets/qwen3_6/impl/runtime/layouts_impl.h:152,253,286), including prefill token counts."""
+    assert ops.gqa_attention_workspace_bound(24, 1) > 0
+    assert ops.gqa_attention_workspace_bound(16, 4) > 0
+    assert ops.gqa_attention_workspace_bound(40, 0) == 0
+    assert ops.gqa_attention_workspace_bound(24, 4096) == 0  # no built route above 32 tokens
+    with pytest.raises(ValueError, match="unsupported Q/KV head geometry"):
+        ops.gqa_attention_workspace_bound(36, 4)
+
+
+def test_head_plane_of_2_31_bytes_is_unsupported():
+    """Kernels address a KV head's plane with 32-bit offsets: P * D * element bytes >= 2^31 is rejected
+    before any launch instead of reading wrong rows."""
+    P = 1 << 24  # INT8 at head_dim 128: exactly 2^31 bytes per plane
+    c = _cache(P=P, max_ctx=P - 8)
+    a, ws = _attention_args(cache=c, envelope=(1, 4100))
+    with pytest.raises(NotImplementedError, match="2\\^31"):
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], ws, a["out"])
+    c = _cache(P=P - 128, max_ctx=P - 200)
+    a, ws = _attention_args(cache=c, envelope=(1, 4100))
+    with pytest.raises(ValueError, match="workspace"):  # passes the plane check, fails later on the host
+        ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], c, a["envelope"], _WS(16), a["out"])
+
+
+def _cyclic(cap=4096, padded=4096, dtype=None):
+    v = na.CyclicKVLayerView()
+    dtype = na.BF16 if dtype is None else dtype
+    v.k = _t(dtype, (128, padded, 8))
+    v.v = _t(dtype, (128, padded, 8))
+    v.k_scale = _t(na.FP16, (1,), ptr=0)
+    v.v_scale = _t(na.FP16, (1,), ptr=0)
+    v.capacity, v.padded_capacity, v.num_kv_heads, v.head_dim = cap, padded, 8, 128
+    v.dtype, v.quant_group = dtype, 0
+    return v
+
+
+def test_cyclic_commit_validation():
+    k = _t(na.BF16, (128, 8, 4))
+    pos, cnt = _t(na.I32, (4,)), _t(na.I32, (1,))
+    with pytest.raises(ValueError, match="invalid cyclic cache"):
+        ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (0, 4), _cyclic(cap=3000, padded=3072))
+    with pytest.raises(ValueError, match="invalid cyclic cache"):
+        ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (0, 4), _cyclic(padded=2048))
+    with pytest.raises(ValueError, match="invalid execution envelope"):
+        ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (3, 2), _cyclic())
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        kk = _t(na.BF16, (128, 8, 4), ptr=0x10002)
+        ops.kv_cache_append_prefix_cyclic(kk, kk, pos, cnt, (0, 4), _cyclic())
+    with pytest.raises(ValueError, match="must not have scales"):
+        c = _cyclic()
+        c.k_scale = _t(na.FP16, (1,))
+        ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (0, 4), c)
+
+
+def _driver():
+    """The compiled ops.hpp driver (tests/cpp), built by __graft_entry__.build(); rebuilt here if absent."""
+    import subprocess
+    exe = ROOT / "tests" / "cpp" / "ops_hpp_driver"
+    if not exe.exists():
+        subprocess.run(["make", "-s", "-C", str(exe.parent)], check=True)
+    return exe
+
+
+def test_compiled_cpp_layer_maps_statuses_to_reference_exceptions():
+    """include/ninfer_amd/ops.hpp compiled by hipcc as a reference caller would compile it: the
+    (q_heads, tokens) workspace query of layouts_impl.h:152, std::invalid_argument /
+    std::overflow_error from host validation, and std::runtime_error for the unbuilt prompt route."""
+    import subprocess
+    r = subprocess.run([str(_driver()), "errors"], capture_output=True, text=True, timeout=60)
+    print(r.stdout)
+    assert r.returncode == 0 and "ERRORS PASS" in r.stdout, r.stdout + r.stderr

@@ -186,3 +186,21 @@ def test_other_group_sizes(gpu, Hq, Hkv):
     out, cache = gpu_runner.run_attention(case, out_f32=True)
     _check_cache(cache, expected_cache)
     _check_out(out, ref, REL_L2_F32)
+
+
+def test_large_magnitude_groups_within_fp16_range(gpu):
+    """K' and V' enter the MFMA as FP16(code * scale): groups whose absolute maximum stays below
+    65,504 (FP16's largest finite value) decode exactly as the reference's FP32 decode does. Here
+    1% of the history's entries are +-20 and a few whole groups are scaled to an absolute maximum
+    of 6e4 (K and V), with Q small enough to keep the softmax non-degenerate."""
+    case = AttnCase([3000], T=4, seed=61, outliers=True, qstd=0.002)
+    rng = np.random.default_rng(61)
+    # the scales of 20 random (head, row, group) of K and of V become 6e4 / 127
+    for s in (case.ks, case.vs):
+        for _ in range(20):
+            h, r, g = int(rng.integers(0, 8)), int(rng.integers(0, 3000)), int(rng.integers(0, 2))
+            s[0, h, r, g] = np.float16(60000.0 / 127.0).view(np.uint16)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
