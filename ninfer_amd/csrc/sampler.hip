@@ -188,6 +188,77 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* logits, in
     (void)physical_rows;
 }
 
+// Multi-workgroup argmax: one 256-thread workgroup per (tile of kArgmaxTile rows, column), eight
+// 16-byte loads in flight per thread. The tile's best key (value as an ordered float with -0 = +0,
+// then the lowest row) is folded into out[col] by a compare-and-swap loop on the row index, which
+// compares against the key of the row out[col] holds at that moment (the reference's tiled atomic
+// route, src/ops/kernel/argmax.cuh:96-129). The reference zeroes out first with a memset
+// (src/ops/launcher/argmax.cu); here nothing needs initializing: a value outside [0, valid_rows)
+// counts as no candidate, and a row inside it is a real candidate whose key the argmax beats or
+// equals, so the loop ends at the argmax whatever out held before the call.
+constexpr int kArgmaxTile = 256 * 64;
+
+__global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits, int32_t* out,
+                                                          int32_t valid_rows, int64_t column_stride) {
+    const int col = blockIdx.y;
+    const uint16_t* x = logits + static_cast<int64_t>(col) * column_stride;
+    const int base = blockIdx.x * kArgmaxTile + threadIdx.x * 8;
+    uint64_t best = 0;
+    if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
+        i4 raw[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int r0 = base + u * 256 * 8;
+            raw[u] = r0 + 8 <= valid_rows ? *reinterpret_cast<const i4*>(x + r0) : i4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int r0 = base + u * 256 * 8;
+            if (r0 + 8 <= valid_rows) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint64_t k = sort_key(bf16_to_f32(bf16_at(raw[u], e)), r0 + e);
+                    best = k > best ? k : best;
+                }
+            } else {
+                for (int v = r0; v < valid_rows && v < r0 + 8; ++v) {
+                    const uint64_t k = sort_key(bf16_to_f32(x[v]), v);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    } else {
+        for (int u = 0; u < 8; ++u) {
+            for (int e = 0; e < 8; ++e) {
+                const int v = base + u * 256 * 8 + e;
+                if (v < valid_rows) {
+                    const uint64_t k = sort_key(bf16_to_f32(x[v]), v);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+    }
+    best = wave_max_u64(best);
+    __shared__ uint64_t wbest[4];
+    if ((threadIdx.x & 63) == 0) { wbest[threadIdx.x >> 6] = best; }
+    __syncthreads();
+    if (threadIdx.x != 0) { return; }
+    best = wbest[0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) { best = wbest[w] > best ? wbest[w] : best; }
+    if (best == 0) { return; } // no row of this tile is below valid_rows
+    int32_t* slot = out + col;
+    int cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int mine = key_index(best);
+    while (true) {
+        const uint64_t ck = (cur >= 0 && cur < valid_rows) ? sort_key(bf16_to_f32(x[cur]), cur) : 0ull;
+        if (ck >= best) { break; } // keys are unique per row: the holder is at least as good
+        const int seen = atomicCAS(slot, cur, mine);
+        if (seen == cur) { break; }
+        cur = seen;
+    }
+}
+
 // ---- verify inputs ---------------------------------------------------------------------------------
 
 // src/ops/kernel/speculative_round.cuh:19-28, per sequence b.
@@ -603,9 +674,16 @@ SpecPlan plan_spec(int32_t token_domain, int32_t columns, int32_t batch) {
 
 void launch_argmax(const uint16_t* logits, int32_t* out, int32_t physical_rows, int32_t valid_rows,
                    int32_t columns, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(columns), dim3(1024), 0, stream, logits, out,
-                       physical_rows, valid_rows, static_cast<int64_t>(physical_rows));
-    check_launch("argmax_kernel");
+    const int tiles = (valid_rows + kArgmaxTile - 1) / kArgmaxTile;
+    if (tiles < 2) {
+        hipLaunchKernelGGL(argmax_kernel, dim3(columns), dim3(1024), 0, stream, logits, out,
+                           physical_rows, valid_rows, static_cast<int64_t>(physical_rows));
+        check_launch("argmax_kernel");
+        return;
+    }
+    hipLaunchKernelGGL(argmax_tile_kernel, dim3(tiles, columns), dim3(256), 0, stream, logits, out, valid_rows,
+                       static_cast<int64_t>(physical_rows));
+    check_launch("argmax_tile_kernel");
 }
 
 void launch_prepare_verify_inputs(const int32_t* token, const int32_t* drafts, const int32_t* length,

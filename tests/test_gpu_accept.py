@@ -103,6 +103,28 @@ def test_argmax_packed_key_cases(gpu, oracle):
     assert list(out2.numpy()) == list(exp2)
 
 
+@pytest.mark.parametrize("prior", ["low_row", "negative", "huge", "answer", "last_row"])
+def test_argmax_whatever_out_held_before(gpu, oracle, prior):
+    """The tiled argmax folds its tiles into out[] by compare-and-swap without zeroing it first: an
+    in-range prior value is a real candidate the argmax beats or equals, an out-of-range one is
+    none, so the result is the argmax whatever out held (here also an odd physical stride, so the
+    columns take the unaligned path)."""
+    for rows, domain in ((248320, 248077), (100001, 99999)):
+        C = 4
+        x = syn.normal_bf16(13 + rows % 7, rows * C, std=2.0).reshape(C, rows)
+        x[1, 77] = BF(np.array([30.0], dtype=np.float32))[0]
+        x[2, domain - 1] = BF(np.array([30.0], dtype=np.float32))[0]
+        exp = oracle.argmax(x.reshape(-1), rows, C, domain)
+        low = [int(np.argmin(syn.bf16_bits_to_f32(x[c, :domain]))) for c in range(C)]
+        init = {"low_row": low, "negative": [-5] * C, "huge": [1 << 30] * C, "answer": list(exp),
+                "last_row": [domain - 1] * C}[prior]
+        d = DeviceArray.from_numpy(na.BF16, x, (rows, C))
+        out = DeviceArray.from_numpy(na.I32, np.array(init, np.int32), (C,))
+        ops.argmax(d.tensor(), out.tensor(), domain)
+        synchronize()
+        assert list(out.numpy()) == list(exp), (rows, prior)
+
+
 # ---- reference known answers -------------------------------------------------------------------------
 
 def test_prepare_verify_inputs_kat(gpu):
