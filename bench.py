@@ -85,14 +85,16 @@ def log(msg: str) -> None:
 class Layer:
     """One attention layer: its own cache planes, inputs, output and positions."""
 
-    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22, copy_from=None, kv_bf16=False):
+    def __init__(self, L, max_context, seed, outliers=False, gen_chunk=1 << 22, copy_from=None, kv_bf16=False,
+                 spare_rows=0):
         import ninfer_amd as na
         from ninfer_amd import device, ops, synthetic as syn
         from ninfer_amd.device import DeviceArray, synchronize
         from ninfer_amd.kv_cache import KVCacheLayer
 
         self.L = L
-        self.cache = KVCacheLayer(max_context, HKV, D, dtype=na.BF16 if kv_bf16 else na.I8)
+        # spare_rows: capacity past the envelope for rounds that append beyond the first step
+        self.cache = KVCacheLayer(max_context + spare_rows, HKV, D, dtype=na.BF16 if kv_bf16 else na.I8)
         rng = np.random.default_rng(seed)
         per_tok = D * HKV
         chunk = max(1, gen_chunk // per_tok)
@@ -525,6 +527,108 @@ def gdn_bench(stream, args):
                 frac_of_peak=gbs / HBM_PEAK_GBS, layers=GDN_LAYERS, tokens=T)
 
 
+ROUND_SPARE = 256  # cache rows past the C2 envelope: a round graph replayed N times appends up to 4N rows
+
+
+def q6_head(K: int, seed: int):
+    """A [VOCAB, K] Q6G64_F16S RowSplit output head in the reference payload layout: random code bytes,
+    FP16 scales of 1/16 (the time does not depend on the values)."""
+    import ninfer_amd as na
+    from ninfer_amd._capi import Q6G64_F16S
+    from ninfer_amd.device import DeviceBuffer
+    N = VOCAB
+    G = (K + 127) // 128 * 2
+    nb, hb, sb = N * G * 32, N * G * 16, N * G * 2
+    hoff = (nb + 255) // 256 * 256
+    soff = hoff + (hb + 255) // 256 * 256
+    buf = DeviceBuffer(soff + sb)
+    rng = np.random.default_rng(seed)
+    chunk = 1 << 26
+    for off in range(0, soff + sb, chunk):
+        n = min(chunk, soff + sb - off)
+        buf.upload(rng.integers(0, 256, n, dtype=np.uint8), off)
+    buf.upload(np.full(N * G, 0x2C00, np.uint16).view(np.uint8), soff)
+    w = na.Weight()
+    w.payload, w.payload_bytes, w.high_plane_bytes = buf.ptr, soff + sb, hb
+    w.qtype, w.group_size, w.ndim = Q6G64_F16S, 64, 2
+    w.shape[:] = [N, K, 1, 1]
+    w.padded_shape[:] = [N, G * 64, 1, 1]
+    w.qdata, w.qhigh, w.scales = buf.ptr, buf.ptr + hoff, buf.ptr + soff
+    w.n, w.k, w.group, w.layout, w.scale_dtype = N, K, 64, 0, na.FP16
+    return w, buf
+
+
+def round_bench(stream, args, layers, L2: int) -> dict:
+    """One whole greedy verify round captured as one graph and replayed back to back, every replay
+    continuing from the device state the previous one left (reference
+    src/targets/qwen3_6/impl/runtime/speculative_impl.h:35-45): prepare ids/positions from the device length -> the 64 layers' A1
+    attention at those positions -> Q6 lm_head [248320, 5120] over the 4 verify columns (BF16
+    logits) -> argmax -> greedy accept (length += A + 1) -> accepted hidden row -> MTP alignment
+    ids -> recurrent-state slot = accepted. Drafts are planted from the round's own targets: each
+    of the 3 drafts agrees with probability 0.8 (seeded; the prefix stops at the first miss)."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    K, HID = T - 1, 5120
+    w, wbuf = q6_head(HID, seed=5120)
+    rng = np.random.default_rng(77)
+    x = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, HID * T).astype(np.float32)), (HID, T))
+    hidden = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(HID * T, dtype=np.float32)), (HID, T))
+    logits = DeviceArray(na.BF16, (VOCAB, T))
+    target = DeviceArray(na.I32, (T,))
+    # the round's targets do not change between replays (same x, same head): read them once
+    ops.linear(x.tensor(), w, logits.tensor(), stream)
+    ops.argmax(logits.tensor(), target.tensor(), VOCAB, stream)
+    stream.synchronize()
+    tg = target.numpy()
+    agree = rng.random(K) < 0.8
+    drafts_h = np.array([tg[i] if agree[: i + 1].all() else (tg[i] + 1) % VOCAB for i in range(K)], np.int32)
+    st = dict(token=DeviceArray.from_numpy(na.I32, np.array([7], np.int32), (1,)),
+              drafts=DeviceArray.from_numpy(na.I32, drafts_h, (K,)),
+              length=DeviceArray.from_numpy(na.I32, np.array([L2], np.int32), (1,)),
+              ids=DeviceArray(na.I32, (T,)), pos=DeviceArray(na.I32, (T,)),
+              so=DeviceArray(na.I32, (T,)), ns=DeviceArray(na.I32, (1,)), acc=DeviceArray(na.I32, (1,)),
+              stats=DeviceArray.from_numpy(na.I64, np.zeros(4 + K, np.int64), (4 + K,)),
+              sel=DeviceArray(na.BF16, (HID, 1)), align=DeviceArray(na.I32, (T,)),
+              slot=DeviceArray.from_numpy(na.I32, np.zeros(1, np.int32), (1,)))
+    cfg = DeviceBuffer(40)
+    cfg.upload(np.frombuffer(bytes(memoryview(na.SamplingConfig())), dtype=np.uint8))
+    sws = DeviceBuffer(max(256, ops.sampling_workspace_bytes(VOCAB, T)))
+    env = (1, L2 + T + ROUND_SPARE)
+    ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, env[1]))
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+
+    def one_round():
+        ops.speculative_prepare_verify_inputs(st["token"].tensor(), st["drafts"].tensor(), st["length"].tensor(),
+                                              st["ids"].tensor(), st["pos"].tensor(), stream)
+        for ly in layers:
+            ops.gqa_attention(ly.q.tensor(), ly.k.tensor(), ly.v.tensor(), st["pos"].tensor(), scale, ly.view, env,
+                              ws, ly.out.tensor(), stream)
+        ops.linear(x.tensor(), w, logits.tensor(), stream)
+        ops.argmax(logits.tensor(), target.tensor(), VOCAB, stream)
+        ops.speculative_accept_greedy_drafts(target.tensor(), logits.tensor(), st["drafts"].tensor(),
+                                             st["length"].tensor(), st["token"].tensor(), st["so"].tensor(),
+                                             st["ns"].tensor(), st["acc"].tensor(), st["stats"].tensor(), VOCAB,
+                                             cfg.ptr, sws, stream)
+        ops.speculative_select_accepted_hidden(hidden.tensor(), st["acc"].tensor(), st["sel"].tensor(), stream)
+        ops.mtp_prepare_alignment_ids(st["ids"].tensor(), st["token"].tensor(), st["acc"].tensor(),
+                                      st["align"].tensor(), stream)
+        ops.assign_i32_scalar(st["acc"].tensor(), st["slot"].tensor(), stream)
+
+    g = capture(stream, one_round)
+    reps = min(args.steps, (ROUND_SPARE - T) // T - args.warmup)
+    ms, p95, _ = time_graph(g, stream, reps, args.warmup)
+    stats = st["stats"].numpy()
+    rounds = int(stats[2])
+    produced = (int(stats[1]) + rounds) / rounds
+    length = int(st["length"].numpy()[0])
+    assert length == L2 + int(stats[1]) + rounds, "round length bookkeeping"
+    del g, wbuf
+    return dict(round_ms=ms, round_p95_ms=p95, rounds=rounds, produced_per_round=produced,
+                tokens_per_s=produced / (ms * 1e-3), planted_accepted=int(agree.cumprod().sum()),
+                layers=len(layers), lm_head="Q6G64_F16S [248320, 5120] linear + argmax")
+
+
 def cpu_baseline(sample_layers: int):
     """Oracle attention on the host for `sample_layers` C2 layers (reported only)."""
     from oracle import pyoracle
@@ -566,13 +670,15 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--only", choices=["c2", "c3", "c3_bf16", "sampler", "c4", "c5", "gdn", "lm_head", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "round", "c3", "c3_bf16", "sampler", "c4", "c5", "gdn", "lm_head", "copy"],
+                    default=None,
                     help="profile helper: run one workload's replays and exit (no JSON line); 'copy' "
                          "runs 256 MiB device-to-device copies, the reference kernel for HBM counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}). "
-              "The verify step shards by KV head or by context; see DESIGN.md.", file=sys.stderr)
+              "The verify step would shard by KV head (no exchange) or by context (one all-gather of the split "
+              "partials per layer).", file=sys.stderr)
         sys.exit(2)
 
     import ninfer_amd as na
@@ -648,10 +754,10 @@ def main():
         device.synchronize()
 
     # ---- C2: 64 layers at context 7680 + greedy acceptance --------------------------------------
-    if args.only in (None, "c2"):
+    if args.only in (None, "c2", "round"):
         L2 = 7680
         t0 = time.perf_counter()
-        layers = [Layer(L2, L2 + T, seed=1000 + i) for i in range(args.layers)]
+        layers = [Layer(L2, L2 + T, seed=1000 + i, spare_rows=ROUND_SPARE) for i in range(args.layers)]
         log(f"C2: {args.layers} layers generated + quantized in {time.perf_counter() - t0:.1f}s")
         ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, L2 + T))
         acc = make_accept_inputs(1, 3, seed=2, stochastic=False)
@@ -668,8 +774,8 @@ def main():
         acc1_ms, acc_p95, _ = time_graph(g_acc, stream, args.steps, args.warmup)
         acc_ms = time_graph(g_acc_r, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
         step_ms, step_p95, _ = time_graph(g_step, stream, args.steps, args.warmup)
-        if args.only:
-            log(f"C2 attention {attn_ms / args.layers * 1e3:.2f} us/layer")
+        if args.only == "c2":
+            log(f"C2 attention {attn_ms / args.layers * 1e3:.2f} us/layer, accept {acc_ms * 1e3:.2f} us")
             return
         us_layer = attn_ms * 1e3 / args.layers
         gbs = attn_bytes(L2) / (us_layer * 1e-6) / 1e9
@@ -686,7 +792,15 @@ def main():
                             step_ms=step_ms, step_p95_ms=step_p95, expected_tokens_per_step=produced,
                             planted_accepted=a_planted, tokens_per_s=produced / (step_ms * 1e-3))
         log(f"C2: {us_layer:.2f} us/layer, {gbs:.0f} GB/s, accept {acc_ms * 1e3:.1f} us, step {step_ms:.3f} ms")
-        del layers, g_attn, g_step
+        del g_attn, g_step
+        if args.only in (None, "round"):
+            rres = round_bench(stream, args, layers, L2)
+            result["round"] = rres
+            log(f"round: {rres['round_ms']:.3f} ms, {rres['produced_per_round']:.2f} tokens/round, "
+                f"{rres['tokens_per_s']:.1f} tokens/s")
+        del layers
+        if args.only == "round":
+            return
         device.synchronize()
 
     # ---- sampler: top-20 stochastic acceptance at B=1 and B=16 --------------------------------------
@@ -789,6 +903,12 @@ def main():
         "accept_us": round(c2["accept_us"], 2),
         "c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c2.items()},
     }
+    if "round" in result:
+        line["round"] = {
+            "workload": "whole greedy verify round as one replayed graph: prepare ids/positions, 64 A1 layers at "
+                        "context 7680+ (device-advanced positions), Q6 lm_head [248320, 5120] + argmax, greedy "
+                        "accept, accepted hidden row, MTP alignment ids, state slot; drafts planted at 0.8",
+            **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["round"].items()}}
     if "c3" in result:
         line["long_context"] = {"workload": "C3: context 260096, 1% outliers +-20, one layer",
                                 **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["c3"].items()}}
