@@ -465,9 +465,62 @@ def lm_head_bench(stream, args):
         out["bytes"] = byts
         out["fused_gbs"] = byts / (out["fused_us"] * 1e-6) / 1e9
         out["fused_frac_of_peak"] = out["fused_gbs"] / HBM_PEAK_GBS
+        if K == 5120:
+            out["mode_r"] = mode_r_head_bench(stream, args, w, N, K)
         res[f"k{K}"] = out
         del buf
     return res
+
+
+def mode_r_head_bench(stream, args, w, N: int, hidden: int) -> dict:
+    """Stochastic (Mode R: T = 0.7, top-p 0.95) verify of K = 3 drafts over the lm_head: the fused
+    lm_head -> top-20 candidates -> accept (speculative_accept_fused_head, no logits written) against
+    linear (BF16 logits) + speculative_accept_greedy_drafts (per-tile candidates, then merge + accept),
+    at B = 1 and B = 16, each call timed in a graph of CALLS_PER_GRAPH calls (the device state advances
+    from call to call)."""
+    import ninfer_amd as na
+    from ninfer_amd import ops, synthetic as syn
+    from ninfer_amd.device import DeviceArray, DeviceBuffer
+    import ctypes as C
+    Kd = 3
+    out = {}
+    for B in (1, 16):
+        T = (Kd + 1) * B
+        rng = np.random.default_rng(77 + B)
+        x = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, hidden * T).astype(np.float32)),
+                                   (hidden, Kd + 1, B))
+        x2 = DeviceArray(na.BF16, (hidden, T), buf=x.buf)  # the same bytes viewed as [hidden, T]
+        drafts = DeviceArray.from_numpy(na.I32, rng.integers(0, N, Kd * B).astype(np.int32), (Kd, B))
+        length = DeviceArray.from_numpy(na.I32, np.full(B, 600, np.int32), (B,))
+        scal = [DeviceArray(na.I32, (B,)) for _ in range(3)]
+        so = DeviceArray(na.I32, (Kd + 1, B))
+        stats = DeviceArray.from_numpy(na.I64, np.zeros((B, 4 + Kd), np.int64), (4 + Kd, B))
+        cfg = na.SamplingConfig()
+        cfg.temperature, cfg.top_p, cfg.seed = 0.7, 0.95, 5
+        cfg_buf = DeviceBuffer(C.sizeof(cfg) * B)
+        cfg_buf.upload(np.frombuffer(bytes(memoryview(cfg)) * B, dtype=np.uint8))
+        logits = DeviceArray(na.BF16, (N, Kd + 1, B))
+        logits2 = DeviceArray(na.BF16, (N, T), buf=logits.buf)
+        target = DeviceArray(na.I32, (Kd + 1, B))
+        ws_f = DeviceBuffer(ops.speculative_accept_fused_head_workspace_bytes(Kd, B))
+        ws_u = DeviceBuffer(max(256, ops.sampling_workspace_bytes(N, Kd + 1, B)))
+
+        def fused():
+            ops.speculative_accept_fused_head(x.tensor(), w, drafts.tensor(), length.tensor(), scal[0].tensor(),
+                                              so.tensor(), scal[1].tensor(), scal[2].tensor(), stats.tensor(), N,
+                                              cfg_buf.ptr, ws_f, stream)
+
+        def unfused():
+            ops.linear(x2.tensor(), w, logits2.tensor(), stream)
+            ops.speculative_accept_greedy_drafts(target.tensor(), logits.tensor(), drafts.tensor(), length.tensor(),
+                                                 scal[0].tensor(), so.tensor(), scal[1].tensor(), scal[2].tensor(),
+                                                 stats.tensor(), N, cfg_buf.ptr, ws_u, stream)
+        for name, fn in (("fused", fused), ("unfused", unfused)):
+            g = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
+            ms = time_graph(g, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
+            out[f"b{B}_{name}_us"] = ms * 1e3
+            del g
+    return out
 
 
 GDN_S, GDN_HQK, GDN_HV, GDN_LAYERS = 128, 16, 48, 48  # Qwen3.6-27B (src/targets/qwen3_6_27b/impl/config.h:23-26)

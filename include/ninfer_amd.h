@@ -316,6 +316,23 @@ size_t nmi_linear_argmax_workspace_bytes(int32_t tokens);
 int nmi_linear_argmax(const nmi_tensor* x, const nmi_weight* w, int32_t valid_rows, void* workspace,
                       size_t workspace_bytes, nmi_tensor* out, nmi_stream_t stream);
 
+/* EXTENSION: the lm_head and nmi_speculative_accept_greedy_drafts in one call, the logits never
+ * written: the top-cap half of the deferred FUT-F03 fusion
+ * (docs/maintainer/qwen3.6-35b-a3b-dflash-op-checklist.md:985-1001), replacing the per-tile
+ * candidate pass over materialized logits (src/ops/kernel/speculative_round.cuh:169-211).
+ * x BF16 [hidden, K+1, B]: the final hidden rows of every verify column; w as for nmi_linear;
+ * drafts .. config as for nmi_speculative_accept_greedy_drafts (config a DEVICE pointer). Per column
+ * the lm_head keeps the 20 largest keys of the BF16 logits over rows [0, token_domain), penalty
+ * adjusted for stochastic sequences and raw for greedy ones (whose target is the largest); the
+ * acceptance then runs as in nmi_speculative_accept_greedy_drafts. Decisions equal nmi_linear
+ * followed by nmi_argmax and nmi_speculative_accept_greedy_drafts on the same input. */
+size_t nmi_speculative_accept_fused_head_workspace_bytes(int32_t K, int32_t batch);
+int nmi_speculative_accept_fused_head(const nmi_tensor* x, const nmi_weight* w, const nmi_tensor* drafts,
+                                      nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,
+                                      nmi_tensor* num_sampled, nmi_tensor* accepted, nmi_tensor* stats,
+                                      int32_t token_domain, const nmi_sampling_config* config, void* workspace,
+                                      size_t workspace_bytes, nmi_stream_t stream);
+
 /* ---------------------------------------------------------------- recurrent state (hybrid layers) */
 
 /* Replaces gated_delta_rule_workspace_bytes (include/ninfer/ops/gated_delta_rule.h:18-21), as a

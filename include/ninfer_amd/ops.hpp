@@ -376,6 +376,24 @@ inline void linear_argmax(const Tensor& x, const nmi_weight& w, int32_t valid_ro
     detail::check(nmi_linear_argmax(&cx, &w, valid_rows, p, need, &co, detail::st(stream)));
 }
 
+// Extension: the lm_head and speculative_accept_greedy_drafts in one call (the logits never written).
+[[nodiscard]] inline std::size_t speculative_accept_fused_head_workspace_bytes(int32_t K, int32_t batch) {
+    return nmi_speculative_accept_fused_head_workspace_bytes(K, batch);
+}
+inline void speculative_accept_fused_head(const Tensor& x, const nmi_weight& w, const Tensor& drafts, Tensor& length,
+                                          Tensor& token, Tensor& sampled_out, Tensor& num_sampled, Tensor& accepted,
+                                          Tensor& stats, int32_t token_domain, const SamplingConfig* config,
+                                          WorkspaceArena& workspace, hipStream_t stream) {
+    auto scope = workspace.scope();
+    const std::size_t need = speculative_accept_fused_head_workspace_bytes(drafts.ne[0], drafts.ne[1]);
+    void* ws = need ? workspace.alloc_bytes(need) : nullptr;
+    const nmi_tensor cx = x.c(), cd = drafts.c();
+    nmi_tensor clen = length.c(), ctok = token.c(), cso = sampled_out.c(), cns = num_sampled.c(),
+               cacc = accepted.c(), cst = stats.c();
+    detail::check(nmi_speculative_accept_fused_head(&cx, &w, &cd, &clen, &ctok, &cso, &cns, &cacc, &cst, token_domain,
+                                                    config, ws, need, detail::st(stream)));
+}
+
 // ---- recurrent state of the hybrid layers -------------------------------------------------------
 
 // include/ninfer/ops/gated_delta_rule.h:18-21

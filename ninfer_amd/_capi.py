@@ -159,6 +159,9 @@ _SIGNATURES = {
     "nmi_linear": (C.c_int, [_T, P(Weight), _T, _STREAM]),
     "nmi_linear_argmax_workspace_bytes": (C.c_size_t, [C.c_int32]),
     "nmi_linear_argmax": (C.c_int, [_T, P(Weight), C.c_int32, C.c_void_p, C.c_size_t, _T, _STREAM]),
+    "nmi_speculative_accept_fused_head_workspace_bytes": (C.c_size_t, [C.c_int32, C.c_int32]),
+    "nmi_speculative_accept_fused_head": (C.c_int, [_T, P(Weight), _T, _T, _T, _T, _T, _T, _T, C.c_int32, C.c_void_p,
+                                                    C.c_void_p, C.c_size_t, _STREAM]),
     "nmi_gated_delta_rule_workspace_bytes": (C.c_int, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, P(C.c_size_t)]),
     "nmi_gated_delta_rule": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),
     "nmi_gated_delta_rule_snapshot": (C.c_int, [_T, _T, _T, _T, _T, C.c_float, C.c_int32, _T, _T, _T, _STREAM]),

@@ -2,6 +2,7 @@
 // the reference wrapper (src/ops/linear/linear.cpp:65-152,200-209).
 #include "common.h"
 #include "linear_internal.h"
+#include "sampler_internal.h"
 
 #include <limits>
 
@@ -27,16 +28,19 @@ struct Checked {
 };
 
 // src/ops/linear/linear.cpp:65-152 (shapes, RowSplit metadata, payload size) and :200-209 (Q6
-// alignment: 16-byte x/out/code/high, 4-byte scales).
+// alignment: 16-byte x/out/code/high, 4-byte scales). out_dtype < 0: no output tensor (the fused
+// acceptance form).
 Checked check(const nmi_tensor* x, const nmi_weight* w, const nmi_tensor* out, int32_t out_dtype) {
-    require(x != nullptr && w != nullptr && out != nullptr, "x, weight and out must be non-null");
+    require(x != nullptr && w != nullptr && (out != nullptr || out_dtype < 0), "x, weight and out must be non-null");
     require(x->dtype == NMI_BF16, "x must be BF16");
     require(x->ne[2] == 1 && x->ne[3] == 1, "x must have shape [K,T]");
     require(w->n > 0 && w->k > 0, "weight n/k must be positive");
     require(x->ne[0] == w->k, "x K dimension must match weight.k");
     const int32_t T = x->ne[1];
     require(T >= 1, "T must be positive");
-    if (out_dtype == NMI_BF16) {
+    if (out_dtype < 0) {
+        out = x; // only x is checked below
+    } else if (out_dtype == NMI_BF16) {
         require(out->dtype == NMI_BF16 && out->ne[2] == 1 && out->ne[3] == 1 && out->ne[1] == T, "out must have shape [N,T]");
         require(out->ne[0] == w->n, "out N dimension must match weight.n");
     } else {
@@ -64,7 +68,7 @@ Checked check(const nmi_tensor* x, const nmi_weight* w, const nmi_tensor* out, i
     require(w->payload_bytes >= expected, "payload is too small");
     require(w->qdata != nullptr && w->scales != nullptr, "nibble and scale planes must be non-null");
     require(w->qhigh != nullptr && w->high_plane_bytes >= high, "high plane must be non-null");
-    require(aligned(x->data, 16) && aligned(out->data, out_dtype == NMI_BF16 ? 16 : 4) && aligned(w->qdata, 16) &&
+    require(aligned(x->data, 16) && aligned(out->data, out_dtype == NMI_I32 ? 4 : 16) && aligned(w->qdata, 16) &&
                 aligned(w->qhigh, 16) && aligned(w->scales, 4),
             "Q6 RowSplit requires 16-byte x/out/code/high and 4-byte scale alignment");
     if (Kp > static_cast<uint64_t>(kLinearMaxPaddedK) || nib >= (1ull << 31)) {
@@ -123,6 +127,48 @@ int nmi_linear_argmax(const nmi_tensor* x, const nmi_weight* w, int32_t valid_ro
         const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         launch_linear_q6(c.args, p, s);
         launch_linear_argmax_reduce(c.args.keys, c.T, p.grid * p.waves, static_cast<int32_t*>(out->data), s);
+    });
+}
+
+size_t nmi_speculative_accept_fused_head_workspace_bytes(int32_t K, int32_t batch) {
+    if (K < 1 || K + 1 > kMaxColumns || batch < 1) { return 0; }
+    return linear_topcap_workspace_bytes((K + 1) * batch);
+}
+
+int nmi_speculative_accept_fused_head(const nmi_tensor* x, const nmi_weight* w, const nmi_tensor* drafts,
+                                      nmi_tensor* length, nmi_tensor* token, nmi_tensor* sampled_out,
+                                      nmi_tensor* num_sampled, nmi_tensor* accepted, nmi_tensor* stats,
+                                      int32_t token_domain, const nmi_sampling_config* config, void* workspace,
+                                      size_t workspace_bytes, nmi_stream_t stream) {
+    const std::string op = "speculative_accept_fused_head";
+    return guarded([&] {
+        int32_t B = 0;
+        SpecArgs s = check_accept_state(drafts, length, token, sampled_out, num_sampled, accepted, stats, config, op, B);
+        const int32_t K = s.K;
+        require(x != nullptr && x->ne[1] == K + 1 && x->ne[2] == B && x->ne[3] == 1,
+                "x must be [hidden, K+1, B] (the verify columns of every sequence)");
+        nmi_tensor x2 = *x; // the columns of all sequences as one [hidden, (K+1) * B] operand
+        x2.ne[1] = (K + 1) * B;
+        x2.ne[2] = 1;
+        x2.nb[2] = x2.nb[1] * x2.ne[1];
+        Checked c = check(&x2, w, nullptr, -1);
+        require(token_domain >= 1 && token_domain <= w->n, "token_domain must be in [1, weight.n]");
+        const size_t need = linear_topcap_workspace_bytes(c.T);
+        require(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 256),
+                "workspace must be non-null, 256-byte aligned and at least the size query");
+        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T, true);
+        c.args.valid_rows = token_domain;
+        c.args.cand = static_cast<uint64_t*>(workspace);
+        c.args.config = config;
+        c.args.drafts = s.drafts;
+        c.args.cols_per_seq = K + 1;
+        const hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        launch_linear_q6(c.args, p, st);
+        s.target_tokens = nullptr;
+        s.partial = c.args.cand;
+        s.token_domain = token_domain;
+        s.ntiles = p.grid;
+        launch_spec_merge_accept_wide(s, B, st);
     });
 }
 

@@ -42,6 +42,45 @@ void require_workspace(void* ws, size_t bytes, size_t need, const std::string& o
 }
 
 } // namespace
+
+// Shapes shared by every chain acceptance (src/ops/wrapper/speculative_round.cpp:67-102): drafts
+// [K, B], length/token/num_sampled/accepted [B], sampled_out [K+1, B], stats [>=4+K, B], a non-null
+// device config; fills the state and output pointers of the kernel arguments.
+SpecArgs check_accept_state(const nmi_tensor* drafts, nmi_tensor* length, nmi_tensor* token,
+                            nmi_tensor* sampled_out, nmi_tensor* num_sampled, nmi_tensor* accepted,
+                            nmi_tensor* stats, const nmi_sampling_config* config, const std::string& op,
+                            int32_t& B) {
+    require(drafts != nullptr, op, "drafts must be non-null");
+    const int32_t K = drafts->ne[0];
+    B = drafts->ne[1];
+    require(K >= 1, op, "K must be >=1");
+    require(K + 1 <= kMaxColumns, op, "K must be <= 15");
+    require(B >= 1, op, "batch must be >=1");
+    require_matrix(drafts, NMI_I32, K, B, op, "drafts");
+    require_scalars(length, NMI_I32, B, op, "length");
+    require_scalars(token, NMI_I32, B, op, "token");
+    require_matrix(sampled_out, NMI_I32, K + 1, B, op, "sampled_out");
+    require_scalars(num_sampled, NMI_I32, B, op, "num_sampled");
+    require_scalars(accepted, NMI_I32, B, op, "accepted");
+    require_dtype(stats, NMI_I64, op, "stats");
+    require(stats->ne[0] >= 4 + K && stats->ne[1] == B && stats->ne[2] == 1 && stats->ne[3] == 1, op,
+            "invalid vector shape for stats");
+    require(config != nullptr, op, "config must be non-null");
+    SpecArgs a{};
+    a.drafts = static_cast<const int32_t*>(drafts->data);
+    a.length = static_cast<int32_t*>(length->data);
+    a.token = static_cast<int32_t*>(token->data);
+    a.sampled_out = static_cast<int32_t*>(sampled_out->data);
+    a.num_sampled = static_cast<int32_t*>(num_sampled->data);
+    a.accepted = static_cast<int32_t*>(accepted->data);
+    a.stats = static_cast<int64_t*>(stats->data);
+    a.config = config;
+    a.K = K;
+    a.columns = K + 1;
+    a.stats_stride = stats->ne[0];
+    return a;
+}
+
 } // namespace nmi
 
 using namespace nmi;
@@ -107,50 +146,25 @@ int nmi_speculative_accept_greedy_drafts(const nmi_tensor* target_tokens, const 
                                          size_t workspace_bytes, nmi_stream_t stream) {
     const std::string op = "speculative_accept_greedy_drafts";
     return guarded([&] {
-        require(drafts != nullptr, op, "drafts must be non-null");
-        const int32_t K = drafts->ne[0];
-        const int32_t B = drafts->ne[1];
-        require(K >= 1, op, "K must be >=1");
-        require(K + 1 <= kMaxColumns, op, "K must be <= 15");
-        require(B >= 1, op, "batch must be >=1");
+        int32_t B = 0;
+        SpecArgs a = check_accept_state(drafts, length, token, sampled_out, num_sampled, accepted, stats, config, op, B);
+        const int32_t K = a.K;
         require_matrix(target_tokens, NMI_I32, K + 1, B, op, "target_tokens");
         require_dtype(logits, NMI_BF16, op, "logits");
         require(logits->ne[0] > 0 && logits->ne[1] >= K + 1 && logits->ne[2] == B && logits->ne[3] == 1, op,
                 "logits must be [physical_rows, >=k+1]");
         require(token_domain > 0 && token_domain <= logits->ne[0], op, "token_domain must be in [1, logits.ne[0]]");
-        require_matrix(drafts, NMI_I32, K, B, op, "drafts");
-        require_scalars(length, NMI_I32, B, op, "length");
-        require_scalars(token, NMI_I32, B, op, "token");
-        require_matrix(sampled_out, NMI_I32, K + 1, B, op, "sampled_out");
-        require_scalars(num_sampled, NMI_I32, B, op, "num_sampled");
-        require_scalars(accepted, NMI_I32, B, op, "accepted");
-        require_dtype(stats, NMI_I64, op, "stats");
-        require(stats->ne[0] >= 4 + K && stats->ne[1] == B && stats->ne[2] == 1 && stats->ne[3] == 1, op,
-                "invalid vector shape for stats");
-        require(config != nullptr, op, "config must be non-null");
         const SpecPlan plan = plan_spec(token_domain, K + 1, B);
         require(plan.ntiles <= kMergeMaxTiles, op, "token_domain exceeds the candidate merge capacity (524288)");
         require_workspace(workspace, workspace_bytes, plan.bytes, op);
         char* ws = static_cast<char*>(workspace);
-        SpecArgs a{};
         a.target_tokens = static_cast<const int32_t*>(target_tokens->data);
         a.logits = static_cast<const uint16_t*>(logits->data);
-        a.drafts = static_cast<const int32_t*>(drafts->data);
-        a.length = static_cast<int32_t*>(length->data);
-        a.token = static_cast<int32_t*>(token->data);
-        a.sampled_out = static_cast<int32_t*>(sampled_out->data);
-        a.num_sampled = static_cast<int32_t*>(num_sampled->data);
-        a.accepted = static_cast<int32_t*>(accepted->data);
-        a.stats = static_cast<int64_t*>(stats->data);
-        a.config = config;
         a.partial = reinterpret_cast<uint64_t*>(ws + plan.partial_offset);
         a.logits_seq_stride = static_cast<int64_t>(logits->ne[0]) * logits->ne[1];
         a.physical_rows = logits->ne[0];
         a.token_domain = token_domain;
-        a.K = K;
-        a.columns = K + 1;
         a.ntiles = plan.ntiles;
-        a.stats_stride = stats->ne[0];
         launch_spec_accept(a, B, reinterpret_cast<hipStream_t>(stream));
     });
 }

@@ -5,6 +5,8 @@
 
 #include <cstdint>
 
+#include "common.h"
+
 namespace nmi {
 
 inline constexpr int kLinearGrid = 256;       // persistent workgroups (one per CU)
@@ -18,6 +20,13 @@ struct LinearArgs {
     const uint16_t* x;      // BF16 [K, T]
     uint16_t* out;          // BF16 [N, T], or null (argmax only)
     uint64_t* keys;         // argmax partial keys [T][waves], or null
+    // Top-cap form (the lm_head half of stochastic acceptance): per column, per workgroup, the
+    // kCandidateCap largest keys of the penalty-adjusted BF16 logits over rows [0, valid_rows),
+    // descending and 0-padded, at cand[(column * grid + workgroup) * kCandidateCap]; null = off.
+    uint64_t* cand;
+    const nmi_sampling_config* config; // [B] device configs (column t belongs to sequence t / cols_per_seq)
+    const int32_t* drafts;             // [cols_per_seq - 1, B]: the penalty overlay of each column
+    int32_t cols_per_seq;
     int64_t nib_bytes, high_bytes, scale_bytes;
     int32_t N, K, Kp, G, T;
     int32_t t0, tp;         // this pass: columns [t0, t0 + tp)
@@ -35,8 +44,10 @@ struct LinearPlan {
     size_t lds;
     int32_t passes;
 };
-LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T);
+LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap = false);
 size_t linear_argmax_workspace_bytes(int32_t T);
+// Candidate-list bytes of the top-cap form for T columns (any plan: at most one list per CU).
+size_t linear_topcap_workspace_bytes(int32_t T);
 
 void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream);
 void launch_linear_argmax_reduce(const uint64_t* keys, int32_t T, int32_t waves, int32_t* out, hipStream_t stream);

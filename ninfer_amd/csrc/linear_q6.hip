@@ -24,6 +24,7 @@
 #include "device_utils.h"
 #include "lds_dma.h"
 #include "linear_internal.h"
+#include "topcap.h"
 
 #include <algorithm>
 
@@ -60,25 +61,54 @@ __device__ __forceinline__ int swz(int row) { return (row / (256 / R)) % (R / 16
 
 __device__ __forceinline__ size_t x_lds_bytes(int TP, int Kp) { return static_cast<size_t>(TP) * (Kp * 2 + kXPad); }
 
+// v << S (S > 0) or v >> -S as one full-rate 64-bit VALU shift (the compiler otherwise splits a
+// 64-bit shift by a constant into two 32-bit operations).
+template <int S>
+__device__ __forceinline__ uint64_t shift64(uint64_t v) {
+    uint64_t r;
+    if constexpr (S == 0) {
+        r = v;
+    } else if constexpr (S > 0) {
+        asm("v_lshlrev_b64 %0, %1, %2" : "=v"(r) : "i"(S), "v"(v));
+    } else {
+        asm("v_lshrrev_b64 %0, %1, %2" : "=v"(r) : "i"(-S), "v"(v));
+    }
+    return r;
+}
+
 // 16 codes (elements 16b .. 16b + 15 of a group) -> two MFMA A operands of 8 FP16 codes each, in
 // the order (e0, e4, e1, e5, e2, e6, e3, e7) of each 8-code half.
-__device__ __forceinline__ void decode16(uint64_t nib, uint32_t hi, h8& a0, h8& a1) {
-    hi ^= 0xaaaaaaaau; // flips bit 5 of every code: (code & 63) ^ 32 = code + 32
+//
+// Word p of a half holds elements p and p + 4: the nibble plane gives them at bits 4p and 4p + 16
+// and the high pairs (spread to bytes 0 and 2 by one permute) at bits 2p and 2p + 16. Both halves
+// shift together as one 64-bit value (bits that cross the 32-bit boundary land outside the fields
+// kept). Per word, two 3-input bit operations: t = M1 ? nibbles : high bits, then
+// w = A ? (t ^ B) : B with A = the 6 code bits of each FP16 and B = 0x6400 | bit 5, which keeps the
+// code bits, flips bit 5 ((code & 63) ^ 32 = code + 32) and sets the exponent of 1024.
+template <int P>
+__device__ __forceinline__ void decode_words(uint64_t nib, uint64_t hs, uint32_t kMaskA, uint32_t kConstB, h2 (&c0)[4],
+                                             h2 (&c1)[4]) {
+    constexpr uint32_t kNibMask = 0x000f000fu;
+    const h2 bias = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+    const uint64_t ns = shift64<-4 * P>(nib);
+    const uint64_t hsh = shift64<4 - 2 * P>(hs);
+    const uint32_t t0 = __builtin_amdgcn_bitop3_b32(kNibMask, static_cast<uint32_t>(ns), static_cast<uint32_t>(hsh), 0xCA);
+    const uint32_t t1 = __builtin_amdgcn_bitop3_b32(kNibMask, static_cast<uint32_t>(ns >> 32), static_cast<uint32_t>(hsh >> 32), 0xCA);
+    const uint32_t w0 = __builtin_amdgcn_bitop3_b32(t0, kMaskA, kConstB, 0x6A);
+    const uint32_t w1 = __builtin_amdgcn_bitop3_b32(t1, kMaskA, kConstB, 0x6A);
+    c0[P] = __builtin_bit_cast(h2, w0) - bias; // 1056 + code - 1056: exact
+    c1[P] = __builtin_bit_cast(h2, w1) - bias;
+}
+
+__device__ __forceinline__ void decode16(uint64_t nib, uint32_t hi, uint32_t kMaskA, uint32_t kConstB, h8& a0, h8& a1) {
     const uint32_t hs0 = __builtin_amdgcn_perm(0u, hi, 0x0c010c00u); // high bytes 0, 1 -> bytes 0, 2
     const uint32_t hs1 = __builtin_amdgcn_perm(0u, hi, 0x0c030c02u);
-    const uint32_t n0 = static_cast<uint32_t>(nib);
-    const uint32_t n1 = static_cast<uint32_t>(nib >> 32);
-    const h2 bias = {static_cast<_Float16>(1056.0f), static_cast<_Float16>(1056.0f)};
+    const uint64_t hs = (static_cast<uint64_t>(hs1) << 32) | hs0;
     h2 c0[4], c1[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const uint32_t h0 = p < 2 ? (hs0 << (4 - 2 * p)) : (hs0 >> (2 * p - 4));
-        const uint32_t h1 = p < 2 ? (hs1 << (4 - 2 * p)) : (hs1 >> (2 * p - 4));
-        const uint32_t w0 = ((n0 >> (4 * p)) & 0x000f000fu) | (h0 & 0x00300030u) | 0x64006400u;
-        const uint32_t w1 = ((n1 >> (4 * p)) & 0x000f000fu) | (h1 & 0x00300030u) | 0x64006400u;
-        c0[p] = __builtin_bit_cast(h2, w0) - bias; // 1056 + code - 1056: exact
-        c1[p] = __builtin_bit_cast(h2, w1) - bias;
-    }
+    decode_words<0>(nib, hs, kMaskA, kConstB, c0, c1);
+    decode_words<1>(nib, hs, kMaskA, kConstB, c0, c1);
+    decode_words<2>(nib, hs, kMaskA, kConstB, c0, c1);
+    decode_words<3>(nib, hs, kMaskA, kConstB, c0, c1);
     a0 = __builtin_bit_cast(h8, c0);
     a1 = __builtin_bit_cast(h8, c1);
 }
@@ -93,10 +123,35 @@ __device__ __forceinline__ uint64_t logit_key(uint16_t b, int row) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), m, 64);
-    const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), m, 64);
+__device__ __forceinline__ uint64_t shfl_u64(uint64_t v, int src) {
+    const uint32_t lo = __shfl(static_cast<uint32_t>(v), src, 64);
+    const uint32_t hi = __shfl(static_cast<uint32_t>(v >> 32), src, 64);
     return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// ---- top-cap form: every lane keeps the kCandidateCap largest keys it has seen, descending ----------
+
+// x enters the descending list if it beats the last entry (a uniform skip when no lane's does).
+__device__ __forceinline__ void list_insert(uint64_t (&l)[kCandidateCap], uint64_t x) {
+    if (!__any(x > l[kCandidateCap - 1])) { return; }
+#pragma unroll
+    for (int i = 0; i < kCandidateCap; ++i) {
+        const bool up = x > l[i];
+        const uint64_t keep = up ? x : l[i];
+        x = up ? l[i] : x;
+        l[i] = keep;
+    }
+}
+
+// Lists per column per wave: with TP < 16 the keys of a finished tile are first spread so that each
+// lane owns one column (64 / TP lanes per column, TP / 4 rows each); with TP = 16 a lane keeps the
+// 4 rows of its own MFMA column.
+template <int TP>
+constexpr int lists_per_column() { return TP == 16 ? 4 : 64 / TP; }
+
+template <int W>
+constexpr size_t topcap_lds_bytes() {
+    return static_cast<size_t>(W) * 64 * kCandidateCap * 8 + static_cast<size_t>(W) * (64 + kCandidateCap) * 8;
 }
 
 // Per-lane DMA source offsets within a tile (fixed for the kernel). Nibble DMA d covers rows
@@ -154,7 +209,7 @@ __device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, c
     dma4s(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
 }
 
-template <int TP, int W, int CG>
+template <int TP, int W, int CG, bool HEAD>
 __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     using CH = Chunk<CG>;
     extern __shared__ __attribute__((aligned(16))) char dsmem[];
@@ -169,6 +224,29 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     const size_t ring0 = (x_lds_bytes(TP, a.Kp) + static_cast<size_t>(TP) * 8 + 15) & ~static_cast<size_t>(15);
     NMI_AS3 char* ring = smem + ring0 + static_cast<size_t>(wave) * 2 * CH::kStage;
 
+    const int gw = blockIdx.x * W + wave; // wave index of the launch
+    const int nch = (G + CG - 1) / CG;
+    const int ntw = gw < a.ntiles ? (a.ntiles - gw + a.waves - 1) / a.waves : 0;
+    const int items = ntw * nch;
+    const Planes pl{raw_buffer(a.qdata, a.nib_bytes), raw_buffer(a.qhigh, a.high_bytes), raw_buffer(a.scales, a.scale_bytes)};
+    const LinDma<CG> dl = make_lin_dma<CG>(lane, G);
+    const int c = lane & 15;  // MFMA column (x column) of this lane
+    const int b = lane >> 4;  // 16-code block of a group / accumulator row block
+
+    // (tile, chunk) of item j and of item j + 2 (the next DMA), advanced by one item per iteration
+    int tile = gw, chunk = 0;
+    int tile2 = gw, chunk2 = 0;
+    auto advance = [&](int& t, int& ch) {
+        if (++ch == nch) {
+            ch = 0;
+            t += a.waves;
+        }
+    };
+    // the first two chunks stream in while x is staged (the ring and x do not overlap)
+    if (items > 0) { issue_item<CG>(ring, pl, dl, tile2, chunk2, G); }
+    advance(tile2, chunk2);
+    if (items > 1) { issue_item<CG>(ring + CH::kStage, pl, dl, tile2, chunk2, G); }
+    advance(tile2, chunk2);
     // ---- x of this pass -> LDS as FP16, each 8-element block stored as (e0, e4, e1, e5, e2, e6, e3,
     // e7); columns past the pass and elements past K are zero. Two passes over x (it is small):
     // the column maxima, then the scaled values.
@@ -222,24 +300,34 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     }
     __syncthreads();
 
-    const int gw = blockIdx.x * W + wave; // wave index of the launch
-    const int nch = (G + CG - 1) / CG;
-    const int ntw = gw < a.ntiles ? (a.ntiles - gw + a.waves - 1) / a.waves : 0;
-    const int items = ntw * nch;
-    const Planes pl{raw_buffer(a.qdata, a.nib_bytes), raw_buffer(a.qhigh, a.high_bytes), raw_buffer(a.scales, a.scale_bytes)};
-    const LinDma<CG> dl = make_lin_dma<CG>(lane, G);
-    const int c = lane & 15;  // MFMA column (x column) of this lane
-    const int b = lane >> 4;  // 16-code block of a group / accumulator row block
-
-    if (items > 0) { issue_item<CG>(ring, pl, dl, gw, 0, G); }
-    if (items > 1) { issue_item<CG>(ring + CH::kStage, pl, dl, gw + (1 / nch) * a.waves, 1 % nch, G); }
+    // x column of this lane's MFMA column: lanes past the pass's columns alias a real one (their
+    // results are never stored), so every lane reads LDS unconditionally
+    const NMI_AS3 char* xcol = xl + (c & (TP - 1)) * xstride + 2 * b * 16;
+    const float cinv = 1.0f / cfac[c & (TP - 1)]; // a power of two: exact
+    const uint32_t kMaskA = 0x003f003fu;  // the 6 code bits of each FP16 half
+    const uint32_t kConstB = 0x64206420u; // exponent of 1024 and bit 5 (the flip) of each half
 
     float tot[4] = {0.f, 0.f, 0.f, 0.f};
     uint64_t best = 0;
+    // top-cap form: the sequence and in-sequence column of this lane's MFMA column, and whether its
+    // keys carry penalties (stochastic sequences with a nonzero presence or frequency penalty; the
+    // keys of a greedy sequence are the raw logits, so its list head is the argmax)
+    uint64_t lst[kCandidateCap];
+    int hseq = 0, hcol = 0;
+    bool hpen = false;
+    if constexpr (HEAD) {
+#pragma unroll
+        for (int q = 0; q < kCandidateCap; ++q) { lst[q] = 0; }
+        if (c < a.tp) {
+            const int t = a.t0 + c;
+            hseq = t / a.cols_per_seq;
+            hcol = t - hseq * a.cols_per_seq;
+            const nmi_sampling_config& cf = a.config[hseq];
+            hpen = cf.temperature > 0.0f && (cf.presence_penalty != 0.0f || cf.frequency_penalty != 0.0f);
+        }
+    }
 #pragma unroll 1
     for (int j = 0; j < items; ++j) {
-        const int tile = gw + (j / nch) * a.waves;
-        const int chunk = j % nch;
         NMI_AS3 char* st = ring + (j & 1) * CH::kStage;
         if (j + 1 < items) {
             __builtin_amdgcn_s_waitcnt((CH::kDma & 0xf) | ((CH::kDma >> 4) << 14) | (0x7 << 4) | (0xf << 8));
@@ -266,52 +354,127 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
         }
         if (j + 2 < items) {
             __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
-            issue_item<CG>(st, pl, dl, gw + ((j + 2) / nch) * a.waves, (j + 2) % nch, G);
+            issue_item<CG>(st, pl, dl, tile2, chunk2, G);
         }
-        const int ng = min(CG, G - chunk * CG);
+        advance(tile2, chunk2);
+        auto group = [&](int gl) {
+            const NMI_AS3 char* xp = xcol + (chunk * CG + gl) * 128;
+            const i4 x0 = *(const NMI_AS3 i4*)xp;
+            const i4 x1 = *(const NMI_AS3 i4*)(xp + 16);
+            h8 a0, a1;
+            decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
+            f4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
 #pragma unroll
-        for (int gl = 0; gl < CG; ++gl) {
-            if (gl < ng) {
-                const int ga = chunk * CG + gl;
-                h8 a0, a1;
-                decode16(nib[gl], hig[gl], a0, a1);
-                i4 x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0};
-                if (c < TP) {
-                    const NMI_AS3 char* xp = xl + c * xstride + (8 * ga + 2 * b) * 16;
-                    x0 = *(const NMI_AS3 i4*)xp;
-                    x1 = *(const NMI_AS3 i4*)(xp + 16);
-                }
-                f4 acc = {0.f, 0.f, 0.f, 0.f};
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t w = sc[i][gl >> 1];
+                const float s = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
+                tot[i] = fmaf(s, acc[i], tot[i]);
+            }
+        };
+        if (chunk * CG + CG <= G) {
+            // a full chunk: straight-line code the scheduler can interleave across groups
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t w = sc[i][gl >> 1];
-                    const float s = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
-                    tot[i] = fmaf(s, acc[i], tot[i]);
-                }
+            for (int gl = 0; gl < CG; ++gl) { group(gl); }
+        } else {
+            const int ng = G - chunk * CG;
+#pragma unroll
+            for (int gl = 0; gl < CG; ++gl) {
+                if (gl < ng) { group(gl); }
             }
         }
         if (chunk == nch - 1) {
             // tile done: lane holds rows 4b + i, column c
             const int r0 = tile * kTileRows;
-            const float inv = c < TP ? 1.0f / cfac[c] : 0.0f; // a power of two: exact
+            uint64_t kk[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = r0 + 4 * b + i;
-                const uint16_t bfv = f32_to_bf16_bits(tot[i] * inv);
+                const uint16_t bfv = f32_to_bf16_bits(tot[i] * cinv);
                 if (a.out != nullptr && c < a.tp && row < a.N) {
                     a.out[row + static_cast<int64_t>(a.N) * (a.t0 + c)] = bfv;
                 }
                 if (row < a.valid_rows) { best = max_u64(best, logit_key(bfv, row)); }
+                if constexpr (HEAD) {
+                    float v = bf16_to_f32(bfv);
+                    if (hpen) {
+                        v = adjusted_logit(v, row, a.config[hseq], a.drafts + static_cast<int64_t>(hseq) * (a.cols_per_seq - 1),
+                                           hcol);
+                    }
+                    kk[i] = (c < a.tp && row < a.valid_rows) ? sort_key(v, row) : 0ull;
+                }
                 tot[i] = 0.0f;
             }
+            if constexpr (HEAD) {
+                if constexpr (TP == 16) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) { list_insert(lst, kk[i]); }
+                } else {
+                    // lane -> (column lane / (64 / TP), rows s, s + 64 / TP, ... of the tile), s = lane % (64 / TP);
+                    // row r of column col sits in lane col + 16 * (r / 4), register r % 4
+                    constexpr int LPC = 64 / TP;
+                    constexpr int RPL = TP / 4;
+                    const int col = lane / LPC;
+                    const int s0 = lane % LPC;
+#pragma unroll
+                    for (int e = 0; e < RPL; ++e) {
+                        const int r = s0 + LPC * e;
+                        const int src = col + 16 * (r >> 2);
+                        uint64_t v = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const uint64_t g = shfl_u64(kk[q], src);
+                            v = q == (r & 3) ? g : v;
+                        }
+                        list_insert(lst, v);
+                    }
+                }
+            }
         }
+        advance(tile, chunk);
     }
     if (a.keys != nullptr) {
         best = max_u64(best, shfl_xor_u64(best, 16));
         best = max_u64(best, shfl_xor_u64(best, 32));
         if (lane < a.tp) { a.keys[static_cast<int64_t>(a.t0 + lane) * a.waves + gw] = best; }
+    }
+    if constexpr (HEAD) {
+        // Workgroup top-cap per column: every lane's list goes to LDS (x and the ring are done with),
+        // then wave w merges the W * lists_per_column lists of columns w, w + W, ...
+        constexpr int LPC = lists_per_column<TP>();
+        constexpr int NL = W * LPC;
+        constexpr int LPL = (NL + 63) / 64;
+        static_assert(LPL <= 2, "top-cap merge holds at most two lists per lane");
+        __syncthreads();
+        NMI_AS3 uint64_t* lists = (NMI_AS3 uint64_t*)smem;
+#pragma unroll
+        for (int q = 0; q < kCandidateCap; ++q) { lists[(wave * 64 + lane) * kCandidateCap + q] = lst[q]; }
+        uint64_t* wcand = (uint64_t*)(lists + W * 64 * kCandidateCap + wave * 64);
+        uint64_t* wout = (uint64_t*)(lists + W * 64 * kCandidateCap + W * 64 + wave * kCandidateCap);
+        __syncthreads();
+        for (int lc = wave; lc < a.tp; lc += W) {
+            uint64_t k[LPL * kCandidateCap];
+            uint64_t heads[LPL];
+#pragma unroll
+            for (int h = 0; h < LPL; ++h) {
+                const int q = lane + 64 * h;
+                const int w = q / LPC;
+                const int sl = q % LPC;
+                const int src = TP == 16 ? lc + 16 * sl : lc * LPC + sl;
+                const bool ok = q < NL;
+#pragma unroll
+                for (int e = 0; e < kCandidateCap; ++e) {
+                    k[h * kCandidateCap + e] = ok ? lists[(w * 64 + src) * kCandidateCap + e] : 0ull;
+                }
+                heads[h] = k[h * kCandidateCap];
+            }
+            wave_top_cap(k, heads, kCandidateCap, wcand, wout);
+            if (lane < kCandidateCap) {
+                a.cand[(static_cast<int64_t>(a.t0 + lc) * gridDim.x + blockIdx.x) * kCandidateCap + lane] = wout[lane];
+            }
+            wave_lds_sync();
+        }
     }
 }
 
@@ -353,12 +516,13 @@ constexpr LinearInstance kInstances[] = {
 };
 constexpr int kInstanceCount = sizeof(kInstances) / sizeof(kInstances[0]);
 
-LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T) {
+LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap) {
     const int32_t ntiles = (N + kTileRows - 1) / kTileRows;
     constexpr size_t kLds = 160 * 1024;
     const int first = T <= 4 ? 6 : (T <= 8 ? 2 : 0);
     LinearPlan p{};
     for (int i = first; i < kInstanceCount; ++i) {
+        if (top_cap && kInstances[i].waves > 8) { continue; } // the top-cap merge holds <= 2 lists per lane
         p.tp = kInstances[i].tp;
         p.waves = kInstances[i].waves;
         p.cg = kInstances[i].cg;
@@ -366,7 +530,11 @@ LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T) {
         if (p.lds <= kLds) { break; }
     }
     p.passes = (T + p.tp - 1) / p.tp;
-    p.grid = std::max<int32_t>(1, std::min<int32_t>(kLinearGrid, (ntiles + p.waves - 1) / p.waves));
+    // Waves get equal tile counts: the fewest workgroups (at most one per CU) for which every wave
+    // holds ceil(ntiles / (256 * waves)) tiles, instead of all 256 with a partial last round.
+    const int32_t per_wave = (ntiles + kLinearGrid * p.waves - 1) / (kLinearGrid * p.waves);
+    const int32_t waves_needed = (ntiles + per_wave - 1) / per_wave;
+    p.grid = std::max<int32_t>(1, std::min<int32_t>(kLinearGrid, (waves_needed + p.waves - 1) / p.waves));
     return p;
 }
 
@@ -374,15 +542,34 @@ size_t linear_argmax_workspace_bytes(int32_t T) {
     return static_cast<size_t>(T) * kLinearGrid * kLinearMaxWaves * sizeof(uint64_t);
 }
 
-template <int TP, int W, int CG>
-void launch_instance(const LinearArgs& a, const LinearPlan& p, hipStream_t stream) {
+size_t linear_topcap_workspace_bytes(int32_t T) {
+    return static_cast<size_t>(T) * kLinearGrid * kCandidateCap * sizeof(uint64_t);
+}
+
+template <int TP, int W, int CG, bool HEAD>
+void launch_kernel(const LinearArgs& a, const LinearPlan& p, hipStream_t stream) {
     static const bool lds_raised = [] {
-        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_kernel<TP, W, CG>),
+        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_kernel<TP, W, CG, HEAD>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
         return true;
     }();
     (void)lds_raised;
-    hipLaunchKernelGGL((linear_q6_kernel<TP, W, CG>), dim3(p.grid), dim3(64 * W), p.lds, stream, a);
+    size_t lds = p.lds;
+    if constexpr (HEAD) { lds = std::max(lds, topcap_lds_bytes<W>()); }
+    hipLaunchKernelGGL((linear_q6_kernel<TP, W, CG, HEAD>), dim3(p.grid), dim3(64 * W), lds, stream, a);
+}
+
+template <int TP, int W, int CG>
+void launch_instance(const LinearArgs& a, const LinearPlan& p, hipStream_t stream) {
+    if constexpr (W <= 8) {
+        if (a.cand != nullptr) {
+            launch_kernel<TP, W, CG, true>(a, p, stream);
+            return;
+        }
+    } else {
+        if (a.cand != nullptr) { throw Unsupported("linear: no top-cap instance with more than 8 waves"); }
+    }
+    launch_kernel<TP, W, CG, false>(a, p, stream);
 }
 
 void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream) {

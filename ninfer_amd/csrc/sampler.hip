@@ -11,6 +11,7 @@
 #include "device_utils.h"
 #include "sampler_internal.h"
 #include "sampler_common.h"
+#include "topcap.h"
 
 #pragma clang fp contract(off)
 
@@ -65,27 +66,6 @@ __device__ __forceinline__ void wave_topk(uint64_t (&k)[N], int cap, uint64_t* o
             k[N - 1] = 0;
         }
     }
-}
-
-__device__ __forceinline__ int candidate_cap(const nmi_sampling_config& cfg, int32_t vocab) {
-    int cap = kCandidateCap; // src/ops/kernel/sampling_device.cuh:110-118
-    if (cfg.top_k > 0 && cfg.top_k < cap) { cap = cfg.top_k; }
-    if (vocab < cap) { cap = vocab; }
-    return cap;
-}
-
-// src/ops/kernel/sampling_device.cuh:137-149; overlay = drafts[0..col-1].
-__device__ __forceinline__ float adjusted_logit(float raw, int v, const nmi_sampling_config& c,
-                                                const int32_t* overlay, int overlay_len) {
-    float x = raw;
-    if (c.presence_penalty == 0.0f && c.frequency_penalty == 0.0f) { return x; }
-    int cnt = c.token_counts != nullptr ? c.token_counts[v] : 0;
-    for (int j = 0; j < overlay_len; ++j) {
-        if (overlay[j] == v) { ++cnt; }
-    }
-    if (cnt > 0) { x = x - c.presence_penalty; }
-    if (c.frequency_penalty != 0.0f) { x = x - c.frequency_penalty * static_cast<float>(cnt); }
-    return x;
 }
 
 // ---- argmax ---------------------------------------------------------------------------------------
@@ -291,104 +271,6 @@ __device__ int pick_from_support(const int32_t* cand_idx, const float* prob, int
     return picked;
 }
 
-// ---- exact top-cap selection over unique 64-bit keys (0 = empty slot) -----------------------------
-//
-// A wave never extracts its keys one by one. A threshold T with at least cap keys >= T is found
-// first, with ballots only: MSB-first bit selection over the high words (ordered values) of a few
-// representative keys, the lane maxima or list heads. The keys >= T (a few dozen for real logits)
-// are compacted into LDS, and each one's rank is the number of candidates above it, so rank r goes
-// to out[r]. When more than 64 keys reach T (heavy ties), the exact cap-th largest key is found by a
-// 64-bit bit selection over every key and the ranking repeats with exactly cap candidates.
-
-__device__ __forceinline__ uint32_t key_high(uint64_t k) { return static_cast<uint32_t>(k >> 32); }
-
-// Lanes below this one that are set in `mask`.
-__device__ __forceinline__ int lanes_below(uint64_t mask) {
-    return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
-}
-
-// Orders one wave's LDS writes before its later reads of the same slots by other lanes.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// The cap-th largest high word among the wave's M values per lane (0 = no value): the largest t
-// with at least cap values whose high word is >= t. 0 when fewer than cap values exist.
-template <int M>
-__device__ __forceinline__ uint32_t wave_cap_high(const uint32_t (&hi)[M], int cap) {
-    uint32_t t = 0;
-#pragma unroll 1
-    for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t c = t | (1u << bit);
-        int n = 0;
-#pragma unroll
-        for (int m = 0; m < M; ++m) { n += __popcll(__ballot(hi[m] >= c)); }
-        if (n >= cap) { t = c; }
-    }
-    return t;
-}
-
-// The exact cap-th largest key among the wave's N keys per lane (0 when fewer than cap exist).
-template <int N>
-__device__ __forceinline__ uint64_t wave_cap_key(const uint64_t (&k)[N], int cap) {
-    uint64_t t = 0;
-#pragma unroll 1
-    for (int bit = 63; bit >= 0; --bit) {
-        const uint64_t c = t | (1ull << bit);
-        int n = 0;
-#pragma unroll
-        for (int e = 0; e < N; ++e) { n += __popcll(__ballot(k[e] >= c)); }
-        if (n >= cap) { t = c; }
-    }
-    return t;
-}
-
-// Ranks the candidates {k[e] != 0, k[e] >= T} if there are at most 64 of them: the cap largest
-// go to out[0..cap) in descending order, 0-padded. cand: 64 slots of wave-private LDS.
-template <int N>
-__device__ __forceinline__ bool wave_rank_top(const uint64_t (&k)[N], uint64_t T, int cap, uint64_t* cand,
-                                              uint64_t* out) {
-    const int lane = threadIdx.x & 63;
-    int total = 0;
-#pragma unroll
-    for (int e = 0; e < N; ++e) { total += __popcll(__ballot(k[e] != 0 && k[e] >= T)); }
-    if (total > 64) { return false; }
-    int base = 0;
-#pragma unroll
-    for (int e = 0; e < N; ++e) {
-        const bool sel = k[e] != 0 && k[e] >= T;
-        const uint64_t mask = __ballot(sel);
-        if (sel) { cand[base + lanes_below(mask)] = k[e]; }
-        base += __popcll(mask);
-    }
-    wave_lds_sync();
-    if (lane < total) {
-        const uint64_t key = cand[lane];
-        int r = 0;
-        for (int j = 0; j < total; ++j) { r += cand[j] > key ? 1 : 0; }
-        if (r < cap) { out[r] = key; }
-    } else if (lane < cap) {
-        out[lane] = 0;
-    }
-    wave_lds_sync();
-    return true;
-}
-
-// Top cap of the wave's N keys per lane; `heads` are one or more keys per lane that include every
-// lane's (or list's) largest key, so at least cap keys reach the threshold derived from them.
-template <int N, int M>
-__device__ __forceinline__ void wave_top_cap(const uint64_t (&k)[N], const uint64_t (&heads)[M], int cap,
-                                             uint64_t* cand, uint64_t* out) {
-    uint32_t hi[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) { hi[m] = key_high(heads[m]); }
-    const uint64_t T = static_cast<uint64_t>(wave_cap_high(hi, cap)) << 32;
-    if (!wave_rank_top(k, T, cap, cand, out)) { wave_rank_top(k, wave_cap_key(k, cap), cap, cand, out); }
-}
-
 // ---- Mode R launch 1: per-tile top-cap candidates ------------------------------------------------
 
 __global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
@@ -453,8 +335,86 @@ __global__ __launch_bounds__(256) void spec_tile_topk_kernel(SpecArgs a) {
 
 // ---- Mode R launch 2: per-sequence merge, distributions and the sequential accept -----------------
 
-// One workgroup per sequence; wave w merges columns w, w + 4, ... (lane j holds tile lists j and
-// j + 64), builds each column's truncated distribution in LDS, then thread 0 runs the accept.
+// Key j of a candidate list (descending, 0-padded; slots past cap are never read).
+__device__ __forceinline__ uint64_t list_key(const i4& v, int half) {
+    return (static_cast<uint64_t>(static_cast<uint32_t>(v[2 * half + 1])) << 32) | static_cast<uint32_t>(v[2 * half]);
+}
+
+// The cap largest keys of up to 64 * LISTS descending lists (lane j holds lists j, j + 64, ...) into
+// out[0..cap), descending and 0-padded. The threshold T from the list heads bounds the answer from
+// below (cap heads reach it), so only keys >= T matter; a list's keys >= T form a prefix, and the
+// first kPrefix of every list are read first. When no list has more than kPrefix keys >= T (the
+// usual case: the top candidates spread over many lists), the prefixes are ranked directly;
+// otherwise every key of every list is loaded and ranked.
+template <int LISTS>
+__device__ __forceinline__ void merge_sorted_lists(const uint64_t* part, int nlists, int cap, uint64_t* cand,
+                                                   uint64_t* out) {
+    constexpr int kPrefix = 4;
+    const int lane = threadIdx.x & 63;
+    uint64_t k[LISTS * kPrefix];
+    uint64_t heads[LISTS];
+    uint32_t hi[LISTS];
+#pragma unroll
+    for (int h = 0; h < LISTS; ++h) {
+        const int j = lane + 64 * h;
+        if (j < nlists) {
+            const i4* src = reinterpret_cast<const i4*>(part + static_cast<int64_t>(j) * kCandidateCap);
+            const i4 v0 = src[0];
+            const i4 v1 = src[1];
+            k[h * kPrefix + 0] = list_key(v0, 0);
+            k[h * kPrefix + 1] = list_key(v0, 1);
+            k[h * kPrefix + 2] = list_key(v1, 0);
+            k[h * kPrefix + 3] = list_key(v1, 1);
+        } else {
+#pragma unroll
+            for (int e = 0; e < kPrefix; ++e) { k[h * kPrefix + e] = 0; }
+        }
+#pragma unroll
+        for (int e = 0; e < kPrefix; ++e) {
+            if (e >= cap) { k[h * kPrefix + e] = 0; } // slots past cap were never written
+        }
+        heads[h] = k[h * kPrefix];
+        hi[h] = key_high(heads[h]);
+    }
+    const uint64_t T = static_cast<uint64_t>(wave_cap_high(hi, cap)) << 32;
+    bool deep = false;
+#pragma unroll
+    for (int h = 0; h < LISTS; ++h) {
+        const uint64_t last = k[h * kPrefix + kPrefix - 1];
+        deep = deep || (kPrefix < cap && last != 0 && last >= T);
+    }
+    if (!__any(deep) && wave_rank_top(k, T, cap, cand, out)) { return; }
+    uint64_t lk[LISTS * kCandidateCap];
+#pragma unroll
+    for (int h = 0; h < LISTS; ++h) {
+        const int j = lane + 64 * h;
+        if (j < nlists) {
+            const i4* src = reinterpret_cast<const i4*>(part + static_cast<int64_t>(j) * kCandidateCap);
+#pragma unroll
+            for (int q = 0; q < kCandidateCap / 2; ++q) {
+                const i4 v = src[q];
+                lk[h * kCandidateCap + 2 * q] = list_key(v, 0);
+                lk[h * kCandidateCap + 2 * q + 1] = list_key(v, 1);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < kCandidateCap; ++q) { lk[h * kCandidateCap + q] = 0; }
+        }
+#pragma unroll
+        for (int q = 0; q < kCandidateCap; ++q) {
+            if (q >= cap) { lk[h * kCandidateCap + q] = 0; }
+        }
+    }
+    wave_top_cap(lk, heads, cap, cand, out);
+}
+
+
+// One workgroup per sequence; wave w merges columns w, w + 4, ... (lane j holds lists j, j + 64, ...,
+// LISTS per lane), builds each column's truncated distribution in LDS, then thread 0 runs the accept.
+// The lists are the per-tile candidates of spec_tile_topk_kernel, or (target_tokens null) the
+// per-workgroup candidates of the fused lm_head, whose keys of a greedy sequence are the raw logits:
+// the greedy target of a column is then the largest list head.
+template <int LISTS>
 __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     const int b = blockIdx.x;
     const nmi_sampling_config cfg = a.config[b];
@@ -467,10 +427,29 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     int32_t* accepted = a.accepted + b;
     int64_t* stats = a.stats + static_cast<int64_t>(b) * a.stats_stride;
 
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     if (!(cfg.temperature > 0.0f)) {
         // Greedy: src/ops/kernel/speculative_round.cuh:51-72.
+        __shared__ int32_t g_target[kMaxColumns];
+        const int32_t* target = a.target_tokens + static_cast<int64_t>(b) * (K + 1);
+        if (a.target_tokens == nullptr) {
+            for (int col = wave; col <= K; col += 4) {
+                const uint64_t* part = a.partial + (static_cast<int64_t>(b) * a.columns + col) * a.ntiles * kCandidateCap;
+                uint64_t h = 0;
+#pragma unroll
+                for (int q = 0; q < LISTS; ++q) {
+                    const int j = lane + 64 * q;
+                    const uint64_t v = j < a.ntiles ? part[static_cast<int64_t>(j) * kCandidateCap] : 0ull;
+                    h = v > h ? v : h;
+                }
+                h = wave_max_u64(h);
+                if (lane == 0) { g_target[col] = key_index(h); }
+            }
+            __syncthreads();
+            target = g_target;
+        }
         if (threadIdx.x == 0) {
-            const int32_t* target = a.target_tokens + static_cast<int64_t>(b) * (K + 1);
             int acc = 0;
             while (acc < K && target[acc] == drafts[acc]) { ++acc; }
             commit_round(drafts, K, acc, target[acc], *length, length, token, sampled_out,
@@ -479,8 +458,6 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
         return;
     }
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     const int cap = candidate_cap(cfg, a.token_domain);
     __shared__ uint64_t cand[4][64];
     __shared__ uint64_t top[4][kCandidateCap];
@@ -491,30 +468,7 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     const float inv_temp = 1.0f / cfg.temperature;
     for (int col = wave; col <= K; col += 4) {
         const uint64_t* part = a.partial + (static_cast<int64_t>(b) * a.columns + col) * a.ntiles * kCandidateCap;
-        uint64_t lk[2 * kCandidateCap];
-        uint64_t heads[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = lane + 64 * h;
-            if (j < a.ntiles) {
-                const i4* src = reinterpret_cast<const i4*>(part + static_cast<int64_t>(j) * kCandidateCap);
-#pragma unroll
-                for (int q = 0; q < kCandidateCap / 2; ++q) {
-                    const i4 v = src[q];
-                    lk[h * kCandidateCap + 2 * q] = (static_cast<uint64_t>(static_cast<uint32_t>(v[1])) << 32) | static_cast<uint32_t>(v[0]);
-                    lk[h * kCandidateCap + 2 * q + 1] = (static_cast<uint64_t>(static_cast<uint32_t>(v[3])) << 32) | static_cast<uint32_t>(v[2]);
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < kCandidateCap; ++q) { lk[h * kCandidateCap + q] = 0; }
-            }
-#pragma unroll
-            for (int q = 0; q < kCandidateCap; ++q) {
-                if (q >= cap) { lk[h * kCandidateCap + q] = 0; } // slots past cap were never written
-            }
-            heads[h] = lk[h * kCandidateCap];
-        }
-        wave_top_cap(lk, heads, cap, cand[wave], top[wave]);
+        merge_sorted_lists<LISTS>(part, a.ntiles, cap, cand[wave], top[wave]);
         // src/ops/kernel/sampling_device.cuh:190-223 with det_expf(fma(x, inv_temp, -m)).
         const float m = key_float(top[wave][0]) * inv_temp;
         if (lane < cap) {
@@ -698,7 +652,12 @@ void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream)
     hipLaunchKernelGGL(spec_tile_topk_kernel, dim3(args.ntiles, args.K + 1, batch), dim3(256), 0,
                        stream, args);
     check_launch("spec_tile_topk_kernel");
-    hipLaunchKernelGGL(spec_merge_accept_kernel, dim3(batch), dim3(256), 0, stream, args);
+    hipLaunchKernelGGL(spec_merge_accept_kernel<2>, dim3(batch), dim3(256), 0, stream, args);
+    check_launch("spec_merge_accept_kernel");
+}
+
+void launch_spec_merge_accept_wide(const SpecArgs& args, int32_t batch, hipStream_t stream) {
+    hipLaunchKernelGGL(spec_merge_accept_kernel<4>, dim3(batch), dim3(256), 0, stream, args);
     check_launch("spec_merge_accept_kernel");
 }
 

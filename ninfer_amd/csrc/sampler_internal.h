@@ -14,6 +14,7 @@ inline constexpr int kMaxColumns = 16;            // K <= 15 (reference kSampler
 inline constexpr int kTileTokens = 4096;   // tokens per candidate tile (256 threads x 16)
 inline constexpr int kMaxTreeNodes = 32;
 inline constexpr int kMergeMaxTiles = 128;   // tile lists one merge wave holds (2 per lane)
+inline constexpr int kMergeWideLists = 256;  // lists of the wide merge (4 per lane)
 
 struct SpecPlan {
     int32_t ntiles = 0;
@@ -22,7 +23,7 @@ struct SpecPlan {
 };
 
 struct SpecArgs {
-    const int32_t* target_tokens; // [K+1, B]
+    const int32_t* target_tokens; // [K+1, B]; null: greedy targets are the list heads (fused lm_head)
     const uint16_t* logits;       // [physical_rows, columns_total, B]
     const int32_t* drafts;        // [K, B]
     int32_t* length;              // [B]
@@ -44,12 +45,22 @@ struct SpecArgs {
 
 SpecPlan plan_spec(int32_t token_domain, int32_t columns, int32_t batch);
 
+// Validates the acceptance state and outputs (drafts [K, B], scalars [B], sampled_out [K+1, B],
+// stats [>=4+K, B], config) and fills those fields of the kernel arguments; B out.
+SpecArgs check_accept_state(const nmi_tensor* drafts, nmi_tensor* length, nmi_tensor* token,
+                            nmi_tensor* sampled_out, nmi_tensor* num_sampled, nmi_tensor* accepted,
+                            nmi_tensor* stats, const nmi_sampling_config* config, const std::string& op,
+                            int32_t& B);
+
 void launch_argmax(const uint16_t* logits, int32_t* out, int32_t physical_rows, int32_t valid_rows,
                    int32_t columns, hipStream_t stream);
 void launch_prepare_verify_inputs(const int32_t* token, const int32_t* drafts, const int32_t* length,
                                   int32_t* verify_ids, int32_t* positions, int32_t K, int32_t B,
                                   hipStream_t stream);
 void launch_spec_accept(const SpecArgs& args, int32_t batch, hipStream_t stream);
+// Merge + accept alone over up to kMergeWideLists candidate lists per column (the fused lm_head's
+// per-workgroup lists in args.partial, ntiles = lists per column).
+void launch_spec_merge_accept_wide(const SpecArgs& args, int32_t batch, hipStream_t stream);
 void launch_mtp_alignment_ids(const int32_t* verify_ids, const int32_t* token, const int32_t* accepted,
                               int32_t* alignment_ids, int32_t T, hipStream_t stream);
 void launch_select_hidden(const uint16_t* hidden, const int32_t* accepted, uint16_t* out,

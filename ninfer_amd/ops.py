@@ -152,6 +152,20 @@ def linear_argmax(x, weight, valid_rows, ws, out, stream=None) -> None:
                                   _s(stream)))
 
 
+def speculative_accept_fused_head_workspace_bytes(K: int, batch: int = 1) -> int:
+    return int(lib().nmi_speculative_accept_fused_head_workspace_bytes(K, batch))
+
+
+def speculative_accept_fused_head(x, weight, drafts, length, token, sampled_out, num_sampled, accepted, stats,
+                                  token_domain: int, config_ptr: int, workspace, stream=None) -> None:
+    """lm_head (Q6G64 linear) + speculative_accept_greedy_drafts in one call, the logits never written:
+    x BF16 [hidden, K+1, B]; `config_ptr` addresses device SamplingConfig[B]."""
+    ws, nb = _ws(workspace)
+    check(lib().nmi_speculative_accept_fused_head(
+        _p(x), C.byref(weight), _p(drafts), _p(length), _p(token), _p(sampled_out), _p(num_sampled), _p(accepted),
+        _p(stats), int(token_domain), C.c_void_p(config_ptr), ws, nb, _s(stream)))
+
+
 # ---- recurrent state of the hybrid layers (gated_delta_rule.h, causal_conv1d_silu.h, scalar.h) --
 
 def gated_delta_rule_workspace_bytes(head_dim, qk_heads, value_heads, tokens, normalize_qk) -> int:
