@@ -168,15 +168,17 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const uint16_t* logits, in
     (void)physical_rows;
 }
 
-// Multi-workgroup argmax: one 256-thread workgroup per (tile of kArgmaxTile rows, column), eight
-// 16-byte loads in flight per thread. The tile's best key (value as an ordered float with -0 = +0,
+// Multi-workgroup argmax: one 256-thread workgroup per (tile of kArgmaxTile rows, column), one
+// 16-byte load per thread (measured on MI355X at [248320, 4]: 2,048-row tiles, 488 workgroups, take
+// the greedy acceptance from 8.4 to 6.5 us; 16,384-row tiles leave most CUs idle). The tile's best key (value as an ordered float with -0 = +0,
 // then the lowest row) is folded into out[col] by a compare-and-swap loop on the row index, which
 // compares against the key of the row out[col] holds at that moment (the reference's tiled atomic
 // route, src/ops/kernel/argmax.cuh:96-129). The reference zeroes out first with a memset
 // (src/ops/launcher/argmax.cu); here nothing needs initializing: a value outside [0, valid_rows)
 // counts as no candidate, and a row inside it is a real candidate whose key the argmax beats or
 // equals, so the loop ends at the argmax whatever out held before the call.
-constexpr int kArgmaxTile = 256 * 64;
+constexpr int kArgmaxLoads = 1;                  // 16-byte loads per thread
+constexpr int kArgmaxTile = 256 * 8 * kArgmaxLoads;
 
 __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits, int32_t* out,
                                                           int32_t valid_rows, int64_t column_stride) {
@@ -185,14 +187,14 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
     const int base = blockIdx.x * kArgmaxTile + threadIdx.x * 8;
     uint64_t best = 0;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
-        i4 raw[8];
+        i4 raw[kArgmaxLoads];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kArgmaxLoads; ++u) {
             const int r0 = base + u * 256 * 8;
             raw[u] = r0 + 8 <= valid_rows ? *reinterpret_cast<const i4*>(x + r0) : i4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kArgmaxLoads; ++u) {
             const int r0 = base + u * 256 * 8;
             if (r0 + 8 <= valid_rows) {
 #pragma unroll
@@ -208,7 +210,7 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
             }
         }
     } else {
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kArgmaxLoads; ++u) {
             for (int e = 0; e < 8; ++e) {
                 const int v = base + u * 256 * 8 + e;
                 if (v < valid_rows) {
