@@ -615,10 +615,11 @@ def round_bench(stream, args, layers, L2: int) -> dict:
     """One whole greedy verify round captured as one graph and replayed back to back, every replay
     continuing from the device state the previous one left (reference
     src/targets/qwen3_6/impl/runtime/speculative_impl.h:35-45): prepare ids/positions from the device length -> the 64 layers' A1
-    attention at those positions -> Q6 lm_head [248320, 5120] over the 4 verify columns (BF16
-    logits) -> argmax -> greedy accept (length += A + 1) -> accepted hidden row -> MTP alignment
-    ids -> recurrent-state slot = accepted. Drafts are planted from the round's own targets: each
-    of the 3 drafts agrees with probability 0.8 (seeded; the prefix stops at the first miss)."""
+    attention at those positions -> fused Q6 lm_head [248320, 5120] -> greedy accept over the 4
+    verify columns (speculative_accept_fused_head: per-workgroup top-20 keys, no logits written;
+    length += A + 1) -> accepted hidden row -> MTP alignment ids -> recurrent-state slot = accepted.
+    Drafts are planted from the round's own targets: each of the 3 drafts agrees with probability
+    0.8 (seeded; the prefix stops at the first miss)."""
     import ninfer_amd as na
     from ninfer_amd import ops, synthetic as syn
     from ninfer_amd.device import DeviceArray, DeviceBuffer
@@ -646,7 +647,8 @@ def round_bench(stream, args, layers, L2: int) -> dict:
               slot=DeviceArray.from_numpy(na.I32, np.zeros(1, np.int32), (1,)))
     cfg = DeviceBuffer(40)
     cfg.upload(np.frombuffer(bytes(memoryview(na.SamplingConfig())), dtype=np.uint8))
-    sws = DeviceBuffer(max(256, ops.sampling_workspace_bytes(VOCAB, T)))
+    x3 = DeviceArray(na.BF16, (HID, T, 1), buf=x.buf)  # the verify columns of the one sequence
+    hws = DeviceBuffer(ops.speculative_accept_fused_head_workspace_bytes(K, 1))
     env = (1, L2 + T + ROUND_SPARE)
     ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, env[1]))
     scale = float(np.float32(1.0 / np.sqrt(D)))
@@ -657,12 +659,9 @@ def round_bench(stream, args, layers, L2: int) -> dict:
         for ly in layers:
             ops.gqa_attention(ly.q.tensor(), ly.k.tensor(), ly.v.tensor(), st["pos"].tensor(), scale, ly.view, env,
                               ws, ly.out.tensor(), stream)
-        ops.linear(x.tensor(), w, logits.tensor(), stream)
-        ops.argmax(logits.tensor(), target.tensor(), VOCAB, stream)
-        ops.speculative_accept_greedy_drafts(target.tensor(), logits.tensor(), st["drafts"].tensor(),
-                                             st["length"].tensor(), st["token"].tensor(), st["so"].tensor(),
-                                             st["ns"].tensor(), st["acc"].tensor(), st["stats"].tensor(), VOCAB,
-                                             cfg.ptr, sws, stream)
+        ops.speculative_accept_fused_head(x3.tensor(), w, st["drafts"].tensor(), st["length"].tensor(),
+                                          st["token"].tensor(), st["so"].tensor(), st["ns"].tensor(),
+                                          st["acc"].tensor(), st["stats"].tensor(), VOCAB, cfg.ptr, hws, stream)
         ops.speculative_select_accepted_hidden(hidden.tensor(), st["acc"].tensor(), st["sel"].tensor(), stream)
         ops.mtp_prepare_alignment_ids(st["ids"].tensor(), st["token"].tensor(), st["acc"].tensor(),
                                       st["align"].tensor(), stream)
@@ -679,11 +678,12 @@ def round_bench(stream, args, layers, L2: int) -> dict:
     del g, wbuf
     return dict(round_ms=ms, round_p95_ms=p95, rounds=rounds, produced_per_round=produced,
                 tokens_per_s=produced / (ms * 1e-3), planted_accepted=int(agree.cumprod().sum()),
-                layers=len(layers), lm_head="Q6G64_F16S [248320, 5120] linear + argmax")
+                layers=len(layers), lm_head="Q6G64_F16S [248320, 5120] fused lm_head -> top-20 keys -> greedy accept")
 
 
-def cpu_baseline(sample_layers: int):
-    """Oracle attention on the host for `sample_layers` C2 layers (reported only)."""
+def cpu_baseline(min_seconds: float = 10.0):
+    """Oracle attention on the host over whole C2 steps (64 layers each), repeated until at least
+    `min_seconds` have passed (reported only): a bounded sample of the same workload."""
     from oracle import pyoracle
     from ninfer_amd import synthetic as syn
     from ninfer_amd.kv_cache import align_up
@@ -695,13 +695,18 @@ def cpu_baseline(sample_layers: int):
     q = syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * T, dtype=np.float32))
     pos = np.arange(L, L + T, dtype=np.int32)
     threads = min(os.cpu_count() or 1, HKV)
+    layers = 0
     t0 = time.perf_counter()
-    for _ in range(sample_layers):
-        pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=threads)
-    dt = (time.perf_counter() - t0) / sample_layers
+    while layers == 0 or time.perf_counter() - t0 < min_seconds:
+        for _ in range(64):
+            pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=threads)
+        layers += 64
+    elapsed = time.perf_counter() - t0
+    dt = elapsed / layers
     t0 = time.perf_counter()
-    pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=1)
-    dt1 = time.perf_counter() - t0
+    for _ in range(4):
+        pyoracle.attention(q, kc, vc, sc, sc, pos, None, T, 1, HQ, HKV, D, Pn, 1 / np.sqrt(D), threads=1)
+    dt1 = (time.perf_counter() - t0) / 4
     # Sampler: one stochastic top-20 round over the full vocabulary on one core.
     logits = syn.f32_to_bf16_bits(rng.standard_normal(VOCAB * T, dtype=np.float32) * np.float32(np.sqrt(3)))
     cfg = pyoracle.SamplingConfig()
@@ -711,8 +716,8 @@ def cpu_baseline(sample_layers: int):
     for _ in range(reps):
         pyoracle.speculative_accept(None, logits, VOCAB, [1, 2, 3], 7680, [0] * 7, VOCAB, cfg)
     ds = (time.perf_counter() - t0) / reps
-    return dict(us_per_layer=dt * 1e6, us_per_layer_1thread=dt1 * 1e6, threads=threads,
-                hardware_concurrency=os.cpu_count(), sampler_us_per_seq=ds * 1e6)
+    return dict(us_per_layer=dt * 1e6, us_per_layer_1thread=dt1 * 1e6, threads=threads, layers=layers,
+                seconds=elapsed, hardware_concurrency=os.cpu_count(), sampler_us_per_seq=ds * 1e6)
 
 
 def main():
@@ -928,7 +933,7 @@ def main():
     cpu = None
     if not args.skip_cpu:
         t0 = time.perf_counter()
-        cpu = cpu_baseline(sample_layers=2)
+        cpu = cpu_baseline()
         log(f"CPU baseline in {time.perf_counter() - t0:.1f}s: {cpu}")
 
     c2 = result["c2"]
@@ -959,8 +964,9 @@ def main():
     if "round" in result:
         line["round"] = {
             "workload": "whole greedy verify round as one replayed graph: prepare ids/positions, 64 A1 layers at "
-                        "context 7680+ (device-advanced positions), Q6 lm_head [248320, 5120] + argmax, greedy "
-                        "accept, accepted hidden row, MTP alignment ids, state slot; drafts planted at 0.8",
+                        "context 7680+ (device-advanced positions), fused Q6 lm_head [248320, 5120] -> top-20 keys -> "
+                        "greedy accept (no logits written), accepted hidden row, MTP alignment ids, state slot; "
+                        "drafts planted at 0.8",
             **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in result["round"].items()}}
     if "c3" in result:
         line["long_context"] = {"workload": "C3: context 260096, 1% outliers +-20, one layer",
@@ -1025,7 +1031,8 @@ def main():
             "unit": "GB/s",
             "cores": cpu["threads"],
             "kind": "port",
-            "sample": "oracle FP64 attention, 2 C2 layers (context 7680, 40Q/8KV, q_len 4), threads over KV heads",
+            "sample": f"oracle FP64 attention over {cpu['layers'] // 64} whole C2 steps ({cpu['layers']} layers, "
+                      f"context 7680, 40Q/8KV, q_len 4) in {cpu['seconds']:.1f} s, threads over KV heads",
             "us_per_layer": round(cpu["us_per_layer"], 1),
             "us_per_layer_1thread": round(cpu["us_per_layer_1thread"], 1),
             "hardware_concurrency": cpu["hardware_concurrency"],

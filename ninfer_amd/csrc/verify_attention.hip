@@ -976,8 +976,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 // Same split-K structure. A stage holds 32 keys of BF16 K (row r's 16-byte piece p at slot
 // p ^ (r % PB)) and V (natural order), no scales; QK^T and PV run on v_mfma_f32_16x16x32_bf16 with
 // the cache values and BF16 Q exactly as stored. P goes to the MFMA as two BF16 terms
-// (hi = BF16(p), lo = BF16(p - hi)), so the product keeps ~16 significant bits of P. New rows are
-// copied into the cache by a launch of their own before this kernel (BF16 caches have no codec).
+// (hi = BF16(p), lo = BF16(p - hi)), so the product keeps ~16 significant bits of P. At head_dim
+// 128 the split that owns the new rows copies them into the cache and into a stage of its own
+// (BF16 caches have no codec); at head_dim 256, or when several row chunks read the new rows, a
+// launch of their own copies them before this kernel.
 template <int D>
 struct GeoB {
     static constexpr int PB = D / 8;                // 16-byte pieces of a BF16 row

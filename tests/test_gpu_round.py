@@ -7,6 +7,10 @@ program_impl.h:780-870; replay contract docs/maintainer/op-development.md:106-12
   argmax -> greedy acceptance (advances length, sets token, stats) -> accepted hidden row ->
   MTP alignment ids -> recurrent-state slot = accepted.
 
+The "fused" form runs the lm_head and the acceptance as one call (nmi_speculative_accept_fused_head:
+per-workgroup top-20 keys, no logits written); its logits for the oracle check come from an eager
+linear on the same input after each replay.
+
 Between replays only the round's inputs change (per-layer q/k/v, the lm_head input rows, the draft
 tokens and the hidden rows), uploaded by the host; every piece of state the round carries (length,
 token, positions, caches, stats, the state slot) moves on the device. Every replay is checked against
@@ -34,7 +38,9 @@ def _f32(bits):
     return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def test_full_round_graph_replay(gpu, oracle):
+@pytest.mark.parametrize("head_form", ["unfused", "fused"])
+def test_full_round_graph_replay(gpu, oracle, head_form):
+    fused = head_form == "fused"
     L0 = 1500
     max_ctx = L0 + ROUNDS * T + T
     rng = np.random.default_rng(2024)
@@ -62,12 +68,15 @@ def test_full_round_graph_replay(gpu, oracle):
                   acc=DeviceArray(na.I32, (1,)),
                   stats=DeviceArray.from_numpy(na.I64, np.zeros(4 + K, np.int64), (4 + K,)),
                   sws=DeviceBuffer(max(256, ops.sampling_workspace_bytes(VALID, T))),
+                  hws=DeviceBuffer(ops.speculative_accept_fused_head_workspace_bytes(K, 1)),
                   hidden=DeviceArray(na.BF16, (HID, T)), sel=DeviceArray(na.BF16, (HID, 1)),
                   align=DeviceArray.from_numpy(na.I32, np.full(T, -1, np.int32), (T,)),
                   slot=DeviceArray.from_numpy(na.I32, np.array([-1], np.int32), (1,)))
         cfg, keep = gpu_runner.upload_configs([na.SamplingConfig()])  # greedy (temperature 0)
         st["cfg"], st["keep"] = cfg, keep
         st["ws"].fill(0xFF)
+        st["hws"].fill(0xFF)
+        st["x3"] = DeviceArray(na.BF16, (HID, T, 1), buf=st["x"].buf)
         return st
 
     states = [make_state(), make_state()]  # [graph, eager]
@@ -79,12 +88,18 @@ def test_full_round_graph_replay(gpu, oracle):
             ops.gqa_attention(st["q"][l].tensor(), st["k"][l].tensor(), st["v"][l].tensor(), st["pos"].tensor(),
                               cases[0].scale, st["caches"][l].view(), (1, max_ctx), st["ws"],
                               st["out"][l].tensor(), stream)
-        ops.linear(st["x"].tensor(), head.w, st["logits"].tensor(), stream)
-        ops.argmax(st["logits"].tensor(), st["target"].tensor(), VALID, stream)
-        ops.speculative_accept_greedy_drafts(st["target"].tensor(), st["logits"].tensor(), st["drafts"].tensor(),
-                                             st["length"].tensor(), st["token"].tensor(), st["so"].tensor(),
-                                             st["ns"].tensor(), st["acc"].tensor(), st["stats"].tensor(), VALID,
-                                             st["cfg"].ptr, st["sws"], stream)
+        if fused:
+            ops.speculative_accept_fused_head(st["x3"].tensor(), head.w, st["drafts"].tensor(), st["length"].tensor(),
+                                              st["token"].tensor(), st["so"].tensor(), st["ns"].tensor(),
+                                              st["acc"].tensor(), st["stats"].tensor(), VALID, st["cfg"].ptr,
+                                              st["hws"], stream)
+        else:
+            ops.linear(st["x"].tensor(), head.w, st["logits"].tensor(), stream)
+            ops.argmax(st["logits"].tensor(), st["target"].tensor(), VALID, stream)
+            ops.speculative_accept_greedy_drafts(st["target"].tensor(), st["logits"].tensor(), st["drafts"].tensor(),
+                                                 st["length"].tensor(), st["token"].tensor(), st["so"].tensor(),
+                                                 st["ns"].tensor(), st["acc"].tensor(), st["stats"].tensor(), VALID,
+                                                 st["cfg"].ptr, st["sws"], stream)
         ops.speculative_select_accepted_hidden(st["hidden"].tensor(), st["acc"].tensor(), st["sel"].tensor(), stream)
         ops.mtp_prepare_alignment_ids(st["ids"].tensor(), st["token"].tensor(), st["acc"].tensor(),
                                       st["align"].tensor(), stream)
@@ -99,7 +114,7 @@ def test_full_round_graph_replay(gpu, oracle):
     length, token, stats = L0, 11, np.zeros(4 + K, np.int64)
     align = np.full(T, -1, np.int32)
     for r in range(ROUNDS):
-        print(f"case whole round graph replay round {r} length {length}", flush=True)
+        print(f"case whole round graph replay ({head_form}) round {r} length {length}", flush=True)
         q = [syn.normal_bf16(syn.derive_seed(40, r, l, 1), D * Hq * T) for l in range(LAYERS)]
         kk = [syn.normal_bf16(syn.derive_seed(40, r, l, 2), D * Hkv * T) for l in range(LAYERS)]
         vv = [syn.normal_bf16(syn.derive_seed(40, r, l, 3), D * Hkv * T) for l in range(LAYERS)]
@@ -121,10 +136,14 @@ def test_full_round_graph_replay(gpu, oracle):
             st["drafts"].upload(drafts)
         graph.launch()
         round_ops(states[1])
+        if fused:  # the logits the fused call never wrote, for the checks below
+            ops.linear(states[0]["x"].tensor(), head.w, states[0]["logits"].tensor(), stream)
         stream.synchronize()
         g, e = states
-        for name in ("ids", "pos", "logits", "target", "so", "ns", "acc", "length", "token", "stats", "sel",
-                     "align", "slot"):
+        names = ["ids", "pos", "so", "ns", "acc", "length", "token", "stats", "sel", "align", "slot"]
+        if not fused:
+            names += ["logits", "target"]
+        for name in names:
             assert np.array_equal(g[name].numpy(), e[name].numpy()), f"round {r}: graph != eager in {name}"
         for l in range(LAYERS):
             assert np.array_equal(g["out"][l].numpy(), e["out"][l].numpy()), f"round {r} layer {l}"
@@ -143,7 +162,8 @@ def test_full_round_graph_replay(gpu, oracle):
         # targets are the argmax of the logits the lm_head wrote; acceptance follows the oracle
         logits = g["logits"].numpy().reshape(T, V)
         tgt = np.array([qp.argmax_lowest(logits[t], VALID) for t in range(T)], np.int32)
-        assert list(g["target"].numpy()) == list(tgt)
+        if not fused:
+            assert list(g["target"].numpy()) == list(tgt)
         exp = oracle.speculative_accept(tgt, logits.reshape(-1), V, drafts, length, stats, VALID,
                                         oracle.SamplingConfig())
         assert list(g["so"].numpy()) == list(exp["sampled_out"]), r
