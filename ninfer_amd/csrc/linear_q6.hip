@@ -203,10 +203,10 @@ __device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, c
     const int o_h = r0 * (G * 16) + chunk * C::kHighRow;
     const int o_s = r0 * (G * 2) + chunk * C::kScaleRow;
 #pragma unroll
-    for (int q = 0; q < C::kNibDma; ++q) { dma16(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
+    for (int q = 0; q < C::kNibDma; ++q) { dma16_nt(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
 #pragma unroll
-    for (int q = 0; q < C::kHighDma; ++q) { dma16(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
-    dma4s(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
+    for (int q = 0; q < C::kHighDma; ++q) { dma16_nt(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
+    dma4s_nt(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
 }
 
 template <int TP, int W, int CG, bool HEAD>
