@@ -31,10 +31,10 @@ __device__ __forceinline__ void dma4s(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char*
 
 // Non-temporal forms (cache policy nt, lines evicted first): for streams whose bytes one workgroup
 // reads once per call. Measured on MI355X with the attention's K/V code DMAs: C3 120 -> 107 us and
-// C2 15.0 -> 14.5 us per layer, the BF16-cache C3 192 -> 171 us; the [248320, 5120] lm_head 191 ->
-// 187 us. They cost where other workgroups re-read the lines through L2 (row-chunked tree attention:
-// 304 -> 339 us), so attention uses them only for one sequence with one row chunk, and only for the
-// code planes (the small scale DMAs measured faster with the default policy).
+// C2 15.0 -> 14.5 us per layer, the BF16-cache C3 192 -> 171 us, the batch-16 layer 135 -> 130 us;
+// the [248320, 5120] lm_head 191 -> 187 us. They cost where other workgroups re-read the lines
+// through L2 (row-chunked tree attention: 304 -> 339 us), so attention uses them only with one row
+// chunk, and only for the code planes (the small scale DMAs measured faster with the default).
 __device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t rsrc, NMI_AS3 char* lds, int voff, int soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (NMI_AS3 void*)lds, 16, voff, soff, 0, 2);
 }

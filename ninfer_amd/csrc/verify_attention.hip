@@ -325,8 +325,8 @@ __device__ __forceinline__ DmaLanes make_dma_lanes(int lane) {
 // codes go through soffset, which moves only the source address; the LDS address is M0 + 16 * lane
 // (4 * lane for scales). Both scale loads run on the full wave: lane-divergent descriptors would
 // turn one DMA into a waterfall loop.
-// ONCE: every key of the launch is read by one workgroup (one sequence, one row chunk), so the code
-// DMAs take the non-temporal policy (the scale DMAs keep the default: measured faster).
+// ONCE: every key of the launch is read by one workgroup (one row chunk), so the code DMAs take the
+// non-temporal policy (the scale DMAs keep the default: measured faster).
 template <int D, bool ONCE>
 __device__ __forceinline__ void issue_chunk(NMI_AS3 char* st, const HeadBuffers& hb, const DmaLanes& dl,
                                             int c0, int lane) {
@@ -1781,8 +1781,8 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.split_budget = plan.split_budget;
     a.max_keys = static_cast<int32_t>(max_keys);
     a.scale_log2 = scale * 1.4426950408889634f;
-    // One sequence and one row chunk: every key is read by exactly one workgroup (non-temporal DMAs).
-    const bool once = c.B == 1 && plan.row_chunks == 1;
+    // One row chunk: every key is read by exactly one workgroup (non-temporal DMAs).
+    const bool once = plan.row_chunks == 1;
     const int rows = plan.tokens_per_chunk * plan.G;
     dim3 grid(plan.split_slots, c.Hkv, plan.row_chunks);
 #define NMI_PARTIAL(KERNEL, NT, D)                                                                             \
