@@ -104,7 +104,7 @@ int nmi_linear(const nmi_tensor* x, const nmi_weight* w, nmi_tensor* out, nmi_st
     return guarded([&] {
         Checked c = check(x, w, out, NMI_BF16);
         c.args.out = static_cast<uint16_t*>(out->data);
-        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T);
+        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T, false, c.args.K);
         launch_linear_q6(c.args, p, reinterpret_cast<hipStream_t>(stream));
     });
 }
@@ -123,7 +123,7 @@ int nmi_linear_argmax(const nmi_tensor* x, const nmi_weight* w, int32_t valid_ro
                 "workspace must be non-null, 256-byte aligned and at least the size query");
         c.args.valid_rows = valid_rows;
         c.args.keys = static_cast<uint64_t*>(workspace);
-        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T);
+        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T, false, c.args.K);
         const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
         launch_linear_q6(c.args, p, s);
         launch_linear_argmax_reduce(c.args.keys, c.T, p.grid * p.waves, static_cast<int32_t*>(out->data), s);
@@ -156,7 +156,7 @@ int nmi_speculative_accept_fused_head(const nmi_tensor* x, const nmi_weight* w, 
         const size_t need = linear_topcap_workspace_bytes(c.T);
         require(workspace != nullptr && workspace_bytes >= need && aligned(workspace, 256),
                 "workspace must be non-null, 256-byte aligned and at least the size query");
-        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T, true);
+        const LinearPlan p = plan_linear(c.args.N, c.args.Kp, c.T, true, c.args.K);
         c.args.valid_rows = token_domain;
         c.args.cand = static_cast<uint64_t*>(workspace);
         c.args.config = config;

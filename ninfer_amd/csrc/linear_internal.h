@@ -37,14 +37,16 @@ struct LinearArgs {
 
 // Columns per pass and waves per workgroup for a problem (LDS fit), and the LDS bytes.
 struct LinearPlan {
-    int32_t tp;      // 4, 8 or 16
+    bool wide;       // K-outer form: 32 or 64 columns per pass (T > 16)
+    int32_t tp;      // 4, 8, 16, or 32 / 64 (wide)
     int32_t waves;   // per workgroup
     int32_t cg;      // groups of 64 codes per streamed chunk (4 or 8)
     int32_t grid;    // workgroups
     size_t lds;
     int32_t passes;
 };
-LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap = false);
+// K: the unpadded K (the wide form needs K % 8 == 0: x columns start 16-byte aligned).
+LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap, int32_t K);
 size_t linear_argmax_workspace_bytes(int32_t T);
 // Candidate-list bytes of the top-cap form for T columns (any plan: at most one list per CU).
 size_t linear_topcap_workspace_bytes(int32_t T);

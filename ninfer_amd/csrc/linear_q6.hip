@@ -397,12 +397,15 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
                 }
                 if (row < a.valid_rows) { best = max_u64(best, logit_key(bfv, row)); }
                 if constexpr (HEAD) {
+                    // rows past valid_rows (the token domain) never reach the penalty lookup: the
+                    // counts array covers the domain only
+                    const bool live = c < a.tp && row < a.valid_rows;
                     float v = bf16_to_f32(bfv);
-                    if (hpen) {
+                    if (hpen && live) {
                         v = adjusted_logit(v, row, a.config[hseq], a.drafts + static_cast<int64_t>(hseq) * (a.cols_per_seq - 1),
                                            hcol);
                     }
-                    kk[i] = (c < a.tp && row < a.valid_rows) ? sort_key(v, row) : 0ull;
+                    kk[i] = live ? sort_key(v, row) : 0ull;
                 }
                 tot[i] = 0.0f;
             }
@@ -478,6 +481,325 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     }
 }
 
+// ---- wide form: more than 16 columns, 32 per pass over the weight --------------------------------
+//
+// The column passes above re-stream the whole weight once per 4, 8 or 16 columns (x of 16 columns
+// at K = 5120 already fills the LDS). Here K is the outer loop: x moves through the LDS in blocks of
+// 256 (4 groups) for all 16 * NCB columns, and each wave keeps FP32 totals for its kWideTiles tiles x
+// 16 * NCB columns in registers while it streams those tiles' 4-group chunks of the block. A lane
+// decodes its 16 codes of a group once and feeds NCB pairs of MFMAs (one per 16-column block).
+// Each x block carries its own power-of-two column factors (its largest |x| lands in
+// [2^14, 2^15), so its BF16 values are exact in FP16); a block's per-group sums, weighted by their
+// scales, are rescaled by the factor's exact inverse into the totals. The epilogue writes BF16
+// logits, argmax keys, or per column the workgroup's kCandidateCap largest keys (top-cap form).
+constexpr int kWideWaves = 8;
+constexpr int kWideCG = 4;          // groups per streamed chunk and per x block (256 elements of K)
+constexpr int kWideTiles = 8;       // 16-row tiles per wave
+constexpr int kWideStages = 2;      // chunk stages per wave: kWideStages chunks in flight while one computes
+constexpr int kXBlockCol = kWideCG * 128; // bytes of one column of an x block (FP16)
+constexpr int kWideXBuffers = 4;    // x blocks in LDS: the pair in use and the next pair
+constexpr int kWideColumns = 32;    // columns per pass (two 16-column MFMA blocks)
+
+template <int NCB>
+constexpr size_t wide_x_bytes() { return static_cast<size_t>(kWideXBuffers) * 16 * NCB * (kXBlockCol + 4); } // x blocks + factors
+
+template <int NCB>
+constexpr size_t wide_lds_bytes() {
+    constexpr size_t main = wide_x_bytes<NCB>() + static_cast<size_t>(kWideWaves) * kWideStages * Chunk<kWideCG>::kStage;
+    // top-cap epilogue: the workgroup's BF16 logits of every column, then the selection scratch
+    constexpr size_t keys = static_cast<size_t>(16 * NCB) * kWideWaves * kWideTiles * kTileRows * 2 +
+                            static_cast<size_t>(kWideWaves) * (64 + kCandidateCap) * 8;
+    return main > keys ? main : keys;
+}
+
+template <int NCB>
+__global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearArgs a) {
+    constexpr int W = kWideWaves;
+    constexpr int CG = kWideCG;
+    constexpr int MAXT = kWideTiles;
+    constexpr int NC = 16 * NCB;      // columns of the pass
+    constexpr int TPC = 64 * W / NC;  // x staging threads per column (consecutive lanes of one wave)
+    constexpr int EPT = CG * 64 / TPC; // x elements of a block per staging thread
+    constexpr int NX = EPT / 8;       // 16-byte x loads per staging thread
+    static_assert(MAXT % 2 == 0 && MAXT >= 3 && TPC <= 64, "wide geometry");
+    using CH = Chunk<CG>;
+    extern __shared__ __attribute__((aligned(16))) char dsmem[];
+    NMI_AS3 char* smem = (NMI_AS3 char*)dsmem;
+    constexpr int XB = kWideXBuffers;
+    NMI_AS3 float* finv = (NMI_AS3 float*)(smem + XB * NC * kXBlockCol); // [XB][NC] 1 / column factor
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int S = kWideStages;
+    NMI_AS3 char* ring = smem + wide_x_bytes<NCB>() + wave * S * CH::kStage;
+    const int G = a.G;
+    const int nkb = (G + CG - 1) / CG;
+    const int gw = blockIdx.x * W + wave;
+    const int nwaves = gridDim.x * W;
+    const Planes pl{raw_buffer(a.qdata, a.nib_bytes), raw_buffer(a.qhigh, a.high_bytes), raw_buffer(a.scales, a.scale_bytes)};
+    const LinDma<CG> dl = make_lin_dma<CG>(lane, G);
+    const int c = lane & 15; // MFMA column within a 16-column block
+    const int b = lane >> 4; // 16-code block of a group / accumulator row block
+
+    // x staging: thread -> (column scol, K slice spart of a block). One 16-byte buffer load per piece
+    // whatever the column or K (past K or past the pass's columns the offset leaves the range and
+    // reads zero), so every lane issues exactly NX loads.
+    const int scol = threadIdx.x / TPC;
+    const int spart = threadIdx.x - scol * TPC;
+    const __amdgpu_buffer_rsrc_t xr_src = raw_buffer(a.x, static_cast<int64_t>(a.K) * a.T * 2);
+    i4 xr[NX];
+    auto xload = [&](int kb) {
+#pragma unroll
+        for (int n = 0; n < NX; ++n) {
+            const int k = kb * CG * 64 + spart * EPT + 8 * n;
+            const int off = (scol < a.tp && k < a.K) ? 2 * (a.K * (a.t0 + scol) + k) : kOutOfRange;
+            xr[n] = __builtin_bit_cast(i4, __builtin_amdgcn_raw_buffer_load_b128(xr_src, off, 0, 0));
+        }
+    };
+    // Column factor over the TPC lanes of the column, then the pieces as FP16 in the pairing
+    // (e0, e4, e1, e5, e2, e6, e3, e7); piece q of column col sits at 16-byte slot q ^ (col % 16).
+    auto xstage = [&](int buf) {
+        uint32_t m = 0;
+#pragma unroll
+        for (int n = 0; n < NX; ++n) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const uint32_t w = static_cast<uint32_t>(xr[n][h]);
+                m = max(m, max(w & 0x7fffu, (w >> 16) & 0x7fffu));
+            }
+        }
+#pragma unroll
+        for (int s = 1; s < TPC; s <<= 1) { m = max(m, static_cast<uint32_t>(__shfl_xor(static_cast<int>(m), s, 64))); }
+        float f = 1.0f;
+        if (m != 0 && m < 0x7f80u) { f = ldexpf(1.0f, 14 - max(static_cast<int>(m >> 7) - 127, -100)); }
+        NMI_AS3 char* dst = smem + buf * NC * kXBlockCol + scol * kXBlockCol;
+#pragma unroll
+        for (int n = 0; n < NX; ++n) {
+            uint16_t v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) { v[e] = static_cast<uint16_t>(static_cast<uint32_t>(xr[n][e >> 1]) >> (16 * (e & 1))); }
+            h2 pk[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                pk[p] = h2{static_cast<_Float16>(bf16_to_f32(v[p]) * f), static_cast<_Float16>(bf16_to_f32(v[p + 4]) * f)};
+            }
+            const int q = spart * NX + n;
+            *(NMI_AS3 i4*)(dst + 16 * (q ^ (scol & 15))) = __builtin_bit_cast(i4, pk);
+        }
+        if (spart == 0) { finv[buf * NC + scol] = 1.0f / f; } // a power of two: exact
+    };
+
+    // Blocks go in pairs: item j of pair p streams chunk 2p + (j & 1) of tile gw + (j / 2) * nwaves,
+    // so a tile's two chunks of the pair are consecutive items and the 128-byte lines of its high
+    // plane (64 bytes per chunk) are used whole while they are in L2. x block kb lives in buffer
+    // kb % 4: pair p computes on blocks 2p and 2p + 1 while blocks 2p + 2 and 2p + 3 are staged.
+    // Slots past the last tile and blocks past the last one still issue their DMAs (they read zero
+    // or bytes that are never used), so every wait below is one fixed count.
+    constexpr int J = 2 * MAXT; // items per pair
+    auto issue = [&](NMI_AS3 char* st, int p, int j) {
+        issue_item<CG>(st, pl, dl, gw + (j >> 1) * nwaves, 2 * p + (j & 1), G);
+    };
+    const int npairs = (nkb + 1) / 2;
+    auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
+    xload(0);
+#pragma unroll
+    for (int j = 0; j < S; ++j) { issue(ring + j * CH::kStage, 0, j); }
+    __builtin_amdgcn_s_waitcnt(((S * CH::kDma) & 0xf) | (((S * CH::kDma) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+    xstage(0);
+    xload(clamp_block(1));
+    __builtin_amdgcn_s_waitcnt(0); // once per launch: block 1 lands behind the first items
+    xstage(1);
+
+    const uint32_t kMaskA = 0x003f003fu;
+    const uint32_t kConstB = 0x64206420u;
+    float tot[MAXT][NCB][4];
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) { tot[i][cb][r] = 0.0f; }
+        }
+    }
+    // waits for item j: the S - 1 younger items stay in flight, and the x loads while they are younger
+    constexpr int kYoung = (S - 1) * CH::kDma;
+    constexpr int kWaitItem = (kYoung & 0xf) | ((kYoung >> 4) << 14) | (0x7 << 4) | (0xf << 8);
+    constexpr int kWaitItemX = ((kYoung + NX) & 0xf) | (((kYoung + NX) >> 4) << 14) | (0x7 << 4) | (0xf << 8);
+    static_assert(J > 2 * S, "both x blocks of the next pair land inside the pair");
+#pragma unroll 1
+    for (int p = 0; p < npairs; ++p) {
+        __syncthreads(); // blocks 2p, 2p + 1 are in LDS; every wave is done with blocks 2p - 2, 2p - 1
+        // x loads of block 2p + 2: issued after items 0 .. S - 1, staged at item S; those of block
+        // 2p + 3: issued at item S after items .. 2S - 1, staged at item 2S
+        xload(clamp_block(2 * p + 2));
+        float fi[2][NCB];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) { fi[h][cb] = finv[((2 * p + h) & (XB - 1)) * NC + c + 16 * cb]; }
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int i = j >> 1;
+            const int h = j & 1;
+            const int kb = 2 * p + h;
+            NMI_AS3 char* st = ring + (j % S) * CH::kStage;
+            if (j < S || (j > S && j < 2 * S)) {
+                __builtin_amdgcn_s_waitcnt(kWaitItemX);
+            } else {
+                __builtin_amdgcn_s_waitcnt(kWaitItem);
+            }
+            if (j == S) {
+                xstage((2 * p + 2) & (XB - 1));
+                xload(clamp_block(2 * p + 3));
+            }
+            if (j == 2 * S) { xstage((2 * p + 3) & (XB - 1)); }
+            const NMI_AS3 char* xk = smem + (kb & (XB - 1)) * NC * kXBlockCol;
+            const int ng = min(CG, G - kb * CG); // <= 0 for the block past the last
+            float bacc[NCB][4];
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) { bacc[cb][r] = 0.0f; }
+            }
+            uint64_t nib[CG];
+            uint32_t hig[CG];
+            uint32_t sc[4][CG / 2];
+#pragma unroll
+            for (int gl = 0; gl < CG; ++gl) {
+                nib[gl] = *(const NMI_AS3 uint64_t*)(st + c * CH::kNibRow + 16 * ((2 * gl + (b >> 1)) ^ swz<CH::kNibRow>(c)) +
+                                                     8 * (b & 1));
+                hig[gl] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + c * CH::kHighRow + 16 * (gl ^ swz<CH::kHighRow>(c)) + 4 * b);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int q = 0; q < CG / 2; ++q) {
+                    sc[r][q] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + CH::kHigh + (4 * b + r) * CH::kScaleRow + 4 * q);
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
+            if (j + S < J) {
+                issue(st, p, j + S);
+            } else {
+                issue(st, p + 1, j + S - J);
+            }
+#pragma unroll
+            for (int gl = 0; gl < CG; ++gl) {
+                if (gl < ng) {
+                    h8 a0, a1;
+                    decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
+                    const int q0 = 8 * gl + 2 * b;
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb) {
+                        const NMI_AS3 char* xc = xk + (c + 16 * cb) * kXBlockCol;
+                        const i4 x0 = *(const NMI_AS3 i4*)(xc + 16 * (q0 ^ c));
+                        const i4 x1 = *(const NMI_AS3 i4*)(xc + 16 * ((q0 + 1) ^ c));
+                        f4 acc = {0.f, 0.f, 0.f, 0.f};
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const uint32_t w = sc[r][gl >> 1];
+                            const float sv = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
+                            bacc[cb][r] = fmaf(sv, acc[r], bacc[cb][r]);
+                        }
+                    }
+                }
+            }
+            if (ng > 0) {
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) { tot[i][cb][r] = fmaf(bacc[cb][r], fi[h][cb], tot[i][cb][r]); }
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0); // the DMAs of the items past the last block
+    __syncthreads();               // LDS is free for the epilogue
+
+    // ---- epilogue: lane holds rows 4b + r of tile gw + i * nwaves for columns c + 16 cb. The
+    // top-cap form first puts the workgroup's BF16 logits in LDS ([column][wave][tile slot][16 rows]).
+    constexpr int RPW = MAXT * kTileRows; // rows per wave and column
+    NMI_AS3 uint16_t* lg = (NMI_AS3 uint16_t*)smem;
+    uint64_t best[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) { best[cb] = 0; }
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+        const int r0 = (gw + i * nwaves) * kTileRows + 4 * b;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            const int col = c + 16 * cb;
+            uint16_t bf[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                bf[r] = f32_to_bf16_bits(tot[i][cb][r]);
+                if (r0 + r < a.valid_rows) { best[cb] = max_u64(best[cb], logit_key(bf[r], r0 + r)); }
+            }
+            const uint2 packed{static_cast<uint32_t>(bf[0]) | (static_cast<uint32_t>(bf[1]) << 16),
+                               static_cast<uint32_t>(bf[2]) | (static_cast<uint32_t>(bf[3]) << 16)};
+            if (a.cand != nullptr) {
+                *(NMI_AS3 i2*)(lg + (col * W + wave) * RPW + i * kTileRows + 4 * b) =
+                    i2{static_cast<int>(packed.x), static_cast<int>(packed.y)};
+            }
+            if (a.out != nullptr && col < a.tp) {
+                uint16_t* o = a.out + static_cast<int64_t>(a.N) * (a.t0 + col) + r0;
+                if (r0 + 4 <= a.N && (a.N & 3) == 0) { // 8-byte aligned
+                    *reinterpret_cast<uint2*>(o) = packed;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (r0 + r < a.N) { o[r] = bf[r]; }
+                    }
+                }
+            }
+        }
+    }
+    if (a.keys != nullptr) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            uint64_t v = max_u64(best[cb], shfl_xor_u64(best[cb], 16));
+            v = max_u64(v, shfl_xor_u64(v, 32));
+            if (lane < 16 && c + 16 * cb < a.tp) { a.keys[static_cast<int64_t>(a.t0 + c + 16 * cb) * nwaves + gw] = v; }
+        }
+    }
+    if (a.cand != nullptr) {
+        // Top-cap form: wave w takes columns w, w + W, ...: the column's W * RPW keys (penalty-adjusted
+        // logits of rows below valid_rows), 16 per lane, then the kCandidateCap largest.
+        constexpr int KPL = W * RPW / 64; // keys per lane
+        uint64_t* wcand = (uint64_t*)(smem + NC * W * RPW * 2 + wave * 64 * 8);
+        uint64_t* wout = (uint64_t*)(smem + NC * W * RPW * 2 + W * 64 * 8 + wave * kCandidateCap * 8);
+        __syncthreads();
+#pragma unroll 1
+        for (int lc = wave; lc < a.tp; lc += W) {
+            const int t = a.t0 + lc;
+            const int hseq = t / a.cols_per_seq;
+            const int hcol = t - hseq * a.cols_per_seq;
+            const nmi_sampling_config& cf = a.config[hseq];
+            const bool hpen = cf.temperature > 0.0f && (cf.presence_penalty != 0.0f || cf.frequency_penalty != 0.0f);
+            uint64_t k[KPL];
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) {
+                const int slot = (e % (RPW / 64)) * 64 + lane; // row slot within the origin wave
+                const int wv = e / (RPW / 64);                 // origin wave
+                const int row = ((blockIdx.x * W + wv) + (slot / kTileRows) * nwaves) * kTileRows + slot % kTileRows;
+                k[e] = 0;
+                if (row < a.valid_rows) { // the penalty counts cover the token domain only
+                    float v = bf16_to_f32(lg[(lc * W + wv) * RPW + slot]);
+                    if (hpen) { v = adjusted_logit(v, row, cf, a.drafts + static_cast<int64_t>(hseq) * (a.cols_per_seq - 1), hcol); }
+                    k[e] = sort_key(v, row);
+                }
+            }
+            wave_top_cap(k, k, kCandidateCap, wcand, wout);
+            if (lane < kCandidateCap) {
+                a.cand[(static_cast<int64_t>(t) * gridDim.x + blockIdx.x) * kCandidateCap + lane] = wout[lane];
+            }
+            wave_lds_sync();
+        }
+    }
+}
+
 // One workgroup per column: the largest partial key -> the row.
 __global__ __launch_bounds__(256) void linear_argmax_reduce_kernel(const uint64_t* keys, int32_t waves, int32_t* out) {
     const int t = blockIdx.x;
@@ -516,9 +838,23 @@ constexpr LinearInstance kInstances[] = {
 };
 constexpr int kInstanceCount = sizeof(kInstances) / sizeof(kInstances[0]);
 
-LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap) {
+LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap, int32_t K) {
     const int32_t ntiles = (N + kTileRows - 1) / kTileRows;
     constexpr size_t kLds = 160 * 1024;
+    const int32_t wide_grid = (ntiles + kWideWaves * kWideTiles - 1) / (kWideWaves * kWideTiles);
+    if (T > 16 && K % 8 == 0 && wide_grid <= kLinearGrid) {
+        // one pass over the weight per 32 columns (64 columns per pass need 128 FP32 totals per lane
+        // beside the streaming registers: more than the 256 a lane has at two waves per SIMD)
+        LinearPlan p{};
+        p.wide = true;
+        p.tp = kWideColumns;
+        p.waves = kWideWaves;
+        p.cg = kWideCG;
+        p.lds = wide_lds_bytes<kWideColumns / 16>();
+        p.passes = (T + p.tp - 1) / p.tp;
+        p.grid = wide_grid;
+        return p;
+    }
     const int first = T <= 4 ? 6 : (T <= 8 ? 2 : 0);
     LinearPlan p{};
     for (int i = first; i < kInstanceCount; ++i) {
@@ -572,9 +908,29 @@ void launch_instance(const LinearArgs& a, const LinearPlan& p, hipStream_t strea
     launch_kernel<TP, W, CG, false>(a, p, stream);
 }
 
+template <int NCB>
+void launch_wide(const LinearArgs& a, const LinearPlan& p, hipStream_t stream) {
+    static const bool lds_raised = [] {
+        NMI_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_q6_wide_kernel<NCB>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        return true;
+    }();
+    (void)lds_raised;
+    hipLaunchKernelGGL((linear_q6_wide_kernel<NCB>), dim3(p.grid), dim3(64 * kWideWaves), wide_lds_bytes<NCB>(), stream, a);
+    check_launch("linear_q6_wide_kernel");
+}
+
 void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream) {
     a.ntiles = (a.N + kTileRows - 1) / kTileRows;
     a.waves = p.grid * p.waves;
+    if (p.wide) {
+        for (int32_t pass = 0; pass < p.passes; ++pass) {
+            a.t0 = pass * p.tp;
+            a.tp = std::min(p.tp, a.T - a.t0);
+            launch_wide<kWideColumns / 16>(a, p, stream);
+        }
+        return;
+    }
     for (int32_t pass = 0; pass < p.passes; ++pass) {
         a.t0 = pass * p.tp;
         a.tp = std::min(p.tp, a.T - a.t0);

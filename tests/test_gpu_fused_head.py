@@ -227,10 +227,12 @@ def test_fused_head_b16(gpu, big_head):
 
 
 @pytest.mark.parametrize("N,hidden,B,domain", [(1000, 512, 1, 1000), (5000, 640, 3, 4321), (3000, 1024, 5, 3000),
-                                               (17, 256, 2, 9), (2048, 8192, 2, 2048)])
+                                               (17, 256, 2, 9), (2048, 8192, 2, 2048), (6000, 1024, 9, 5000),
+                                               (20000, 2048, 16, 19000)])
 def test_fused_head_small_heads(gpu, N, hidden, B, domain):
-    """Several column passes (B = 5: 20 columns), rows not a multiple of 16, a token domain below the
-    cap (9 < 20 candidates), padded K and the largest K."""
+    """Rows not a multiple of 16, a token domain below the cap (9 < 20 candidates), padded K and the
+    largest K; more than 16 columns (B = 5, 9, 16) take the K-outer form, 32 columns per pass. The
+    penalty counts hold exactly the token domain."""
     print(f"case fused head N={N} hidden={hidden} B={B} domain={domain}", flush=True)
     rng = np.random.default_rng(N + hidden + B)
     Kp = qp.align_up(hidden, 128)
@@ -241,7 +243,7 @@ def test_fused_head_small_heads(gpu, N, hidden, B, domain):
     drafts = _plant(dw, x, domain, 2, 10)
     names = list(B1_CONFIGS)
     cfgs = [B1_CONFIGS[names[(b + N) % len(names)]] for b in range(B)]
-    counts = [np.ones(N, np.int32) if c.presence_penalty != 0.0 else None for c in cfgs]
+    counts = [np.ones(domain, np.int32) if c.presence_penalty != 0.0 else None for c in cfgs]
     check_case(dw, x, drafts, 50 + np.arange(B), domain, cfgs, counts, tag=f"N={N} hidden={hidden} B={B}")
 
 

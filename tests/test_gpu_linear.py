@@ -123,14 +123,14 @@ def head(request):
     return DeviceWeight(nib, high, sc, VOCAB, K)
 
 
-@pytest.mark.parametrize("T", [1, 4, 9, 16])
+@pytest.mark.parametrize("T", [1, 4, 9, 16, 24, 64])
 def test_linear_full_head(gpu, head, T):
     x = _x(100 + T, T, head.k)
     got = run_linear(head, x)
     check_logits(got, oracle_logits(head, x), f"linear [{head.n},{head.k}] T={T}")
 
 
-@pytest.mark.parametrize("T,valid", [(4, VOCAB), (16, VOCAB), (4, 151936)])
+@pytest.mark.parametrize("T,valid", [(4, VOCAB), (16, VOCAB), (4, 151936), (40, VOCAB)])
 def test_linear_argmax_full_head(gpu, head, T, valid):
     x = _x(200 + T, T, head.k)
     got = run_argmax(head, x, valid)
@@ -143,10 +143,12 @@ def test_linear_argmax_full_head(gpu, head, T, valid):
 
 
 @pytest.mark.parametrize("N,K,T", [(1, 64, 1), (17, 200, 3), (100, 1000, 5), (250, 4096, 9), (33, 640, 17),
-                                   (4096, 8192, 4), (64, 128, 16)])
+                                   (4096, 8192, 4), (64, 128, 16), (100, 1000, 33), (4096, 8192, 40),
+                                   (50, 1004, 20), (3000, 320, 64)])
 def test_linear_edge_shapes(gpu, N, K, T):
     """Rows not a multiple of 16, padded K (groups past K hold codes that x = 0 cancels), K up to the
-    8192 limit, several column passes (T = 17)."""
+    8192 limit, several column passes. T > 16 with K % 8 == 0 takes the K-outer form (32 columns per
+    pass: T = 17, 33, 40, 64); K = 1004 keeps the column passes."""
     print(f"case linear edge N={N} K={K} T={T}", flush=True)
     rng = np.random.default_rng(N * 7 + K + T)
     Kp = qp.align_up(K, 128)
