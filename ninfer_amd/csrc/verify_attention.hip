@@ -765,24 +765,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
         }
     }
 
-    // The first two chunks do not depend on the positions: start their DMA right away. A chunk
-    // that turns out to lie past the split's range is simply never read (it stays inside the
-    // padded cache, and the waits below fall back to vmcnt(0) when the next chunk is unused).
+    // The first two chunks do not depend on the positions. A chunk that turns out to lie past the
+    // split's range is simply never read (it stays inside the padded cache, and the waits below
+    // fall back to vmcnt(0) when the next chunk is unused). The first chunk's DMA starts right away;
+    // the second waits until Q has landed, so Q is not queued behind every wave's two chunks at
+    // launch (measured on MI355X: C2 14.60 -> 13.92 us per layer, C3, C4 and C5 unchanged).
     const int first = k0 + kChunk * wave;
     if (first + kChunk <= a.P) { issue_chunk<D, ONCE>(ring, hb, dl, first, lane); }
-    if (first + kStride + kChunk <= a.P) { issue_chunk<D, ONCE>(ring + GE::kStageBytes, hb, dl, first + kStride, lane); }
     if (wave == 0) {
-        if (first + kStride + kChunk <= a.P) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * GE::kDmaPerChunk));
-        } else if (first + kChunk <= a.P) {
+        if (first + kChunk <= a.P) {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(GE::kDmaPerChunk));
         } else {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
         }
     }
     // A bare barrier: the DMA'd Q and positions are in LDS once wave 0's wait returns, and a full
-    // __syncthreads() would also wait for every chunk DMA.
+    // __syncthreads() would also wait for the chunk DMAs.
     __builtin_amdgcn_s_barrier();
+    if (first + kStride + kChunk <= a.P) { issue_chunk<D, ONCE>(ring + GE::kStageBytes, hb, dl, first + kStride, lane); }
     i4 qraw[NT][G][2];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
