@@ -940,6 +940,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
         stage = 1;
 #pragma unroll 1
         for (; cj < hend; cj += kStride) {
+            // Issue priority alternates per chunk (phase offset by the workgroup index), so waves
+            // sharing a SIMD take turns by progress instead of the oldest one always issuing first
+            // (MI355X, C3, four paired runs: -1.0 to -2.5 us per layer; C2 unchanged).
+            if ((((cj - first) / kStride) + blockIdx.x + blockIdx.y) & 1) {
+                __builtin_amdgcn_s_setprio(3);
+            } else {
+                __builtin_amdgcn_s_setprio(0);
+            }
             const int cn = cj + kStride; // next chunk (if < hend, its DMA was issued two steps ago)
             NMI_AS3 char* stn = ring + stage * GE::kStageBytes;
             // Chunk j+1's DMA done (j+2's may stay outstanding). Reading a stage past the end is
