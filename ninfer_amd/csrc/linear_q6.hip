@@ -545,13 +545,15 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
     // reads zero), so every lane issues exactly NX loads.
     const int scol = threadIdx.x / TPC;
     const int spart = threadIdx.x - scol * TPC;
-    const __amdgpu_buffer_rsrc_t xr_src = raw_buffer(a.x, static_cast<int64_t>(a.K) * a.T * 2);
+    // The pass's own columns only (at most 8192 x 32 BF16 values), so the out-of-range offset lies
+    // far past the resource whatever T is.
+    const __amdgpu_buffer_rsrc_t xr_src = raw_buffer(a.x + static_cast<int64_t>(a.K) * a.t0, static_cast<int64_t>(a.K) * a.tp * 2);
     i4 xr[NX];
     auto xload = [&](int kb) {
 #pragma unroll
         for (int n = 0; n < NX; ++n) {
             const int k = kb * CG * 64 + spart * EPT + 8 * n;
-            const int off = (scol < a.tp && k < a.K) ? 2 * (a.K * (a.t0 + scol) + k) : kOutOfRange;
+            const int off = (scol < a.tp && k < a.K) ? 2 * (a.K * scol + k) : kOutOfRange;
             xr[n] = __builtin_bit_cast(i4, __builtin_amdgcn_raw_buffer_load_b128(xr_src, off, 0, 0));
         }
     };
