@@ -190,7 +190,12 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
             require_contiguous_nonnull(*parents, op, "parents");
         }
         require_built(c, op);
-        const SplitPlan plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys);
+        // The 80-row form (INT8, head_dim 128) unless the static scratch of the allocation-free entry
+        // cannot hold its partials.
+        SplitPlan plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys, c.kb == nullptr);
+        if (static_ws && plan.bytes > kStaticScratchBytes && plan.rows_per_slot != kAttnRowsPerTile) {
+            plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys, false);
+        }
         if (static_ws) {
             ws = static_scratch(plan.bytes, op);
             ws_bytes = plan.bytes;
@@ -280,7 +285,9 @@ size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int3
         q_heads % kv_heads != 0 || head_dim <= 0 || max_visible_keys == 0 || q_heads / kv_heads > kAttnRowsPerTile) {
         return 0;
     }
-    return plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys).bytes;
+    // the cache type is not an argument: the larger of the two row forms
+    return std::max(plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys, true).bytes,
+                    plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys, false).bytes);
 }
 
 // reference gqa_attention_workspace_bytes(q_heads, tokens) (src/ops/wrapper/gqa_attention.cpp:229-245):

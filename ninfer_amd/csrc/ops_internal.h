@@ -31,6 +31,7 @@ struct SplitPlan {
     int32_t keys_per_split = 0;   // multiple of 128 (B == 1)
     int32_t split_slots = 0;      // partial slots per (row chunk, KV head)
     int32_t split_budget = 0;     // B > 1: most splits per (row chunk, KV head) the device cuts the batch into
+    int32_t rows_per_slot = 32;   // query rows of one partial slot: 32, or 80 (one row chunk of 5 MFMA tiles)
     size_t part_o_offset = 0;
     size_t part_ml_offset = 0;
     size_t seq_table_offset = 0; // B > 1: per sequence (first slot, split count)
@@ -38,14 +39,17 @@ struct SplitPlan {
 };
 
 inline constexpr int32_t kAttnRowsPerTile = 32;
+inline constexpr int32_t kAttnWideRows = 80;          // INT8, head_dim 128: up to 80 rows in one row chunk
 inline constexpr int32_t kAttnTargetWorkgroups = 512; // 2 per CU on 256 CUs
 inline constexpr int32_t kAttnMinKeysPerSplit = 256;
 inline constexpr int32_t kAttnMaxTokens = 32;
 
+// wide_rows: the INT8 head_dim-128 cache may serve 33..80 query rows (T x G) in one row chunk of
+// five 16-row tiles (one workgroup per CU) instead of several 32-row chunks that each stream every key.
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
-                         uint32_t max_visible_keys);
+                         uint32_t max_visible_keys, bool wide_rows);
 
-// The largest plan_attention(Hq, Hkv, D, T, 1, keys).bytes over every envelope (keys >= 1).
+// The largest plan_attention(Hq, Hkv, D, T, 1, keys, either form).bytes over every envelope (keys >= 1).
 size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T);
 
 // Size of the per-device static split scratch of nmi_gqa_attention_noalloc. 16 MiB holds every plan

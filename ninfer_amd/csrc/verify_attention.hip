@@ -28,6 +28,9 @@
 //  * The softmax keeps a lazy reference maximum: probabilities are FP16 exp2(s - m + 8) and m
 //    moves (rescaling O) only when a score exceeds it by 2^7, so most chunks skip the rescale.
 //  * GQA x q_len rows (5 x 4 = 20 for the 40/8 geometry) are padded to two 16-row MFMA tiles.
+//    33..80 rows (a 16-node tree at group 5) take five tiles in one workgroup at one wave per
+//    SIMD, so every key is streamed once (several 32-row chunks would each stream all keys): the
+//    Q operands sit in LDS and the tiles run one after another on each chunk's converted K', V'.
 #include "common.h"
 #include "device_utils.h"
 #include "ops_internal.h"
@@ -35,6 +38,7 @@
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 #include "lds_dma.h"
 
@@ -586,6 +590,109 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<D>& r, int c0, boo
     pv_chunk<NT, D>(pop, r.vr, r.vsw, c0, masked, s, kr, c, g);
 }
 
+// The five-tile form (80 rows): the chunk's K' and V'^T operands are converted once and the row
+// tiles then run one after another (QK^T, softmax, PV per tile), so only one tile's scores are live.
+// Per row the arithmetic is the one compute_chunk does.
+template <int D, typename State>
+__device__ __forceinline__ void softmax_tile(const f4 (&sacc)[2], int nt, int c0, bool masked, State& s,
+                                             const KeyRange& kr, int g, float (&p)[8]) {
+    float sv[8];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { sv[4 * kt + e] = sacc[kt][e]; }
+    }
+    if (masked) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int key = c0 + 16 * (i >> 2) + 4 * g + (i & 3);
+            const int u = key - kr.new_base;
+            const bool bit = ((s.nmask[nt] >> (u & 31)) & 1u) != 0u;
+            const bool vis = (key < kr.vis_all) | ((key < kr.key_end) & (static_cast<unsigned>(u) < 32u) & bit);
+            sv[i] = vis ? sv[i] : -INFINITY;
+        }
+    }
+    float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
+    cmax = group4_max(cmax);
+    const bool need = cmax > s.m[nt] + s.rowthr[nt];
+    if (__any(need)) {
+        const float mn = need ? cmax : s.m[nt];
+        const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) { s.O[nt][t] *= alpha; }
+        s.l[nt] *= alpha;
+        s.m[nt] = mn;
+    }
+    const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) { p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)); }
+}
+
+template <int TT, int D>
+__device__ __forceinline__ void v_operand(const typename ChunkRegs<D>::VRow (&vr)[8], const h2 (&vsp)[4], h8 (&va)[D / 16]) {
+    h2 pr[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) { pr[w] = __builtin_bit_cast(h2, v_pair<TT>(vr[2 * w], vr[2 * w + 1])) * vsp[w]; }
+    va[TT] = __builtin_bit_cast(h8, pr);
+}
+
+template <int D, int... TT>
+__device__ __forceinline__ void v_operands(const typename ChunkRegs<D>::VRow (&vr)[8], const h2 (&vsp)[4], h8 (&va)[D / 16],
+                                           std::integer_sequence<int, TT...>) {
+    (v_operand<TT, D>(vr, vsp, va), ...);
+}
+
+template <int NT, int D>
+__device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c0, bool masked, RowState<NT, D>& s,
+                                                    const KeyRange& kr, int c, int g, const NMI_AS3 char* qop) {
+    const int lane = threadIdx.x & 63;
+    h8 ka[2][D / 64][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int gq = 0; gq < D / 64; ++gq) {
+            const h2 s2 = __builtin_bit_cast(h2, scale_pair(r.ksc[kt], gq));
+            ka[kt][gq][0] = scale_h8(cvt_codes8(r.kr[kt][gq][0], r.kr[kt][gq][1]), s2);
+            ka[kt][gq][1] = scale_h8(cvt_codes8(r.kr[kt][gq][2], r.kr[kt][gq][3]), s2);
+        }
+    }
+    h2 vsp[4];
+    v_scale_pairs<D>(r.vsw, c, vsp);
+    if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+            if (key >= kr.key_end) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
+        }
+    }
+    h8 va[D / 16];
+    v_operands<D>(r.vr, vsp, va, std::make_integer_sequence<int, D / 16>{});
+    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        f4 sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int gq = 0; gq < D / 64; ++gq) {
+                const f4 acc = gq == 0 ? f4{0.f, 0.f, 0.f, 0.f} : sacc[kt];
+                const h8 q0 = *(const NMI_AS3 h8*)(qop + ((nt * (D / 64) + gq) * 2) * 1024 + 16 * lane);
+                const h8 q1 = *(const NMI_AS3 h8*)(qop + ((nt * (D / 64) + gq) * 2 + 1) * 1024 + 16 * lane);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][gq][0], q0, acc, 0, 0, 0);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][gq][1], q1, sacc[kt], 0, 0, 0);
+            }
+        }
+        float p[8];
+        softmax_tile<D>(sacc, nt, c0, masked, s, kr, g, p);
+        h8 pop;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { pop[i] = static_cast<_Float16>(p[i]); }
+#pragma unroll
+        for (int t = 0; t < D / 16; ++t) { s.O[nt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[t], pop, s.O[nt][t], 0, 0, 0); }
+        s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop, s.l[nt], 0, 0, 0);
+    }
+}
+
 // Quantize one new token row of one KV head (one wave: lane owns dim lane + 64 i of group i of K and
 // V; reference contract include/ninfer/ops/gqa_attention.h:25-30) into the cache and into key slot
 // u of the LDS stage `st`, in the layout the chunk DMA produces.
@@ -639,7 +746,8 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
 }
 
 // Merge the four waves' (m, l, O) through LDS (reusing the staging area) and write the
-// workgroup's partial: out_o [32][D] (rows < R) and out_ml [32][2] (log2-domain max, row sum).
+// workgroup's partial: out_o [rows][D] (rows < R) and out_ml [rows][2] (log2-domain max, row sum).
+// Rows go through LDS 32 at a time (two 16-row tiles per batch).
 template <int NT, int D, typename State>
 __device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
                                               float* out_o, float* out_ml) {
@@ -647,60 +755,72 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
     float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
     float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
     float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
+    constexpr int NB = (NT + 1) / 2;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const int r = 16 * nt + c;
-        if (g == 0) {
-            // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
-            sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
-            sm_l[wave * 32 + r] = s.l[nt][0];
-        }
+    for (int jb = 0; jb < NB; ++jb) {
+        if (jb > 0) { __syncthreads(); } // the previous batch's rows have been read
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            // O^T tile t row (4g + e) is dim (D/16)(4g + e) + t: D/16 consecutive dims per (lane, e).
-            float* dst = sm_o + (wave * 32 + r) * kRowStride + (D / 16) * (4 * g + e);
+        for (int u = 0; u < 2; ++u) {
+            const int nt = 2 * jb + u;
+            if (nt >= NT) { continue; }
+            const int r = 16 * u + c; // row within the batch
+            if (g == 0) {
+                // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
+                sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
+                sm_l[wave * 32 + r] = s.l[nt][0];
+            }
 #pragma unroll
-            for (int q4 = 0; q4 < D / 64; ++q4) {
-                *reinterpret_cast<f4*>(dst + 4 * q4) =
-                    f4{s.O[nt][4 * q4][e], s.O[nt][4 * q4 + 1][e], s.O[nt][4 * q4 + 2][e], s.O[nt][4 * q4 + 3][e]};
+            for (int e = 0; e < 4; ++e) {
+                // O^T tile t row (4g + e) is dim (D/16)(4g + e) + t: D/16 consecutive dims per (lane, e).
+                float* dst = sm_o + (wave * 32 + r) * kRowStride + (D / 16) * (4 * g + e);
+#pragma unroll
+                for (int q4 = 0; q4 < D / 64; ++q4) {
+                    *reinterpret_cast<f4*>(dst + 4 * q4) =
+                        f4{s.O[nt][4 * q4][e], s.O[nt][4 * q4 + 1][e], s.O[nt][4 * q4 + 2][e], s.O[nt][4 * q4 + 3][e]};
+                }
             }
         }
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < R * (D / 4); idx += blockDim.x) {
-        const int r = idx / (D / 4);
-        const int d4 = 4 * (idx - r * (D / 4));
-        float M = -INFINITY;
+        __syncthreads();
+        const int rb = 32 * jb;
+        const int rows = min(32, R - rb);
+        for (int idx = threadIdx.x; idx < rows * (D / 4); idx += blockDim.x) {
+            const int r = idx / (D / 4);
+            const int d4 = 4 * (idx - r * (D / 4));
+            float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
-        f4 o = {0.f, 0.f, 0.f, 0.f};
-        float lsum = 0.0f;
-        if (M != -INFINITY) {
+            for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
+            f4 o = {0.f, 0.f, 0.f, 0.f};
+            float lsum = 0.0f;
+            if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const float mw = sm_m[w * 32 + r];
-                if (mw == -INFINITY) { continue; }
-                const float wgt = __builtin_amdgcn_exp2f(mw - M);
-                o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
-                lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
+                for (int w = 0; w < kWaves; ++w) {
+                    const float mw = sm_m[w * 32 + r];
+                    if (mw == -INFINITY) { continue; }
+                    const float wgt = __builtin_amdgcn_exp2f(mw - M);
+                    o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
+                    lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
+                }
             }
-        }
-        __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + r * D + d4)); // read once, by the merge
-        if (d4 == 0) {
-            __builtin_nontemporal_store(M, out_ml + 2 * r);
-            __builtin_nontemporal_store(lsum, out_ml + 2 * r + 1);
+            __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + (rb + r) * D + d4)); // read once, by the merge
+            if (d4 == 0) {
+                __builtin_nontemporal_store(M, out_ml + 2 * (rb + r));
+                __builtin_nontemporal_store(lsum, out_ml + 2 * (rb + r) + 1);
+            }
         }
     }
 }
 
 // D = 128: 78 KB of LDS and at most 256 registers, two workgroups per CU. D = 256: 152 KB of LDS,
 // one workgroup (one wave per SIMD) per CU, which leaves 512 registers per lane for the doubled
-// accumulators and chunk registers.
+// accumulators and chunk registers. NT = 5 (D = 128): 80 query rows (a 16-node tree at group 5)
+// in one workgroup, so every key is streamed once; one wave per SIMD, the Q tile in LDS of its own.
 template <int NT, int D, bool ONCE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1, D == 128 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && NT <= 2 ? 2 : 1, D == 128 && NT <= 2 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
     constexpr int G = D / 64; // quant groups per row
     using GE = Geo<D>;
-    __shared__ __attribute__((aligned(16))) char smem[GE::kSmemBytes];
+    constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
+    static_assert(NT <= 2 || (NT == 5 && D == 128), "row tiles per wave");
+    __shared__ __attribute__((aligned(16))) char smem[NT == 5 ? GE::kSmemBytes + RMAX * 2 * D : GE::kSmemBytes];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -742,7 +862,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
     const int t0 = rc * a.tokens_per_chunk;
     const int Tc = min(a.tokens_per_chunk, a.T - t0);
     const int R = Tc * a.G;
-    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + GE::kNewStage;
+    NMI_AS3 char* qtile = (NMI_AS3 char*)smem + (NT == 5 ? GE::kSmemBytes : GE::kNewStage);
     NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GE::kPosLds);
     const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
     if (wave == 0) {
@@ -792,7 +912,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 #pragma unroll
             for (int hs = 0; hs < 2; ++hs) {
                 const int piece = 8 * gq + 2 * g + hs; // dims 8 * piece .. + 7
-                const i4 v = *(const NMI_AS3 i4*)(qtile + (r & 31) * (2 * D) + 16 * ((piece + r) & (GE::QPIECES - 1)));
+                const i4 v = *(const NMI_AS3 i4*)(qtile + (NT == 5 ? r : (r & 31)) * (2 * D) + 16 * ((piece + r) & (GE::QPIECES - 1)));
                 qraw[nt][gq][hs] = r < R ? v : i4{0, 0, 0, 0};
             }
         }
@@ -850,7 +970,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
 #pragma unroll
         for (int t8 = 0; t8 < D / 16; ++t8) { s.O[nt][t8] = f4{0.f, 0.f, 0.f, 0.f}; }
     }
-
+    if constexpr (NT == 5) {
+        // The five tiles' Q operands (the same in every wave) move to LDS, over the raw Q rows once
+        // every wave has read them, and are read back per tile: 80 fewer registers per lane.
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+                for (int gq = 0; gq < G; ++gq) {
+#pragma unroll
+                    for (int hs = 0; hs < 2; ++hs) { *(NMI_AS3 h8*)(qtile + ((nt * G + gq) * 2 + hs) * 1024 + 16 * lane) = s.q[nt][gq][hs]; }
+                }
+            }
+        }
+        __syncthreads();
+    }
 
     const int window = min(pos_last + 1, a.max_keys);
     const int L = max(0, min(pos_first, window));
@@ -861,13 +996,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
     const int hend = fused ? min(k1, L) : k1;
     const bool owner = fused && L >= k0 && L < k0 + kps && L < window;
     const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
-    float* out_o = a.part_o + pidx * (32 * D);
-    float* out_ml = a.part_ml + pidx * 64;
+    float* out_o = a.part_o + pidx * (RMAX * D);
+    float* out_ml = a.part_ml + pidx * (2 * RMAX);
 
 
     if (k0 >= hend && !owner) {
         __builtin_amdgcn_s_waitcnt(0);
-        if (threadIdx.x < 32) {
+        if (threadIdx.x < RMAX) {
             out_ml[2 * threadIdx.x] = -INFINITY;
             out_ml[2 * threadIdx.x + 1] = 0.0f;
         }
@@ -893,15 +1028,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
             ChunkRegs<D> r;
             read_chunk<D>(ns, r, lane, c, g);
             const KeyRange nk{L, L, min(window, L + a.T)};
-            compute_chunk<NT, D>(r, L, true, s, nk, c, g);
+            if constexpr (NT == 5) {
+                compute_chunk_tiles<NT, D>(r, L, true, s, nk, c, g, qtile);
+            } else {
+                compute_chunk<NT, D>(r, L, true, s, nk, c, g);
+            }
         }
     }
 
     // ---- history chunks, software-pipelined: while chunk j's softmax and PV run, chunk j+1 is
-    // read from LDS and its QK^T issued, and chunks j+2, j+3 are in flight as DMA. D = 256 holds
-    // one chunk in registers at a time (the DMA lookahead stays two chunks).
+    // read from LDS and its QK^T issued, and chunks j+2, j+3 are in flight as DMA. D = 256 and the
+    // five-tile form hold one chunk in registers at a time (the DMA lookahead stays two chunks).
     const KeyRange hk{min(L, k1), L, hend};
-    if constexpr (D == 256) {
+    if constexpr (D == 256 || NT == 5) {
         int stage = 0;
 #pragma unroll 1
         for (int cj = first; cj < hend; cj += kStride) {
@@ -913,7 +1052,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 
                 __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk cj sits in registers: reuse its stage
                 issue_chunk<D, ONCE>(st, hb, dl, cj + 2 * kStride, lane);
             }
-            compute_chunk<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
+            if constexpr (NT == 5) {
+                compute_chunk_tiles<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g, qtile);
+            } else {
+                compute_chunk<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
+            }
             stage ^= 1;
         }
     } else if (first < hend) {
@@ -1435,6 +1578,7 @@ struct MergeArgs {
     const int32_t* seq_table;
     int32_t B;
     int32_t split_slots;
+    int32_t rows_per_slot; // rows of one partial slot (32, or 80 for the 5-tile tree form)
 };
 
 constexpr int kMergeThreads = 256;
@@ -1449,7 +1593,7 @@ constexpr int kMergeMaxSplits = 2048;
 // split's (m, l) are requested before any reduction, so the block waits for memory about once.
 // The partials are written and read with non-temporal hints (each is read exactly once): 15.08 ->
 // 14.87 us per C2 layer on MI355X.
-template <int D>
+template <int D, int RPS>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
     __shared__ float wts[kMergeMaxSplits];
     __shared__ float lw[kMergeMaxSplits];
@@ -1465,8 +1609,9 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
     const int nsplit = a.nsplit; // B == 1 (batches use verify_attn_merge_rows_kernel)
     const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots;
-    const float* ml = a.part_ml + slot0 * 64;
-    const float* po = a.part_o + slot0 * (32 * D);
+    constexpr int rps = RPS; // rows per partial slot (the launch's plan.rows_per_slot)
+    const float* ml = a.part_ml + slot0 * (2 * rps);
+    const float* po = a.part_o + slot0 * (rps * D);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -1477,12 +1622,12 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
 #pragma unroll
     for (int k = 0; k < kMergePre; ++k) {
         const int s = sg + kMergeGroups * k;
-        pre[k] = s < nsplit ? __builtin_nontemporal_load(po + static_cast<int64_t>(s) * 32 * D + r * D + d) : 0.0f;
+        pre[k] = s < nsplit ? __builtin_nontemporal_load(po + static_cast<int64_t>(s) * rps * D + r * D + d) : 0.0f;
     }
     float M = -INFINITY;
     for (int s = tid; s < nsplit; s += kMergeThreads) {
-        const float ls = __builtin_nontemporal_load(ml + s * 64 + 2 * r + 1);
-        const float ms = __builtin_nontemporal_load(ml + s * 64 + 2 * r);
+        const float ls = __builtin_nontemporal_load(ml + s * (2 * rps) + 2 * r + 1);
+        const float ms = __builtin_nontemporal_load(ml + s * (2 * rps) + 2 * r);
         wts[s] = ls > 0.0f ? ms : -INFINITY;
         lw[s] = ls;
         M = fmaxf(M, wts[s]);
@@ -1514,7 +1659,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
         }
 #pragma unroll 4
         for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
-            const float v = __builtin_nontemporal_load(po + static_cast<int64_t>(s) * 32 * D + r * D + d);
+            const float v = __builtin_nontemporal_load(po + static_cast<int64_t>(s) * rps * D + r * D + d);
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
     }
@@ -1555,8 +1700,9 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
     const int first = a.seq_table[2 * b];
     const int nsplit = a.seq_table[2 * b + 1];
     const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + first;
-    const float* ml = a.part_ml + slot0 * 64 + 2 * r;
-    const float* po = a.part_o + slot0 * (32 * D) + r * D + d;
+    const int rps = a.rows_per_slot;
+    const float* ml = a.part_ml + slot0 * (2 * rps) + 2 * r;
+    const float* po = a.part_o + slot0 * (rps * D) + r * D + d;
     float M = -INFINITY;
     float lsum = 0.0f;
     float o = 0.0f;
@@ -1568,8 +1714,8 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int s = s0 + k;
-            mlv[k] = s < nsplit ? *reinterpret_cast<const float2*>(ml + static_cast<int64_t>(s) * 64) : float2{-INFINITY, 0.0f};
-            ov[k] = s < nsplit ? po[static_cast<int64_t>(s) * 32 * D] : 0.0f;
+            mlv[k] = s < nsplit ? *reinterpret_cast<const float2*>(ml + static_cast<int64_t>(s) * (2 * rps)) : float2{-INFINITY, 0.0f};
+            ov[k] = s < nsplit ? po[static_cast<int64_t>(s) * rps * D] : 0.0f;
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
@@ -1672,30 +1818,48 @@ namespace {
 
 // Splits per (sequence, row chunk, KV head) a batch-1 plan aims for: about 512 workgroups at
 // head_dim 128 (two per CU), 256 at head_dim 256 (its LDS map holds one workgroup per CU).
-int64_t wanted_splits(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B) {
+// Rows of one row chunk and the resident workgroups a plan aims at: 32 rows (two 16-row tiles) and
+// two workgroups per CU; the wide form takes up to 80 rows (five tiles) in one chunk and one
+// workgroup per CU.
+struct RowForm {
+    bool wide;
+    int32_t per_chunk; // tokens per row chunk
+    int64_t target;    // resident workgroups
+};
+
+RowForm row_form(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, bool wide_rows) {
     const int32_t G = Hq / Hkv;
-    const int32_t per_chunk = std::min<int32_t>(std::max<int32_t>(1, kAttnRowsPerTile / G), T);
-    const int64_t row_chunks = (T + per_chunk - 1) / per_chunk;
+    const bool wide = wide_rows && D == 128 && static_cast<int64_t>(T) * G > kAttnRowsPerTile &&
+                      static_cast<int64_t>(T) * G <= kAttnWideRows;
+    RowForm f;
+    f.wide = wide;
+    f.per_chunk = wide ? T : std::min<int32_t>(std::max<int32_t>(1, kAttnRowsPerTile / G), T);
+    f.target = (D == 128 && !wide) ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
+    return f;
+}
+
+int64_t wanted_splits(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B, bool wide_rows) {
+    const RowForm f = row_form(Hq, Hkv, D, T, wide_rows);
+    const int64_t row_chunks = (T + f.per_chunk - 1) / f.per_chunk;
     const int64_t units = static_cast<int64_t>(Hkv) * B * row_chunks;
-    const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
-    return std::max<int64_t>(1, (target + units - 1) / units);
+    return std::max<int64_t>(1, (f.target + units - 1) / units);
 }
 
 } // namespace
 
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
-                         uint32_t max_visible_keys) {
+                         uint32_t max_visible_keys, bool wide_rows) {
     SplitPlan p;
+    const RowForm f = row_form(Hq, Hkv, D, T, wide_rows);
     p.G = Hq / Hkv;
-    p.tokens_per_chunk = std::max<int32_t>(1, kAttnRowsPerTile / p.G);
-    p.tokens_per_chunk = std::min(p.tokens_per_chunk, T);
+    p.tokens_per_chunk = f.per_chunk;
     p.row_chunks = (T + p.tokens_per_chunk - 1) / p.tokens_per_chunk;
-    const int64_t target = D == 128 ? kAttnTargetWorkgroups : kAttnTargetWorkgroups / 2;
-    const int64_t want = wanted_splits(Hq, Hkv, D, T, B);
+    p.rows_per_slot = f.wide ? kAttnWideRows : kAttnRowsPerTile;
+    const int64_t want = wanted_splits(Hq, Hkv, D, T, B, wide_rows);
     // B > 1: the device cuts the batch's actual keys into at most split_budget splits per (row
     // chunk, KV head), sized so that every split workgroup is resident at once.
     const int64_t cols = static_cast<int64_t>(Hkv) * p.row_chunks;
-    p.split_budget = static_cast<int32_t>(std::max<int64_t>(1, target / cols));
+    p.split_budget = static_cast<int32_t>(std::max<int64_t>(1, f.target / cols));
     int64_t kps = (static_cast<int64_t>(max_visible_keys) + want - 1) / want;
     kps = ((kps + 127) / 128) * 128;
     kps = std::max<int64_t>(kps, kAttnMinKeysPerSplit);
@@ -1705,9 +1869,9 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     p.split_slots = B == 1 ? p.nsplit : std::max(p.split_budget, B);
     const size_t part_units = static_cast<size_t>(cols) * p.split_slots;
     p.part_o_offset = 0;
-    const size_t o_bytes = part_units * 32 * static_cast<size_t>(D) * sizeof(float);
+    const size_t o_bytes = part_units * p.rows_per_slot * static_cast<size_t>(D) * sizeof(float);
     p.part_ml_offset = (o_bytes + 255) & ~static_cast<size_t>(255);
-    const size_t ml_bytes = part_units * 64 * sizeof(float);
+    const size_t ml_bytes = part_units * 2 * p.rows_per_slot * sizeof(float);
     p.seq_table_offset = (p.part_ml_offset + ml_bytes + 255) & ~static_cast<size_t>(255);
     const size_t table_bytes = static_cast<size_t>(B) * 2 * sizeof(int32_t);
     p.bytes = ((p.seq_table_offset + table_bytes + 255) & ~static_cast<size_t>(255));
@@ -1717,8 +1881,12 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T) {
     // A batch-1 plan never has more than wanted_splits() splits (at least that many keys per split
     // cover any context), and it reaches that count once every split holds the minimum 256 keys.
-    const int64_t want = wanted_splits(Hq, Hkv, D, T, 1);
-    return plan_attention(Hq, Hkv, D, T, 1, static_cast<uint32_t>(want * kAttnMinKeysPerSplit)).bytes;
+    size_t bound = 0;
+    for (const bool wide : {false, true}) {
+        const int64_t want = wanted_splits(Hq, Hkv, D, T, 1, wide);
+        bound = std::max(bound, plan_attention(Hq, Hkv, D, T, 1, static_cast<uint32_t>(want * kAttnMinKeysPerSplit), wide).bytes);
+    }
+    return bound;
 }
 
 void launch_kv_append(const uint16_t* k, const uint16_t* v, const int32_t* positions,
@@ -1749,6 +1917,9 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
                              void* workspace, const SplitPlan& plan, void* out, bool out_f32,
                              hipStream_t stream) {
     if (c.D != 128 && c.D != 256) { throw Unsupported("verify attention: head_dim 128 and 256 are built"); }
+    if (plan.rows_per_slot != kAttnRowsPerTile && (c.kb != nullptr || c.D != 128 || plan.row_chunks != 1)) {
+        throw Unsupported("verify attention: the 80-row form serves INT8 caches of head_dim 128 only");
+    }
     if (plan.split_slots > kMergeMaxSplits) { throw Unsupported("verify attention: too many key splits"); }
     if (k_new != nullptr && (plan.row_chunks > 1 || (c.kb != nullptr && c.D != 128))) {
         // Several row-chunk workgroups read the new rows, or a BF16 cache of head_dim 256 (no room
@@ -1812,7 +1983,9 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
             NMI_PARTIAL(verify_attn_partial_bf16_kernel, 2, 256)
         }
     } else if (c.D == 128) {
-        if (rows <= 16) {
+        if (plan.rows_per_slot == kAttnWideRows) {
+            NMI_PARTIAL(verify_attn_partial_kernel, 5, 128)
+        } else if (rows <= 16) {
             NMI_PARTIAL(verify_attn_partial_kernel, 1, 128)
         } else {
             NMI_PARTIAL(verify_attn_partial_kernel, 2, 128)
@@ -1839,16 +2012,19 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.seq_table = a.seq_table;
     mg.B = c.B;
     mg.split_slots = plan.split_slots;
+    mg.rows_per_slot = plan.rows_per_slot;
     mg.out_f32 = out_f32 ? 1 : 0;
     const dim3 rows_grid((c.B * T * Hq + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock, c.D / kMergeDims);
     if (c.B > 1 && c.D == 128) {
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<128>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
     } else if (c.B > 1) {
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<256>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
+    } else if (c.D == 128 && plan.rows_per_slot == kAttnWideRows) {
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128) {
-        hipLaunchKernelGGL(verify_attn_merge_kernel<128>, dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else {
-        hipLaunchKernelGGL(verify_attn_merge_kernel<256>, dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     }
     check_launch("verify_attn_merge_kernel");
 }
