@@ -166,25 +166,45 @@ __device__ __forceinline__ int splits_of(int w, unsigned kps) {
     return max(1, static_cast<int>((static_cast<unsigned>(w) + kps - 1u) / kps));
 }
 
+// The batch's windows as the split plan reads them: each lane holds the window of sequence `lane`
+// in a register, so the search below repeats no memory load for batches of up to 64 sequences;
+// later rounds of 64 reload theirs.
+struct BatchWindows {
+    const int32_t* positions;
+    int T, B, max_keys;
+    int w0; // window of sequence `lane` (0 past the batch)
+
+    __device__ __forceinline__ int at(int base, int lane) const {
+        if (base == 0) { return w0; }
+        const int i = base + lane;
+        return i < B ? seq_window(positions, T, max_keys, i) : 0;
+    }
+};
+
+__device__ __forceinline__ BatchWindows batch_windows(const int32_t* positions, int T, int B, int max_keys) {
+    const int lane = threadIdx.x & 63;
+    return BatchWindows{positions, T, B, max_keys, lane < B ? seq_window(positions, T, max_keys, lane) : 0};
+}
+
 // sum over the batch of max(1, ceil(W_i / kps)) (whole wave).
-__device__ int batch_split_count(const int32_t* positions, int T, int B, int max_keys, unsigned kps) {
+__device__ int batch_split_count(const BatchWindows& bw, unsigned kps) {
     const int lane = threadIdx.x & 63;
     int n = 0;
-    for (int base = 0; base < B; base += 64) {
-        const int i = base + lane;
-        if (i < B) { n += splits_of(seq_window(positions, T, max_keys, i), kps); }
+    for (int base = 0; base < bw.B; base += 64) {
+        const int w = bw.at(base, lane);
+        if (base + lane < bw.B) { n += splits_of(w, kps); }
     }
     return wave_sum_i(n);
 }
 
 // Keys per split of the batch (whole wave; every lane returns the same).
-__device__ unsigned batch_kps(const int32_t* positions, int T, int B, int max_keys, int budget) {
+__device__ unsigned batch_kps(const BatchWindows& bw, int budget) {
     const int lane = threadIdx.x & 63;
+    const int B = bw.B;
     unsigned long long total = 0;
     int wmax = 0;
     for (int base = 0; base < B; base += 64) {
-        const int i = base + lane;
-        const int w = i < B ? seq_window(positions, T, max_keys, i) : 0;
+        const int w = bw.at(base, lane);
         total += static_cast<unsigned>(w);
         wmax = max(wmax, w);
     }
@@ -205,7 +225,7 @@ __device__ unsigned batch_kps(const int32_t* positions, int T, int B, int max_ke
         hi = hi < lo ? lo : hi;
         while (lo < hi) {
             const unsigned long long mid = lo + ((hi - lo) / 256ull) * 128ull;
-            if (batch_split_count(positions, T, B, max_keys, static_cast<unsigned>(mid)) <= budget) {
+            if (batch_split_count(bw, static_cast<unsigned>(mid)) <= budget) {
                 hi = mid;
             } else {
                 lo = mid + 128ull;
@@ -223,12 +243,14 @@ __device__ unsigned batch_kps(const int32_t* positions, int T, int B, int max_ke
 __device__ SplitRange batch_split_range(const int32_t* positions, int T, int B, int max_keys, int budget, int slot,
                                         int32_t* table) {
     const int lane = threadIdx.x & 63;
-    const unsigned kps = batch_kps(positions, T, B, max_keys, budget);
+    const BatchWindows bw = batch_windows(positions, T, B, max_keys);
+    const unsigned kps = batch_kps(bw, budget);
     SplitRange r{-1, 0, 0, static_cast<int>(kps)};
     int run = 0;
     for (int base = 0; base < B; base += 64) {
         const int i = base + lane;
-        const int n = i < B ? splits_of(seq_window(positions, T, max_keys, i), kps) : 0;
+        const int w = bw.at(base, lane);
+        const int n = i < B ? splits_of(w, kps) : 0;
         const int incl = wave_inclusive_scan(n);
         const int excl = run + incl - n;
         if (table != nullptr && i < B) {
@@ -447,6 +469,21 @@ __device__ __forceinline__ void qk_chunk(const ChunkRegs<D>& r, const RowState<N
     }
 }
 
+// Maximum of a lane's 8 scores over the 4 lanes that share its row (lanes c, c+16, c+32, c+48).
+// IEEE maximum (NaN-propagating) runs as v_maximum3_f32 on gfx950, without the canonicalizing
+// moves fmaxf needs for operands read back from MFMA accumulators; a NaN score makes the row's
+// output NaN under either maximum.
+__device__ __forceinline__ float fmax_ieee(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ __forceinline__ float score_max(const float (&sv)[8]) {
+    float v = fmax_ieee(fmax_ieee(fmax_ieee(sv[0], sv[1]), fmax_ieee(sv[2], sv[3])),
+                        fmax_ieee(fmax_ieee(sv[4], sv[5]), fmax_ieee(sv[6], sv[7])));
+    auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmax_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmax_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Online softmax of one chunk; the S^T accumulator layout is the B-operand layout of P^T. `masked`
 // is uniform across the wave. State is anything with m, rowmul, rowthr, nmask, O[NT][D/16] and
 // l; the probabilities come out as FP32 exp2(score * rowmul - m * rowmul + kPOffset).
@@ -472,8 +509,7 @@ __device__ __forceinline__ void softmax_probs(const f4 (&sacc)[2][NT], int c0, b
                 sv[i] = vis ? sv[i] : -INFINITY;
             }
         }
-        float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-        cmax = group4_max(cmax);
+        const float cmax = score_max(sv);
         const bool need = cmax > s.m[nt] + s.rowthr[nt];
         if (__any(need)) {
             const float mn = need ? cmax : s.m[nt];
@@ -590,6 +626,22 @@ __device__ __forceinline__ void compute_chunk(const ChunkRegs<D>& r, int c0, boo
     pv_chunk<NT, D>(pop, r.vr, r.vsw, c0, masked, s, kr, c, g);
 }
 
+// acc *= alpha on an MFMA accumulator kept in AGPRs: each element is read, multiplied and written
+// back in place. Written with the multiply in VGPRs instead, the compiler homes the five-tile
+// accumulators in VGPRs and copies all of them out of AGPRs at every loop iteration (~180 moves
+// per chunk), although the lazy rescale itself rarely runs.
+__device__ __forceinline__ void scale_acc(f4& acc, float alpha) {
+    float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float t;
+        asm("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+            : "+a"(x[e]), "=&v"(t)
+            : "v"(alpha));
+    }
+    acc = f4{x[0], x[1], x[2], x[3]};
+}
+
 // The five-tile form (80 rows): the chunk's K' and V'^T operands are converted once and the row
 // tiles then run one after another (QK^T, softmax, PV per tile), so only one tile's scores are live.
 // Per row the arithmetic is the one compute_chunk does.
@@ -612,15 +664,14 @@ __device__ __forceinline__ void softmax_tile(const f4 (&sacc)[2], int nt, int c0
             sv[i] = vis ? sv[i] : -INFINITY;
         }
     }
-    float cmax = fmaxf(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])), fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7])));
-    cmax = group4_max(cmax);
+    const float cmax = score_max(sv);
     const bool need = cmax > s.m[nt] + s.rowthr[nt];
     if (__any(need)) {
         const float mn = need ? cmax : s.m[nt];
         const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
 #pragma unroll
-        for (int t = 0; t < D / 16; ++t) { s.O[nt][t] *= alpha; }
-        s.l[nt] *= alpha;
+        for (int t = 0; t < D / 16; ++t) { scale_acc(s.O[nt][t], alpha); }
+        scale_acc(s.l[nt], alpha);
         s.m[nt] = mn;
     }
     const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
