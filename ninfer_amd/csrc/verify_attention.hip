@@ -642,43 +642,6 @@ __device__ __forceinline__ void scale_acc(f4& acc, float alpha) {
     acc = f4{x[0], x[1], x[2], x[3]};
 }
 
-// The five-tile form (80 rows): the chunk's K' and V'^T operands are converted once and the row
-// tiles then run one after another (QK^T, softmax, PV per tile), so only one tile's scores are live.
-// Per row the arithmetic is the one compute_chunk does.
-template <int D, typename State>
-__device__ __forceinline__ void softmax_tile(const f4 (&sacc)[2], int nt, int c0, bool masked, State& s,
-                                             const KeyRange& kr, int g, float (&p)[8]) {
-    float sv[8];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { sv[4 * kt + e] = sacc[kt][e]; }
-    }
-    if (masked) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int key = c0 + 16 * (i >> 2) + 4 * g + (i & 3);
-            const int u = key - kr.new_base;
-            const bool bit = ((s.nmask[nt] >> (u & 31)) & 1u) != 0u;
-            const bool vis = (key < kr.vis_all) | ((key < kr.key_end) & (static_cast<unsigned>(u) < 32u) & bit);
-            sv[i] = vis ? sv[i] : -INFINITY;
-        }
-    }
-    const float cmax = score_max(sv);
-    const bool need = cmax > s.m[nt] + s.rowthr[nt];
-    if (__any(need)) {
-        const float mn = need ? cmax : s.m[nt];
-        const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
-#pragma unroll
-        for (int t = 0; t < D / 16; ++t) { scale_acc(s.O[nt][t], alpha); }
-        scale_acc(s.l[nt], alpha);
-        s.m[nt] = mn;
-    }
-    const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) { p[i] = __builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)); }
-}
-
 template <int TT, int D>
 __device__ __forceinline__ void v_operand(const typename ChunkRegs<D>::VRow (&vr)[8], const h2 (&vsp)[4], h8 (&va)[D / 16]) {
     h2 pr[4];
@@ -693,6 +656,10 @@ __device__ __forceinline__ void v_operands(const typename ChunkRegs<D>::VRow (&v
     (v_operand<TT, D>(vr, vsp, va), ...);
 }
 
+// The five-tile form (80 rows): the chunk's K' and V'^T operands are converted once, and each phase
+// (QK^T, the score maxima, the lazy rescale, the probabilities and PV) runs over all tiles before
+// the next, so the one wave on its SIMD has independent work between dependent steps and a single
+// rescale branch. Per row the arithmetic is the one compute_chunk does.
 template <int NT, int D>
 __device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c0, bool masked, RowState<NT, D>& s,
                                                     const KeyRange& kr, int c, int g, const NMI_AS3 char* qop) {
@@ -707,18 +674,7 @@ __device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c
             ka[kt][gq][1] = scale_h8(cvt_codes8(r.kr[kt][gq][2], r.kr[kt][gq][3]), s2);
         }
     }
-    h2 vsp[4];
-    v_scale_pairs<D>(r.vsw, c, vsp);
-    if (masked) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
-            if (key >= kr.key_end) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
-        }
-    }
-    h8 va[D / 16];
-    v_operands<D>(r.vr, vsp, va, std::make_integer_sequence<int, D / 16>{});
-    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+    float sv[NT][8];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         f4 sacc[2];
@@ -733,11 +689,60 @@ __device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c
                 sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[kt][gq][1], q1, sacc[kt], 0, 0, 0);
             }
         }
-        float p[8];
-        softmax_tile<D>(sacc, nt, c0, masked, s, kr, g, p);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { sv[nt][4 * kt + e] = sacc[kt][e]; }
+        }
+    }
+    h2 vsp[4];
+    v_scale_pairs<D>(r.vsw, c, vsp);
+    if (masked) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
+            if (key >= kr.key_end) { vsp[j >> 1][j & 1] = static_cast<_Float16>(0.0f); }
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int key = c0 + 16 * (i >> 2) + 4 * g + (i & 3);
+                const int u = key - kr.new_base;
+                const bool bit = ((s.nmask[nt] >> (u & 31)) & 1u) != 0u;
+                const bool vis = (key < kr.vis_all) | ((key < kr.key_end) & (static_cast<unsigned>(u) < 32u) & bit);
+                sv[nt][i] = vis ? sv[nt][i] : -INFINITY;
+            }
+        }
+    }
+    h8 va[D / 16];
+    v_operands<D>(r.vr, vsp, va, std::make_integer_sequence<int, D / 16>{});
+    float cmax[NT];
+    bool need_any = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        cmax[nt] = score_max(sv[nt]);
+        need_any |= cmax[nt] > s.m[nt] + s.rowthr[nt];
+    }
+    if (__any(need_any)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const bool need = cmax[nt] > s.m[nt] + s.rowthr[nt];
+            const float mn = need ? cmax[nt] : s.m[nt];
+            const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
+#pragma unroll
+            for (int t = 0; t < D / 16; ++t) { scale_acc(s.O[nt][t], alpha); }
+            scale_acc(s.l[nt], alpha);
+            s.m[nt] = mn;
+        }
+    }
+    const h8 ones = {1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
         h8 pop;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { pop[i] = static_cast<_Float16>(p[i]); }
+        for (int i = 0; i < 8; ++i) { pop[i] = static_cast<_Float16>(__builtin_amdgcn_exp2f(fmaf(sv[nt][i], s.rowmul[nt], bias))); }
 #pragma unroll
         for (int t = 0; t < D / 16; ++t) { s.O[nt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[t], pop, s.O[nt][t], 0, 0, 0); }
         s.l[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pop, s.l[nt], 0, 0, 0);
