@@ -870,36 +870,19 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
 // one workgroup (one wave per SIMD) per CU, which leaves 512 registers per lane for the doubled
 // accumulators and chunk registers. NT = 5 (D = 128): 80 query rows (a 16-node tree at group 5)
 // in one workgroup, so every key is streamed once; one wave per SIMD, the Q tile in LDS of its own.
+// One partial of the INT8 kernel: the keys [k0, kend) of sequence b (k0 a multiple of 128) for
+// this workgroup's KV head and row chunk, into partial slot `slot`.
 template <int NT, int D, bool ONCE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && NT <= 2 ? 2 : 1, D == 128 && NT <= 2 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
+__device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, int b, int k0, int kend, int slot) {
     constexpr int G = D / 64; // quant groups per row
     using GE = Geo<D>;
     constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
-    static_assert(NT <= 2 || (NT == 5 && D == 128), "row tiles per wave");
-    __shared__ __attribute__((aligned(16))) char smem[NT == 5 ? GE::kSmemBytes + RMAX * 2 * D : GE::kSmemBytes];
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
     const int h = blockIdx.y;
     const int rc = blockIdx.z;
-    int b = 0;
-    int split = blockIdx.x;
-    int kps = a.kps;
-    int slot0 = 0;
-    if (a.B > 1) {
-        // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
-        const bool recorder = blockIdx.x == 0 && h == 0 && rc == 0;
-        const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
-                                                recorder ? a.seq_table : nullptr);
-        if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
-        b = sr.b;
-        split = blockIdx.x - sr.first;
-        kps = sr.kps;
-        slot0 = sr.first;
-    }
-    const int k0 = split * kps;
 
     const int64_t head_code = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
     const int64_t head_scale = static_cast<int64_t>(b) * a.scale_seq + static_cast<int64_t>(h) * a.P * G;
@@ -1045,13 +1028,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
 
     const int window = min(pos_last + 1, a.max_keys);
     const int L = max(0, min(pos_first, window));
-    const int k1 = min(k0 + kps, window);
+    const int k1 = min(kend, window);
     const bool fused = a.k_new != nullptr;
     // With the fused append the cache rows >= L are written by this launch: splits stream only the
     // history below L, and the split holding L attends to the new rows from its own registers.
     const int hend = fused ? min(k1, L) : k1;
-    const bool owner = fused && L >= k0 && L < k0 + kps && L < window;
-    const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
+    const bool owner = fused && L >= k0 && L < kend && L < window;
+    const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot;
     float* out_o = a.part_o + pidx * (RMAX * D);
     float* out_ml = a.part_ml + pidx * (2 * RMAX);
 
@@ -1184,6 +1167,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
     __syncthreads();
     static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
     write_partial<NT, D>(s, smem, R, wave, c, g, out_o, out_ml);
+}
+
+template <int NT, int D, bool ONCE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && NT <= 2 ? 2 : 1, D == 128 && NT <= 2 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
+    using GE = Geo<D>;
+    constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
+    static_assert(NT <= 2 || (NT == 5 && D == 128), "row tiles per wave");
+    __shared__ __attribute__((aligned(16))) char smem[NT == 5 ? GE::kSmemBytes + RMAX * 2 * D : GE::kSmemBytes];
+    if (a.B == 1) {
+        const int k0 = blockIdx.x * a.kps;
+        partial_segment<NT, D, ONCE>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
+        return;
+    }
+    // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
+    const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+    const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
+                                            recorder ? a.seq_table : nullptr);
+    if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
+    const int k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
+    partial_segment<NT, D, ONCE>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
 }
 
 

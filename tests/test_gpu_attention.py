@@ -121,8 +121,9 @@ def test_batch_ragged(gpu):
 
 
 def test_batch_one_long_many_short(gpu):
-    """The batch split plan gives the long sequence most of the workgroups and every short (or
-    empty) sequence one split; each sequence's splits merge in order."""
+    """The batch plan gives every workgroup the same number of keys: the long sequence spans most
+    of them, and one workgroup's range holds several short (or empty) sequences, each with a
+    partial of its own; each sequence's partials merge in order."""
     case = AttnCase([60000, 5, 0, 300, 1, 2000, 17, 128, 0, 9, 4000, 33], T=4, seed=22)
     print("case batch B=12 one long", flush=True)
     expected_cache, ref = case.oracle_after_append()
@@ -132,11 +133,25 @@ def test_batch_one_long_many_short(gpu):
 
 
 def test_batch_more_sequences_than_split_budget(gpu):
-    """72 sequences over 8 KV heads exceed the 64 splits per KV head the plan targets: every
-    sequence then gets exactly one split."""
+    """72 sequences over 8 KV heads exceed the 64 workgroups per KV head the plan targets: each
+    workgroup's range then holds several sequences, and sequences 64-71 take the plan's second
+    64-sequence round."""
     rng = np.random.default_rng(23)
     case = AttnCase([int(x) for x in rng.integers(0, 150, size=72)], T=4, seed=23)
     print("case batch B=72", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def test_batch_ragged_past_64_sequences(gpu):
+    """80 ragged contexts, some long: spans that cross the 64-sequence rounds of the batch plan."""
+    rng = np.random.default_rng(24)
+    Ls = [int(x) for x in rng.integers(0, 3000, size=80)]
+    Ls[70] = 20000
+    case = AttnCase(Ls, T=4, seed=24)
+    print("case batch B=80 ragged", flush=True)
     expected_cache, ref = case.oracle_after_append()
     out, cache = gpu_runner.run_attention(case, out_f32=True)
     _check_cache(cache, expected_cache)
