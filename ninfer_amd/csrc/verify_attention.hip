@@ -490,15 +490,20 @@ __device__ __forceinline__ float score_max(const float (&sv)[8]) {
 template <int NT, int D, typename State>
 __device__ __forceinline__ void softmax_probs(const f4 (&sacc)[2][NT], int c0, bool masked, State& s,
                                               const KeyRange& kr, int g, float (&p)[NT][8]) {
+    // Phases over all tiles (scores, maxima, one rescale branch, probabilities), so the tiles'
+    // dependent steps interleave.
+    float sv[NT][8];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        float sv[8];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { sv[4 * kt + e] = sacc[kt][nt][e]; }
+            for (int e = 0; e < 4; ++e) { sv[nt][4 * kt + e] = sacc[kt][nt][e]; }
         }
-        if (masked) {
+    }
+    if (masked) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 // Branch-free: bitwise operators, and a shift count that is always in range.
@@ -506,22 +511,34 @@ __device__ __forceinline__ void softmax_probs(const f4 (&sacc)[2][NT], int c0, b
                 const int u = key - kr.new_base;
                 const bool bit = ((s.nmask[nt] >> (u & 31)) & 1u) != 0u;
                 const bool vis = (key < kr.vis_all) | ((key < kr.key_end) & (static_cast<unsigned>(u) < 32u) & bit);
-                sv[i] = vis ? sv[i] : -INFINITY;
+                sv[nt][i] = vis ? sv[nt][i] : -INFINITY;
             }
         }
-        const float cmax = score_max(sv);
-        const bool need = cmax > s.m[nt] + s.rowthr[nt];
-        if (__any(need)) {
-            const float mn = need ? cmax : s.m[nt];
+    }
+    float cmax[NT];
+    bool need_any = false;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        cmax[nt] = score_max(sv[nt]);
+        need_any |= cmax[nt] > s.m[nt] + s.rowthr[nt];
+    }
+    if (__any(need_any)) {
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const bool need = cmax[nt] > s.m[nt] + s.rowthr[nt];
+            const float mn = need ? cmax[nt] : s.m[nt];
             const float alpha = need ? __builtin_amdgcn_exp2f((s.m[nt] - mn) * s.rowmul[nt]) : 1.0f;
 #pragma unroll
             for (int t = 0; t < D / 16; ++t) { s.O[nt][t] *= alpha; }
             s.l[nt] *= alpha;
             s.m[nt] = mn;
         }
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
         const float bias = s.m[nt] == -INFINITY ? 0.0f : fmaf(-s.m[nt], s.rowmul[nt], kPOffset);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) { p[nt][i] = __builtin_amdgcn_exp2f(fmaf(sv[i], s.rowmul[nt], bias)); }
+        for (int i = 0; i < 8; ++i) { p[nt][i] = __builtin_amdgcn_exp2f(fmaf(sv[nt][i], s.rowmul[nt], bias)); }
     }
 }
 
