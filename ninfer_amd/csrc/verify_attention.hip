@@ -677,8 +677,8 @@ __device__ __forceinline__ void v_operands(const typename ChunkRegs<D>::VRow (&v
 // (QK^T, the score maxima, the lazy rescale, the probabilities and PV) runs over all tiles before
 // the next, so the one wave on its SIMD has independent work between dependent steps and a single
 // rescale branch. Per row the arithmetic is the one compute_chunk does.
-template <int NT, int D>
-__device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c0, bool masked, RowState<NT, D>& s,
+template <int NT, int D, bool MASKED>
+__device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c0, RowState<NT, D>& s,
                                                     const KeyRange& kr, int c, int g, const NMI_AS3 char* qop) {
     const int lane = threadIdx.x & 63;
     h8 ka[2][D / 64][2];
@@ -714,7 +714,7 @@ __device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c
     }
     h2 vsp[4];
     v_scale_pairs<D>(r.vsw, c, vsp);
-    if (masked) {
+    if constexpr (MASKED) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int key = c0 + (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4));
@@ -1085,7 +1085,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
             read_chunk<D>(ns, r, lane, c, g);
             const KeyRange nk{L, L, min(window, L + a.T)};
             if constexpr (NT == 5) {
-                compute_chunk_tiles<NT, D>(r, L, true, s, nk, c, g, qtile);
+                compute_chunk_tiles<NT, D, true>(r, L, s, nk, c, g, qtile);
             } else {
                 compute_chunk<NT, D>(r, L, true, s, nk, c, g);
             }
@@ -1109,7 +1109,13 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
                 issue_chunk<D, ONCE>(st, hb, dl, cj + 2 * kStride, lane);
             }
             if constexpr (NT == 5) {
-                compute_chunk_tiles<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g, qtile);
+                // The masked and unmasked forms are separate code paths: one merged path would
+                // carry the scores through AGPRs across the mask (40 more moves per chunk).
+                if (cj + kChunk > hk.vis_all) {
+                    compute_chunk_tiles<NT, D, true>(r, cj, s, hk, c, g, qtile);
+                } else {
+                    compute_chunk_tiles<NT, D, false>(r, cj, s, hk, c, g, qtile);
+                }
             } else {
                 compute_chunk<NT, D>(r, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
             }
@@ -1192,18 +1198,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
     constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
     static_assert(NT <= 2 || (NT == 5 && D == 128), "row tiles per wave");
     __shared__ __attribute__((aligned(16))) char smem[NT == 5 ? GE::kSmemBytes + RMAX * 2 * D : GE::kSmemBytes];
-    if (a.B == 1) {
-        const int k0 = blockIdx.x * a.kps;
-        partial_segment<NT, D, ONCE>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
-        return;
+    // B = 1 (up to two row tiles) has a code path of its own, in which the sequence and slot are
+    // compile-time facts (measured on MI355X: C2 13.9 -> 13.5 us per layer). The five-tile form
+    // keeps one path: a second copy raises its register pressure into spills.
+    if constexpr (NT <= 2) {
+        if (a.B == 1) {
+            const int k0 = blockIdx.x * a.kps;
+            partial_segment<NT, D, ONCE>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
+            return;
+        }
+        // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
+        const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+        const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
+                                                recorder ? a.seq_table : nullptr);
+        if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
+        const int k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
+        partial_segment<NT, D, ONCE>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
+    } else {
+        int b = 0;
+        int k0 = blockIdx.x * a.kps;
+        int kend = k0 + a.kps;
+        if (a.B > 1) {
+            const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+            const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
+                                                    recorder ? a.seq_table : nullptr);
+            if (sr.b < 0) { return; }
+            b = sr.b;
+            k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
+            kend = k0 + sr.kps;
+        }
+        partial_segment<NT, D, ONCE>(a, smem, b, k0, kend, blockIdx.x);
     }
-    // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
-    const bool recorder = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
-    const SplitRange sr = batch_split_range(a.positions, a.T, a.B, a.max_keys, a.split_budget, blockIdx.x,
-                                            recorder ? a.seq_table : nullptr);
-    if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
-    const int k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
-    partial_segment<NT, D, ONCE>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
 }
 
 
