@@ -48,7 +48,11 @@ class AttnCase:
     as BF16 when kv="bf16"), T new K/V columns, BF16 Q, positions L..L+T-1 per sequence."""
 
     def __init__(self, Ls, T=4, Hq=40, Hkv=8, D=128, seed=0, outliers=False, parents=None,
-                 max_context=None, qstd=1.0, kv="i8", dist="normal", gen="splitmix"):
+                 max_context=None, qstd=1.0, kv="i8", dist="normal", gen="splitmix", k_boost=0.0):
+        """k_boost > 0 multiplies the history key rows in the last quarter of every 512-position
+        window by k_boost: a split that starts in the plain rows meets scores several log2 units
+        above its running maximum in mid-stream, so its lazy rescale acts on non-zero
+        accumulators, with scores of moderate size."""
         self.Ls = list(Ls)
         self.B = len(self.Ls)
         self.T, self.Hq, self.Hkv, self.D = T, Hq, Hkv, D
@@ -91,6 +95,10 @@ class AttnCase:
                 if L > 0:
                     hk = gen_k(syn.derive_seed(seed, 1, b), D * Hkv * L)
                     hv = gen_v(syn.derive_seed(seed, 2, b), D * Hkv * L)
+                    if k_boost > 0.0:
+                        boost = np.where(np.arange(L) % 512 >= 384, k_boost, 1.0).astype(np.float32)
+                        kf = syn.bf16_bits_to_f32(hk).reshape(L, Hkv * D) * boost[:, None]
+                        hk = syn.f32_to_bf16_bits(kf.reshape(-1))
                     pos = np.arange(L, dtype=np.int32)
                     kcb, vcb, ksb, vsb = self.kc[b], self.vc[b], self.ks[b], self.vs[b]
                     pyoracle.kv_append(hk, hv, pos, L, 1, Hkv, D, P, kcb, vcb, ksb, vsb)

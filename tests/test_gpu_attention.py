@@ -185,6 +185,41 @@ def test_tree_attention(gpu):
     _check_out(out, ref, REL_L2_F32)
 
 
+def test_rising_scores_a1(gpu):
+    """Boosted key rows late in 512-position windows: splits' running maxima rise past the lazy
+    threshold in mid-stream, so the two-tile path rescales non-zero accumulators."""
+    case = AttnCase([40000], T=4, seed=34, k_boost=4.0, gen="pcg")
+    print("case rising scores A1 40000", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+@pytest.mark.parametrize("Ls", [[40000], [9000, 30000]])
+def test_rising_scores_tree(gpu, Ls):
+    """The same mid-stream rises through the five-tile (80-row) tree form, whose lazy rescale works
+    on the accumulators in place in AGPRs; batch 1 and a batch of two."""
+    parents = np.array([_bfs_tree(16)] * len(Ls), dtype=np.int32).reshape(-1)
+    case = AttnCase(Ls, T=16, seed=35 + len(Ls), parents=parents, k_boost=4.0, gen="pcg")
+    print(f"case rising scores tree {Ls}", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, mode="TREE")
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+def test_tree_attention_outliers(gpu):
+    """Five-tile tree form under the long-context statistics (1% of K/V entries at +-20)."""
+    parents = np.array([_bfs_tree(16), _bfs_tree(16)], dtype=np.int32).reshape(-1)
+    case = AttnCase([3000, 9000], T=16, seed=33, parents=parents, outliers=True)
+    print("case tree outliers", flush=True)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, mode="TREE")
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
 def test_chain_tree_equals_causal(gpu):
     T = 6
     parents = np.array([-1] + list(range(T - 1)), dtype=np.int32)
