@@ -980,6 +980,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
 
     // ---- Q operand (B operand of S^T = K' Q^T) from the raw rows.
     RowState<NT, D> s;
+    const float thr_unit = kLazyTau / a.scale_log2; // the lazy threshold of a row whose factor is 1
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int r = 16 * nt + c;
@@ -1005,11 +1006,11 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
         // factor = 2^(14 - floor(log2(amax))) puts max|q| in [2^14, 2^15): FP16 holds every BF16
         // value of the row exactly down to 2^-28 of its maximum. The exponent is clamped so the
         // factor and the lazy threshold stay finite for rows of tiny values.
-        float factor = 1.0f;
+        int fexp = 0; // factor = 2^fexp
         if (amax > 0.0f && amax < INFINITY) {
-            const int ex = max(static_cast<int>((__float_as_uint(amax) >> 23) & 0xff) - 127, -100);
-            factor = ldexpf(1.0f, 14 - ex);
+            fexp = 14 - max(static_cast<int>((__float_as_uint(amax) >> 23) & 0xff) - 127, -100);
         }
+        const float factor = ldexpf(1.0f, fexp);
 #pragma unroll
         for (int gq = 0; gq < G; ++gq) {
 #pragma unroll
@@ -1018,8 +1019,10 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
                 for (int e = 0; e < 8; ++e) { s.q[nt][gq][hs][e] = static_cast<_Float16>(x[gq][hs][e] * factor); }
             }
         }
-        s.rowmul[nt] = a.scale_log2 / factor;
-        s.rowthr[nt] = kLazyTau / s.rowmul[nt];
+        // scale_log2 / factor and kLazyTau / rowmul, as exact power-of-two scalings (no divides on
+        // the path to the first chunk).
+        s.rowmul[nt] = ldexpf(a.scale_log2, -fexp);
+        s.rowthr[nt] = ldexpf(thr_unit, fexp);
         s.nmask[nt] = valid ? new_key_mask(par, t) : 0u;
         s.m[nt] = -INFINITY;
         s.l[nt] = f4{0.f, 0.f, 0.f, 0.f};
