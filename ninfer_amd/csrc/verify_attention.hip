@@ -742,6 +742,9 @@ __device__ __forceinline__ void compute_chunk_tiles(const ChunkRegs<D>& r, int c
         need_any |= cmax[nt] > s.m[nt] + s.rowthr[nt];
     }
     if (__any(need_any)) {
+        // scale_acc reads accumulators that MFMAs wrote: 16 wait states of margin for the MFMA
+        // write -> VALU read hazard, whatever the compiler placed before this rare block.
+        asm volatile("s_nop 7\n\ts_nop 7");
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const bool need = cmax[nt] > s.m[nt] + s.rowthr[nt];
