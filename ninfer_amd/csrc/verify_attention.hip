@@ -74,6 +74,7 @@ static_assert(Geo<128>::kStageBytes == 8704 && Geo<128>::kSmemBytes == 78464, "D
 // exceeds it by more than 2^7, so P <= 2^15 stays inside FP16 and most chunks skip the rescale.
 constexpr float kPOffset = 8.0f;
 constexpr float kLazyTau = 7.0f;
+constexpr int kQOutOfRange = 0x40000000; // a Q DMA offset past every Q buffer: the DMA writes zeros
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt[3:0] + vmcnt[15:14], expcnt[6:4], lgkmcnt[11:8]).
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
@@ -929,18 +930,21 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
         if (lane < a.T) { __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)(pos + lane), (NMI_AS3 void*)pos_lds, 4, 0, 0); }
         constexpr int QP = GE::QPIECES;  // 16-byte pieces of a Q row
         constexpr int RPD = 64 / QP;     // Q rows per 1 KB DMA
-#pragma unroll 1
-        for (int k = 0; RPD * k < R; ++k) {
+        // All 16 * NT rows the tiles read: rows past R take an offset past the buffer and land as
+        // zeros, so the tiles need no masking of their Q operands.
+        const __amdgpu_buffer_rsrc_t qr =
+            raw_buffer(a.q + static_cast<int64_t>(D) * (h * a.G + static_cast<int64_t>(a.Hq) * a.T * b),
+                       static_cast<int64_t>(a.T) * a.Hq * D * 2);
+#pragma unroll
+        for (int k = 0; RPD * k < 16 * NT; ++k) {
             const int row = RPD * k + lane / QP;
-            if (row < R) {
-                const int tl = row / a.G;
-                const int gi = row - tl * a.G;
-                // Slot (lane % QP) of the row holds piece (slot - row) % QP: rows rotate across the
-                // LDS banks, so the 16 lanes that read one column of rows do not conflict.
-                const int piece = ((lane % QP) - row) & (QP - 1);
-                const uint16_t* src = a.q + static_cast<int64_t>(D) * (h * a.G + gi + static_cast<int64_t>(a.Hq) * (t0 + tl + static_cast<int64_t>(a.T) * b)) + 8 * piece;
-                __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)src, (NMI_AS3 void*)(qtile + k * 1024), 16, 0, 0);
-            }
+            const int tl = row / a.G;
+            const int gi = row - tl * a.G;
+            // Slot (lane % QP) of the row holds piece (slot - row) % QP: rows rotate across the LDS
+            // banks, so the 16 lanes that read one column of rows do not conflict.
+            const int piece = ((lane % QP) - row) & (QP - 1);
+            const int off = row < R ? 2 * (D * (gi + a.Hq * (t0 + tl)) + 8 * piece) : kQOutOfRange;
+            dma16(qr, qtile + k * 1024, off, 0);
         }
     }
 
@@ -972,7 +976,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
             for (int hs = 0; hs < 2; ++hs) {
                 const int piece = 8 * gq + 2 * g + hs; // dims 8 * piece .. + 7
                 const i4 v = *(const NMI_AS3 i4*)(qtile + (NT == 5 ? r : (r & 31)) * (2 * D) + 16 * ((piece + r) & (GE::QPIECES - 1)));
-                qraw[nt][gq][hs] = r < R ? v : i4{0, 0, 0, 0};
+                qraw[nt][gq][hs] = v;
             }
         }
     }
