@@ -147,8 +147,20 @@ class Layer:
                           self.out.tensor(), stream)
 
 
+PREWARM_S = 0.3  # seconds of untimed replays before the counted warm-up steps of every timed graph
+
+
 def time_graph(graph, stream, reps, warmup):
+    """Median (and p95) time of one replay of `graph` over `reps` timed replays. Before the `warmup`
+    counted warm-up replays, the graph is replayed untimed for PREWARM_S seconds: the host-side setup
+    of each section (cache generation, weight upload) leaves the GPU idle, and its clocks take tens
+    of milliseconds to come back. Measured on MI355X: C3 timed after 3 warm-up replays 103-106 us per
+    layer, with the first replays at 107-122 us; after 0.5 s of replays 99.4-100.1 us."""
     from ninfer_amd.device import Event
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < PREWARM_S:
+        graph.launch()
+        stream.synchronize()
     for _ in range(warmup):
         graph.launch()
     stream.synchronize()
