@@ -32,6 +32,7 @@ struct SplitPlan {
     int32_t split_slots = 0;      // partial slots per (row chunk, KV head)
     int32_t split_budget = 0;     // B > 1: most splits per (row chunk, KV head) the device cuts the batch into
     int32_t rows_per_slot = 32;   // query rows of one partial slot: 32, or 80 (one row chunk of 5 MFMA tiles)
+    bool cached_partials = false; // partials written and read through the caches (long B = 1 splits)
     size_t part_o_offset = 0;
     size_t part_ml_offset = 0;
     size_t seq_table_offset = 0; // B > 1: per sequence (first slot, split count)
@@ -43,6 +44,11 @@ inline constexpr int32_t kAttnWideRows = 80;          // INT8, head_dim 128: up 
 inline constexpr int32_t kAttnTargetWorkgroups = 512; // 2 per CU on 256 CUs
 inline constexpr int32_t kAttnMinKeysPerSplit = 256;
 inline constexpr int32_t kAttnMaxTokens = 32;
+// B = 1 splits of at least this many keys write their partials with ordinary (cached) stores and the
+// merge reads them with ordinary loads; shorter splits use the non-temporal forms. Measured on
+// MI355X: C3 (4,096-key splits) 99.3-99.5 -> 98.2-98.3 us per layer; C2 (256-key splits) 13.32-13.35
+// us with non-temporal partials against 13.52-13.54 us cached.
+inline constexpr int32_t kAttnCachedPartialKeys = 1024;
 
 // wide_rows: the INT8 head_dim-128 cache may serve 33..80 query rows (T x G) in one row chunk of
 // five 16-row tiles (one workgroup per CU) instead of several 32-row chunks that each stream every key.

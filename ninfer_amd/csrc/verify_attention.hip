@@ -825,7 +825,7 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
 // Merge the four waves' (m, l, O) through LDS (reusing the staging area) and write the
 // workgroup's partial: out_o [rows][D] (rows < R) and out_ml [rows][2] (log2-domain max, row sum).
 // Rows go through LDS 32 at a time (two 16-row tiles per batch).
-template <int NT, int D, typename State>
+template <int NT, int D, bool CACHED, typename State>
 __device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
                                               float* out_o, float* out_ml) {
     constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
@@ -878,10 +878,20 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
                     lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
                 }
             }
-            __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + (rb + r) * D + d4)); // read once, by the merge
-            if (d4 == 0) {
-                __builtin_nontemporal_store(M, out_ml + 2 * (rb + r));
-                __builtin_nontemporal_store(lsum, out_ml + 2 * (rb + r) + 1);
+            // Read once, by the merge: non-temporal unless the plan routes long splits' partials
+            // through the caches.
+            if constexpr (CACHED) {
+                *reinterpret_cast<f4*>(out_o + (rb + r) * D + d4) = o;
+                if (d4 == 0) {
+                    out_ml[2 * (rb + r)] = M;
+                    out_ml[2 * (rb + r) + 1] = lsum;
+                }
+            } else {
+                __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + (rb + r) * D + d4));
+                if (d4 == 0) {
+                    __builtin_nontemporal_store(M, out_ml + 2 * (rb + r));
+                    __builtin_nontemporal_store(lsum, out_ml + 2 * (rb + r) + 1);
+                }
             }
         }
     }
@@ -893,7 +903,7 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
 // in one workgroup, so every key is streamed once; one wave per SIMD, the Q tile in LDS of its own.
 // One partial of the INT8 kernel: the keys [k0, kend) of sequence b (k0 a multiple of 128) for
 // this workgroup's KV head and row chunk, into partial slot `slot`.
-template <int NT, int D, bool ONCE>
+template <int NT, int D, bool ONCE, bool CACHED>
 __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, int b, int k0, int kend, int slot) {
     constexpr int G = D / 64; // quant groups per row
     using GE = Geo<D>;
@@ -1199,10 +1209,12 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
     __syncthreads();
     static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
-    write_partial<NT, D>(s, smem, R, wave, c, g, out_o, out_ml);
+    write_partial<NT, D, CACHED>(s, smem, R, wave, c, g, out_o, out_ml);
 }
 
-template <int NT, int D, bool ONCE>
+// CACHED: the batch-1 partials go out with ordinary (cached) stores; an instance of its own, launched
+// only for the plans that ask for it (kAttnCachedPartialKeys).
+template <int NT, int D, bool ONCE, bool CACHED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && NT <= 2 ? 2 : 1, D == 128 && NT <= 2 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
     using GE = Geo<D>;
     constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
@@ -1214,7 +1226,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
     if constexpr (NT <= 2) {
         if (a.B == 1) {
             const int k0 = blockIdx.x * a.kps;
-            partial_segment<NT, D, ONCE>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
+            partial_segment<NT, D, ONCE, CACHED>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
             return;
         }
         // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
@@ -1223,7 +1235,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
                                                 recorder ? a.seq_table : nullptr);
         if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
         const int k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
-        partial_segment<NT, D, ONCE>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
+        partial_segment<NT, D, ONCE, false>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
     } else {
         int b = 0;
         int k0 = blockIdx.x * a.kps;
@@ -1237,7 +1249,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
             k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
             kend = k0 + sr.kps;
         }
-        partial_segment<NT, D, ONCE>(a, smem, b, k0, kend, blockIdx.x);
+        partial_segment<NT, D, ONCE, false>(a, smem, b, k0, kend, blockIdx.x);
     }
 }
 
@@ -1671,7 +1683,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GB::kSmemBytes, "wave merge exceeds the LDS map");
-    write_partial<NT, D>(s, smem, R, wave, c, g, out_o, out_ml);
+    write_partial<NT, D, false>(s, smem, R, wave, c, g, out_o, out_ml);
 }
 
 struct MergeArgs {
@@ -1704,8 +1716,10 @@ constexpr int kMergeMaxSplits = 2048;
 // split's (m, l) are requested before any reduction, so the block waits for memory about once.
 // The partials are written and read with non-temporal hints (each is read exactly once): 15.08 ->
 // 14.87 us per C2 layer on MI355X.
-template <int D, int RPS>
+template <int D, int RPS, bool CACHED>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
+    // Partials written through the caches are read with ordinary loads, others non-temporally.
+    const auto ld = [](const float* p) { return CACHED ? *p : __builtin_nontemporal_load(p); };
     __shared__ float wts[kMergeMaxSplits];
     __shared__ float lw[kMergeMaxSplits];
     __shared__ float red[kMergeThreads / 64];
@@ -1733,12 +1747,12 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
 #pragma unroll
     for (int k = 0; k < kMergePre; ++k) {
         const int s = sg + kMergeGroups * k;
-        pre[k] = s < nsplit ? __builtin_nontemporal_load(po + static_cast<int64_t>(s) * rps * D + r * D + d) : 0.0f;
+        pre[k] = s < nsplit ? ld(po + static_cast<int64_t>(s) * rps * D + r * D + d) : 0.0f;
     }
     float M = -INFINITY;
     for (int s = tid; s < nsplit; s += kMergeThreads) {
-        const float ls = __builtin_nontemporal_load(ml + s * (2 * rps) + 2 * r + 1);
-        const float ms = __builtin_nontemporal_load(ml + s * (2 * rps) + 2 * r);
+        const float ls = ld(ml + s * (2 * rps) + 2 * r + 1);
+        const float ms = ld(ml + s * (2 * rps) + 2 * r);
         wts[s] = ls > 0.0f ? ms : -INFINITY;
         lw[s] = ls;
         M = fmaxf(M, wts[s]);
@@ -1770,7 +1784,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
         }
 #pragma unroll 4
         for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
-            const float v = __builtin_nontemporal_load(po + static_cast<int64_t>(s) * rps * D + r * D + d);
+            const float v = ld(po + static_cast<int64_t>(s) * rps * D + r * D + d);
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
     }
@@ -1978,6 +1992,9 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     p.nsplit = static_cast<int32_t>((static_cast<int64_t>(max_visible_keys) + kps - 1) / kps);
     p.nsplit = std::max(p.nsplit, 1);
     p.split_slots = B == 1 ? p.nsplit : std::max(p.split_budget, B);
+    // INT8 caches (the only ones offered the wide form) at head_dim 128 with one row chunk.
+    p.cached_partials = B == 1 && wide_rows && D == 128 && !f.wide && p.row_chunks == 1 &&
+                        p.keys_per_split >= kAttnCachedPartialKeys;
     const size_t part_units = static_cast<size_t>(cols) * p.split_slots;
     p.part_o_offset = 0;
     const size_t o_bytes = part_units * p.rows_per_slot * static_cast<size_t>(D) * sizeof(float);
@@ -2096,6 +2113,10 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     } else if (c.D == 128) {
         if (plan.rows_per_slot == kAttnWideRows) {
             NMI_PARTIAL(verify_attn_partial_kernel, 5, 128)
+        } else if (plan.cached_partials && rows <= 16) {
+            hipLaunchKernelGGL((verify_attn_partial_kernel<1, 128, true, true>), grid, dim3(256), 0, stream, a);
+        } else if (plan.cached_partials) {
+            hipLaunchKernelGGL((verify_attn_partial_kernel<2, 128, true, true>), grid, dim3(256), 0, stream, a);
         } else if (rows <= 16) {
             NMI_PARTIAL(verify_attn_partial_kernel, 1, 128)
         } else {
@@ -2131,11 +2152,15 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     } else if (c.B > 1) {
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<256>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128 && plan.rows_per_slot == kAttnWideRows) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows, false>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    } else if (c.D == 128 && plan.cached_partials) {
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile, false>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    } else if (plan.cached_partials) {
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile, false>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     }
     check_launch("verify_attn_merge_kernel");
 }
