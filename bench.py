@@ -101,7 +101,7 @@ class Layer:
         if copy_from is not None:
             # Same history as another layer, in planes of its own (a device-to-device copy).
             for dst, src in zip(self.cache._planes(), copy_from.cache._planes()):
-                device.memcpy_dtod(dst.buf, src.buf, dst.nbytes)
+                device.copy_array(dst, src)
             synchronize()
         elif kv_bf16:
             # History K/V stored as BF16: a generated block of N(0,1) values (optionally 1% outliers
@@ -328,7 +328,7 @@ def c4_bench(stream, args) -> dict:
     for _ in range(C4_LAYERS - 1):  # the same contents in planes of their own
         c = KVCacheLayer(max_ctx, HKV, D, B)
         for dst, src in zip(c._planes(), cache._planes()):
-            dv.memcpy_dtod(dst.buf, src.buf, src.nbytes)
+            dv.copy_array(dst, src)
         layers.append(c)
     dv.synchronize()
     q = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.standard_normal(D * HQ * T * B, dtype=np.float32)), (D, HQ, T, B))

@@ -182,6 +182,13 @@ def synchronize() -> None:
     check(lib().nmi_rt_device_synchronize())
 
 
+def copy_array(dst: "DeviceArray", src: "DeviceArray", stream: Stream | None = None) -> None:
+    """Stream-ordered copy of src's bytes into dst (same byte size; either may live in an arena)."""
+    assert dst.nbytes == src.nbytes
+    check(lib().nmi_rt_memcpy_dtod(C.c_void_p(dst.ptr), C.c_void_p(src.ptr), dst.nbytes,
+                                   stream.handle if stream else None))
+
+
 def memcpy_dtod(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int, stream: Stream | None = None) -> None:
     """Stream-ordered device-to-device copy of `nbytes` (hipMemcpyAsync)."""
     assert nbytes <= dst.nbytes and nbytes <= src.nbytes
