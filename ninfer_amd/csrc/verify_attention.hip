@@ -235,6 +235,7 @@ __device__ unsigned batch_kps(const BatchWindows& bw, int budget) {
         kps = lo;
     }
     kps = kps < kAttnMinKeysPerSplit ? kAttnMinKeysPerSplit : kps;
+    kps = (kps >= 1024 && (kps & (kps - 1)) == 0) ? kps + 128 : kps; // as the host plan: no power-of-two stride
     kps = kps > 0x7FFFFF80ull ? 0x7FFFFF80ull : kps;
     return static_cast<unsigned>(kps);
 }
@@ -1953,6 +1954,13 @@ struct RowForm {
     int64_t target;    // resident workgroups
 };
 
+// Split lengths of 1,024 keys or more that are powers of two get one more 128-key step: the
+// workgroups of a launch stream at one split-length stride from each other, and a power-of-two
+// stride in a physically contiguous plane lands their concurrent reads on the same memory channels.
+// Measured on MI355X at C3 (4,096 -> 4,224 keys): the layers whose planes were placed contiguously
+// ran at 110-125 us against 97-100 us for the others; with 4,224 keys all eight take 97-100 us.
+int64_t off_power_of_two(int64_t kps) { return (kps >= 1024 && (kps & (kps - 1)) == 0) ? kps + 128 : kps; }
+
 RowForm row_form(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, bool wide_rows) {
     const int32_t G = Hq / Hkv;
     const bool wide = wide_rows && D == 128 && static_cast<int64_t>(T) * G > kAttnRowsPerTile &&
@@ -1989,6 +1997,7 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     int64_t kps = (static_cast<int64_t>(max_visible_keys) + want - 1) / want;
     kps = ((kps + 127) / 128) * 128;
     kps = std::max<int64_t>(kps, kAttnMinKeysPerSplit);
+    kps = off_power_of_two(kps);
     p.keys_per_split = static_cast<int32_t>(kps);
     p.nsplit = static_cast<int32_t>((static_cast<int64_t>(max_visible_keys) + kps - 1) / kps);
     p.nsplit = std::max(p.nsplit, 1);
