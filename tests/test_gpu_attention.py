@@ -65,6 +65,18 @@ def test_outliers_long(gpu):
     _check_out(out, ref, REL_L2_F32)
 
 
+@pytest.mark.parametrize("L", [60000, 130000])
+def test_power_of_two_split_lengths_moved(gpu, L):
+    """Batch-1 contexts whose split plan rounds to 1,024 and 2,048 keys per split: the plan moves
+    such lengths one 128-key step up (fewer splits, cached partials), and every key stays covered."""
+    print(f"case pow2 split L={L}", flush=True)
+    case = AttnCase([L], T=4, seed=77 + L)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True)
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
 def test_a2_then_a3_equals_a1(gpu):
     """A2 then A3 against A1: identical cache bytes, and outputs within the reference's A1/A3 parity
     criterion (attention_bf16 composite, tests/ops/test_gqa_attention.cpp:1077-1078). A1 attends to
