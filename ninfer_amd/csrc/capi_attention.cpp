@@ -80,6 +80,11 @@ CacheRef validate_cache(const nmi_kv_layer_view* cache, int32_t kv_heads, int32_
     if (cache->dtype == NMI_BF16) {
         require(cache->k_scale.data == nullptr && cache->v_scale.data == nullptr, op,
                 "BF16 KV cache must not have scales");
+        // Every BF16-cache kernel (the prefix commit, A2, and A1's in-kernel copy of the new rows)
+        // stores 16-byte pieces of rows (reference require_vector_aligned on the cache planes,
+        // src/ops/wrapper/kv_cache_append_prefix.cpp:77-79,98-100).
+        require((reinterpret_cast<uintptr_t>(cache->k.data) & 15u) == 0, op, "cache k must be 16-byte aligned");
+        require((reinterpret_cast<uintptr_t>(cache->v.data) & 15u) == 0, op, "cache v must be 16-byte aligned");
         r.kb = static_cast<uint16_t*>(cache->k.data);
         r.vb = static_cast<uint16_t*>(cache->v.data);
         return r;

@@ -147,6 +147,10 @@ int nmi_speculative_accept_fused_head(const nmi_tensor* x, const nmi_weight* w, 
         const int32_t K = s.K;
         require(x != nullptr && x->ne[1] == K + 1 && x->ne[2] == B && x->ne[3] == 1,
                 "x must be [hidden, K+1, B] (the verify columns of every sequence)");
+        // The kernel reads (K+1) * B packed columns, so x itself must be packed (a view of the first
+        // K+1 columns of a wider hidden buffer would hand sequences b >= 1 the wrong rows); x2 below
+        // rewrites the batch stride, so it is checked here, before the rewrite.
+        require(is_contiguous(*x), "x must be contiguous [hidden, K+1, B]");
         nmi_tensor x2 = *x; // the columns of all sequences as one [hidden, (K+1) * B] operand
         x2.ne[1] = (K + 1) * B;
         x2.ne[2] = 1;

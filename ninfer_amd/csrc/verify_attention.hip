@@ -825,7 +825,9 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
 
 // Merge the four waves' (m, l, O) through LDS (reusing the staging area) and write the
 // workgroup's partial: out_o [rows][D] (rows < R) and out_ml [rows][2] (log2-domain max, row sum).
-// Rows go through LDS 32 at a time (two 16-row tiles per batch).
+// Rows go through LDS 32 at a time (two 16-row tiles per batch). The combine is branch-free (a wave
+// that saw no visible key has m = -inf, weight 0 and zero accumulators) and every LDS read of a row
+// is issued before its first use. CACHED: ordinary stores instead of non-temporal ones.
 template <int NT, int D, bool CACHED, typename State>
 __device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
                                               float* out_o, float* out_ml) {
@@ -834,6 +836,15 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
     float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
     float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
     constexpr int NB = (NT + 1) / 2;
+    constexpr int UPR = D / 4;                              // f4 units of one row
+    constexpr int RPP = 256 / UPR;                          // rows per pass of the 256 threads
+    // The thread index is laundered here, so the unit mapping below is computed at this point
+    // instead of being kept live across the whole kernel (at two workgroups per CU the compiler
+    // otherwise spills a lane offset and reloads it from scratch here).
+    int tid = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    const int d4 = 4 * (tid & (UPR - 1));
+    const int r0 = tid / UPR;
 #pragma unroll
     for (int jb = 0; jb < NB; ++jb) {
         if (jb > 0) { __syncthreads(); } // the previous batch's rows have been read
@@ -861,37 +872,42 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
         __syncthreads();
         const int rb = 32 * jb;
         const int rows = min(32, R - rb);
-        for (int idx = threadIdx.x; idx < rows * (D / 4); idx += blockDim.x) {
-            const int r = idx / (D / 4);
-            const int d4 = 4 * (idx - r * (D / 4));
-            float M = -INFINITY;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) { M = fmaxf(M, sm_m[w * 32 + r]); }
+        for (int k = 0; k < 32 / RPP; ++k) {
+            const int r = r0 + RPP * k;
+            if (r >= rows) { continue; }
+            float mw[kWaves];
+            float lw[kWaves];
+            f4 ow[kWaves];
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                mw[w] = sm_m[w * 32 + r];
+                lw[w] = sm_l[w * 32 + r];
+                ow[w] = *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
+            }
+            const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
             f4 o = {0.f, 0.f, 0.f, 0.f};
             float lsum = 0.0f;
-            if (M != -INFINITY) {
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) {
-                    const float mw = sm_m[w * 32 + r];
-                    if (mw == -INFINITY) { continue; }
-                    const float wgt = __builtin_amdgcn_exp2f(mw - M);
-                    o += wgt * *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
-                    lsum = fmaf(sm_l[w * 32 + r], wgt, lsum);
-                }
+            for (int w = 0; w < kWaves; ++w) {
+                const float wgt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+                o += wgt * ow[w];
+                lsum = fmaf(lw[w], wgt, lsum);
             }
+            const int row = rb + r;
             // Read once, by the merge: non-temporal unless the plan routes long splits' partials
             // through the caches.
             if constexpr (CACHED) {
-                *reinterpret_cast<f4*>(out_o + (rb + r) * D + d4) = o;
+                *reinterpret_cast<f4*>(out_o + row * D + d4) = o;
                 if (d4 == 0) {
-                    out_ml[2 * (rb + r)] = M;
-                    out_ml[2 * (rb + r) + 1] = lsum;
+                    out_ml[2 * row] = M;
+                    out_ml[2 * row + 1] = lsum;
                 }
             } else {
-                __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + (rb + r) * D + d4));
+                __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + row * D + d4));
                 if (d4 == 0) {
-                    __builtin_nontemporal_store(M, out_ml + 2 * (rb + r));
-                    __builtin_nontemporal_store(lsum, out_ml + 2 * (rb + r) + 1);
+                    __builtin_nontemporal_store(M, out_ml + 2 * row);
+                    __builtin_nontemporal_store(lsum, out_ml + 2 * row + 1);
                 }
             }
         }

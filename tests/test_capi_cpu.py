@@ -307,6 +307,22 @@ def test_linear_validation():
         ops.linear_argmax(x, _q6_weight(), 248320, ws, _t(na.BF16, (4,), 0x300000))
 
 
+def test_fused_head_rejects_strided_batch():
+    """The fused lm_head + acceptance reads the (K+1) * B hidden columns as one packed operand: an x
+    whose batch stride is not the packed one (the first K+1 columns of a wider hidden buffer) is
+    rejected before any launch, as is a packed x with a wrong column count."""
+    K, B = 3, 2
+    state = [_t(na.I32, (K, B)), _t(na.I32, (B,)), _t(na.I32, (B,)), _t(na.I32, (K + 1, B)),
+             _t(na.I32, (B,)), _t(na.I32, (B,)), _t(na.I64, (4 + K, B))]
+    ws = _WS(ops.speculative_accept_fused_head_workspace_bytes(K, B))
+    x = _t(na.BF16, (5120, K + 1, B), 0x100000)
+    x.nb[2] = x.nb[1] * 16  # columns 0..K of a [5120, 16, B] buffer
+    with pytest.raises(ValueError, match="x must be contiguous"):
+        ops.speculative_accept_fused_head(x, _q6_weight(), *state, 248320, 0x1000, ws)
+    with pytest.raises(ValueError, match="x must be"):
+        ops.speculative_accept_fused_head(_t(na.BF16, (5120, K, B), 0x100000), _q6_weight(), *state, 248320, 0x1000, ws)
+
+
 def test_argmax_validation():
     with pytest.raises(ValueError, match="valid_rows"):
         ops.argmax(_t(na.BF16, (100, 4)), _t(na.I32, (4,)), 101)
@@ -395,6 +411,14 @@ def test_workspace_bound_covers_every_envelope(q_heads, kv_heads, head_dim):
         assert max(sizes) <= bound and bound in sizes, (T, bound, max(sizes))
 
 
+def test_static_scratch_holds_every_batch1_plan():
+    """The allocation-free entry's 16 MiB static scratch holds the largest batch-1 plan of every
+    registered geometry and T <= 32 (10.2 MiB: the 80-row form at 40/8 heads, T = 16)."""
+    worst = max(ops.gqa_attention_workspace_bound(qh, T) for qh in (40, 24, 16) for T in range(1, 33))
+    assert worst == ops.gqa_attention_workspace_bound(40, 16)
+    assert 10 << 20 < worst <= 16 << 20
+
+
 def test_workspace_bound_reference_call_shapes():
     """The reference sizes its arenas with gqa_attention_workspace_bytes(query_heads, tokens)
     (src/targets/qwen3_6/impl/runtime/layouts_impl.h:152,253,286), including prefill token counts."""
@@ -448,6 +472,12 @@ def test_cyclic_commit_validation():
         c = _cyclic()
         c.k_scale = _t(na.FP16, (1,))
         ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (0, 4), c)
+    # the cache planes too (reference require_vector_aligned(cache.k/v))
+    for plane in ("k", "v"):
+        c = _cyclic()
+        setattr(c, plane, _t(na.BF16, (128, 4096, 8), ptr=0x20008))
+        with pytest.raises(ValueError, match=f"cache {plane} must be 16-byte aligned"):
+            ops.kv_cache_append_prefix_cyclic(k, k, pos, cnt, (0, 4), c)
 
 
 def _driver():

@@ -266,3 +266,37 @@ def test_large_magnitude_groups_within_fp16_range(gpu):
     out, cache = gpu_runner.run_attention(case, out_f32=True)
     _check_cache(cache, expected_cache)
     _check_out(out, ref, REL_L2_F32)
+
+
+def test_repeated_calls_one_workspace(gpu):
+    """Successive calls on one workspace (filled with a non-zero pattern first): no call depends on
+    what an earlier one left in the split scratch. Three A3 calls with different queries on one
+    cache and workspace, each against the oracle, then the first query again, bit-exact against its
+    first result."""
+    import ninfer_amd as na
+    from ninfer_amd import ops
+    from ninfer_amd.device import DeviceArray, DeviceBuffer, synchronize
+    case = AttnCase([5000], T=4, seed=4200, max_context=5100)
+    _, ref0 = case.oracle_after_append()
+    cache = gpu_runner.upload_cache(case)
+    gpu_runner.append(case, cache)
+    D, Hq, T = case.D, case.Hq, case.T
+    env = (1, case.max_context)
+    ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(Hq, case.Hkv, D, T, 1, env[1]))
+    ws.fill(0xA5)
+    pos = DeviceArray.from_numpy(na.I32, case.positions, (T, 1))
+    rng = np.random.default_rng(4201)
+    queries = [case.q] + [((rng.standard_normal(case.q.size).astype(np.float32)).view(np.uint32) >> 16).astype(np.uint16)
+                          for _ in range(2)]
+    outs = []
+    for qv in queries + [case.q]:
+        q = DeviceArray.from_numpy(na.BF16, qv, (D, Hq, T, 1))
+        out = DeviceArray(na.FP32, (D, Hq, T, 1))
+        ops.gqa_attention_cached(q.tensor(), pos.tensor(), case.scale, cache.view(), env, ws, out.tensor(), None)
+        synchronize()
+        outs.append(out.numpy().astype(np.float64))
+    for qv, got in zip(queries, outs):
+        case.q = qv
+        _, ref = case.oracle_after_append()
+        _check_out(got, ref, REL_L2_F32)
+    assert np.array_equal(outs[0], outs[3])

@@ -17,6 +17,87 @@ import gpu_runner
 pytestmark = pytest.mark.gpu
 
 
+ROUNDS = 4
+
+
+def _elem(arr, i):
+    return DeviceArray(na.I32, (1,), buf=arr.buf, offset=arr.offset + 4 * i)
+
+
+@pytest.mark.parametrize("Ls,T,Hq,Hkv,D", [([3000], 4, 40, 8, 128), ([2500], 16, 40, 8, 128), ([1800], 4, 24, 4, 256)],
+                         ids=["A1-40-8", "80row-T16", "D256-24-4"])
+def test_noalloc_under_capture(gpu, oracle, Ls, T, Hq, Hkv, D):
+    """The allocation-free entry is for callers under graph capture. The first test of this file, so
+    the process's first nmi_gqa_attention_noalloc call (which resolves the device's scratch address)
+    runs inside an active capture. The captured round (positions from the device-side length, then
+    the attention into the static scratch) is replayed over several rounds with the length advanced
+    on the device, against eager workspace-form calls on a twin state (bit-exact) and the oracle."""
+    from ninfer_amd import synthetic as syn
+    from ninfer_amd.device import Graph, Stream
+    print(f"case noalloc capture Ls={Ls} T={T} {Hq}|{Hkv} D={D}", flush=True)
+    B, K = len(Ls), T - 1
+    base = AttnCase(Ls, T=T, Hq=Hq, Hkv=Hkv, D=D, seed=700 + T + D, max_context=max(Ls) + ROUNDS * T + T)
+    P = base.P
+    stream = Stream()
+    states = []
+    for _ in range(2):  # [graph with the no-alloc entry, eager workspace form]
+        st = dict(cache=gpu_runner.upload_cache(base),
+                  token=DeviceArray.from_numpy(na.I32, np.arange(B, dtype=np.int32) + 7, (B,)),
+                  drafts=DeviceArray.from_numpy(na.I32, np.arange(B * K, dtype=np.int32) + 100, (K, B)),
+                  length=DeviceArray.from_numpy(na.I32, np.array(Ls, np.int32), (B,)),
+                  ids=DeviceArray(na.I32, (T, B)), pos=DeviceArray(na.I32, (T, B)),
+                  q=DeviceArray(na.BF16, (D, Hq, T, B)), k=DeviceArray(na.BF16, (D, Hkv, T, B)),
+                  v=DeviceArray(na.BF16, (D, Hkv, T, B)), out=DeviceArray(na.BF16, (D, Hq, T, B)),
+                  ws=DeviceBuffer(ops.gqa_attention_workspace_bytes(Hq, Hkv, D, T, B, base.max_context)))
+        st["ws"].fill(0xFF)
+        states.append(st)
+    env = (1, base.max_context)
+
+    def round_ops(st, noalloc):
+        ops.speculative_prepare_verify_inputs(st["token"].tensor(), st["drafts"].tensor(), st["length"].tensor(),
+                                              st["ids"].tensor(), st["pos"].tensor(), stream)
+        if noalloc:
+            ops.gqa_attention_noalloc(st["q"].tensor(), st["k"].tensor(), st["v"].tensor(), st["pos"].tensor(),
+                                      base.scale, st["cache"].view(), env, st["out"].tensor(), stream)
+        else:
+            ops.gqa_attention(st["q"].tensor(), st["k"].tensor(), st["v"].tensor(), st["pos"].tensor(), base.scale,
+                              st["cache"].view(), env, st["ws"], st["out"].tensor(), stream)
+
+    graph = Graph(stream)
+    with graph:
+        round_ops(states[0], True)
+    kc, vc, ks, vs = (a.copy() for a in base.cache_planes())
+    lengths = np.array(Ls, np.int64)
+    rng = np.random.default_rng(41 + T)
+    for r in range(ROUNDS):
+        q = syn.normal_bf16(syn.derive_seed(9, r, 1, D), D * Hq * T * B)
+        k = syn.normal_bf16(syn.derive_seed(9, r, 2, D), D * Hkv * T * B)
+        v = syn.normal_bf16(syn.derive_seed(9, r, 3, D), D * Hkv * T * B)
+        for st in states:
+            st["q"].upload(q)
+            st["k"].upload(k)
+            st["v"].upload(v)
+        graph.launch()
+        round_ops(states[1], False)
+        stream.synchronize()
+        pos = (lengths[:, None] + np.arange(T)[None, :]).astype(np.int32).reshape(-1)
+        oracle.kv_append(k, v, pos, T, B, Hkv, D, P, kc, vc, ks, vs)
+        ref = oracle.attention(q, kc, vc, ks, vs, pos, None, T, B, Hq, Hkv, D, P, base.scale)
+        g_out, e_out = states[0]["out"].numpy(), states[1]["out"].numpy()
+        assert np.array_equal(states[0]["pos"].numpy(), pos), "device positions differ"
+        assert np.array_equal(g_out, e_out), "replayed no-alloc round differs from the workspace form"
+        for got_g, got_e, want in zip(states[0]["cache"].download(), states[1]["cache"].download(), (kc, vc, ks, vs)):
+            assert np.array_equal(got_g, got_e) and np.array_equal(got_g, want), "cache bytes differ"
+        got = (g_out.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        assert rel_l2(got, ref) <= 2e-3
+        produced = rng.integers(1, T + 1, size=B)
+        for st in states:
+            for b, a in enumerate(produced):
+                for _ in range(int(a)):
+                    ops.increment_i32_scalar(_elem(st["length"], b).tensor(), stream)
+        lengths += produced
+
+
 def _run(case, noalloc):
     D, Hq, Hkv, T, B = case.D, case.Hq, case.Hkv, case.T, case.B
     cache = gpu_runner.upload_cache(case)
