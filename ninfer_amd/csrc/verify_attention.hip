@@ -833,8 +833,8 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
                                               float* out_o, float* out_ml) {
     constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
     float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
-    float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [kWaves][32]
-    float* sm_l = sm_m + kWaves * 32;                       // [kWaves][32]
+    float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [32][kWaves]: one 16-byte read per row
+    float* sm_l = sm_m + kWaves * 32;                       // [32][kWaves]
     constexpr int NB = (NT + 1) / 2;
     constexpr int UPR = D / 4;                              // f4 units of one row
     constexpr int RPP = 256 / UPR;                          // rows per pass of the 256 threads
@@ -855,8 +855,8 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
             const int r = 16 * u + c; // row within the batch
             if (g == 0) {
                 // log2-domain maximum of this wave's partial; O and l both carry the 2^kPOffset factor.
-                sm_m[wave * 32 + r] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
-                sm_l[wave * 32 + r] = s.l[nt][0];
+                sm_m[r * kWaves + wave] = s.m[nt] == -INFINITY ? -INFINITY : s.m[nt] * s.rowmul[nt];
+                sm_l[r * kWaves + wave] = s.l[nt][0];
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -872,28 +872,31 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
         __syncthreads();
         const int rb = 32 * jb;
         const int rows = min(32, R - rb);
+        constexpr int KR = 32 / RPP; // rows per thread and batch
+        // Every LDS read of the batch first (rows past the last valid one re-read it), then the
+        // combine, then the guarded stores.
+        f4 mv[KR], lv[KR], ow[KR][kWaves];
 #pragma unroll
-        for (int k = 0; k < 32 / RPP; ++k) {
+        for (int k = 0; k < KR; ++k) {
+            const int r = min(r0 + RPP * k, rows - 1);
+            mv[k] = *reinterpret_cast<const f4*>(sm_m + r * kWaves);
+            lv[k] = *reinterpret_cast<const f4*>(sm_l + r * kWaves);
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) { ow[k][w] = *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4); }
+        }
+#pragma unroll
+        for (int k = 0; k < KR; ++k) {
             const int r = r0 + RPP * k;
-            if (r >= rows) { continue; }
-            float mw[kWaves];
-            float lw[kWaves];
-            f4 ow[kWaves];
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                mw[w] = sm_m[w * 32 + r];
-                lw[w] = sm_l[w * 32 + r];
-                ow[w] = *reinterpret_cast<const f4*>(sm_o + (w * 32 + r) * kRowStride + d4);
-            }
-            const float M = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+            const float M = fmaxf(fmaxf(mv[k][0], mv[k][1]), fmaxf(mv[k][2], mv[k][3]));
             f4 o = {0.f, 0.f, 0.f, 0.f};
             float lsum = 0.0f;
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) {
-                const float wgt = mw[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
-                o += wgt * ow[w];
-                lsum = fmaf(lw[w], wgt, lsum);
+                const float wgt = mv[k][w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv[k][w] - M);
+                o += wgt * ow[k][w];
+                lsum = fmaf(lv[k][w], wgt, lsum);
             }
+            if (r >= rows) { continue; }
             const int row = rb + r;
             // Read once, by the merge: non-temporal unless the plan routes long splits' partials
             // through the caches.
