@@ -67,9 +67,10 @@ struct Geo {
     static constexpr int kRingBytes = kWaves * 2 * kStageBytes; // two stages per wave
     static constexpr int kNewStage = kRingBytes;       // A1: new rows quantized in-kernel (Q tile before)
     static constexpr int kPosLds = kNewStage + kStageBytes; // positions[0 .. T), T <= 32
-    static constexpr int kSmemBytes = kPosLds + 128;   // D=128: 78,464 B (two workgroups per CU); D=256: 152,192 B
+    static constexpr int kWideK = kPosLds + 128;       // a wave met a K scale of 512 or more
+    static constexpr int kSmemBytes = kPosLds + 144;   // D=128: 78,480 B (two workgroups per CU); D=256: 152,208 B
 };
-static_assert(Geo<128>::kStageBytes == 8704 && Geo<128>::kSmemBytes == 78464, "D=128 LDS map");
+static_assert(Geo<128>::kStageBytes == 8704 && Geo<128>::kSmemBytes == 78480, "D=128 LDS map");
 // Probabilities are FP16 exp2(score - m + 8); the reference maximum m moves only when a score
 // exceeds it by more than 2^7, so P <= 2^15 stays inside FP16 and most chunks skip the rescale.
 constexpr float kPOffset = 8.0f;
@@ -417,6 +418,37 @@ __device__ __forceinline__ void read_chunk(const NMI_AS3 char* st, ChunkRegs<D>&
     for (int j = 0; j < 8; ++j) {
         const int row = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
         r.vr[j] = *(const NMI_AS3 typename CR::VRow*)(st + G::kStageV + row * D + (D / 16) * c);
+    }
+}
+
+// ---- FP32-range decode ----------------------------------------------------------------------
+//
+// The MFMA operands are FP16(code * scale), exact for every scale below 512 (FP16 exponent field
+// below 24: |code * scale| <= 127 * 515.8 < 65,504). The reference decodes cached K/V in FP32
+// (include/ninfer/ops/gqa_attention.h:30) and INT8-G64 scales reach 65,504. A larger V scale makes
+// V' overflow, and an overflowing V' always leaves O non-finite (p * inf, or 0 * inf = NaN), which
+// the merge sees. A larger K scale may instead give a score of -inf, which would drop its key
+// silently, so every lane ORs the exponent bits 14 and 13 of its K scale words into a flag (two VALU
+// per chunk, from registers the chunk has in any case), and a workgroup whose waves saw such a
+// scale marks its partial rows (row sum -1). The merge recomputes a marked or non-finite split's
+// partial exactly in FP32 (verify_attn_exact_split below).
+template <int D>
+__device__ __forceinline__ uint32_t wide_k_bits(const ChunkRegs<D>& r) {
+    if constexpr (D == 128) {
+        const uint32_t a = r.ksc[0];
+        const uint32_t b = r.ksc[1];
+        return (a & (a << 1)) | (b & (b << 1));
+    } else {
+        uint32_t f = 0u;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const uint32_t x = static_cast<uint32_t>(r.ksc[kt][w]);
+                f |= x & (x << 1);
+            }
+        }
+        return f;
     }
 }
 
@@ -830,7 +862,7 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
 // is issued before its first use. CACHED: ordinary stores instead of non-temporal ones.
 template <int NT, int D, bool CACHED, typename State>
 __device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
-                                              float* out_o, float* out_ml) {
+                                              float* out_o, float* out_ml, bool kmark = false) {
     constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
     float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
     float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [32][kWaves]: one 16-byte read per row
@@ -898,6 +930,7 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
             }
             if (r >= rows) { continue; }
             const int row = rb + r;
+            if (kmark) { lsum = -1.0f; } // a K scale of 512 or more: the merge recomputes this split
             // Read once, by the merge: non-temporal unless the plan routes long splits' partials
             // through the caches.
             if constexpr (CACHED) {
@@ -955,6 +988,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     NMI_AS3 char* qtile = (NMI_AS3 char*)smem + (NT == 5 ? GE::kSmemBytes : GE::kNewStage);
     NMI_AS3 int32_t* pos_lds = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GE::kPosLds);
     const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
+    if (threadIdx.x == 0) { *(NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GE::kWideK) = 0; }
     if (wave == 0) {
         // Positions travel the same way (a vector load here would wait behind every chunk DMA).
         if (lane < a.T) { __builtin_amdgcn_global_load_lds((const NMI_AS1 void*)(pos + lane), (NMI_AS3 void*)pos_lds, 4, 0, 0); }
@@ -1107,6 +1141,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
 
     // ---- fused A1 append: the owner quantizes the T new rows into the cache and into its new-row
     // stage; wave 0 attends to them before its history chunks.
+    uint32_t kwide = 0u; // exponent bits 14 and 13 of the K scales seen (FP32-range test)
     if (owner) {
         NMI_AS3 char* ns = (NMI_AS3 char*)smem + GE::kNewStage;
         __syncthreads(); // every wave has read its Q rows from this area
@@ -1123,6 +1158,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
         if (wave == 0) {
             ChunkRegs<D> r;
             read_chunk<D>(ns, r, lane, c, g);
+            kwide |= wide_k_bits<D>(r);
             const KeyRange nk{L, L, min(window, L + a.T)};
             if constexpr (NT == 5) {
                 compute_chunk_tiles<NT, D, true>(r, L, s, nk, c, g, qtile);
@@ -1144,6 +1180,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
             wait_chunk<D>(cj + kStride < hend); // chunk cj landed; the next one may stay in flight
             ChunkRegs<D> r;
             read_chunk<D>(st, r, lane, c, g);
+            kwide |= wide_k_bits<D>(r);
             if (cj + 2 * kStride < hend) {
                 __builtin_amdgcn_s_waitcnt(kWaitLgkm0); // chunk cj sits in registers: reuse its stage
                 issue_chunk<D, ONCE>(st, hb, dl, cj + 2 * kStride, lane);
@@ -1172,6 +1209,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
             issue_chunk<D, ONCE>(ring, hb, dl, first + 2 * kStride, lane);
         }
         f4 sacc[2][NT];
+        kwide |= wide_k_bits<D>(r);
         qk_chunk<NT, D>(r, s, sacc);
         typename ChunkRegs<D>::VRow vcur[8];
         i4 vswcur[2][D / 128];
@@ -1208,7 +1246,10 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
             }
             stage ^= 1;
             f4 sn[2][NT];
-            if (cn < hend) { qk_chunk<NT, D>(rn, s, sn); } // the last chunk has no successor
+            if (cn < hend) { // the last chunk has no successor (a stage past the end holds anything)
+                kwide |= wide_k_bits<D>(rn);
+                qk_chunk<NT, D>(rn, s, sn);
+            }
             pv_chunk<NT, D>(pop, vcur, vswcur, cj, cj + kChunk > hk.vis_all, s, hk, c, g);
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
@@ -1225,11 +1266,14 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
         }
     }
 
+    NMI_AS3 int32_t* kwide_word = (NMI_AS3 int32_t*)((NMI_AS3 char*)smem + GE::kWideK);
+    if (__any((kwide & 0x40004000u) != 0u) && lane == 0) { *kwide_word = 1; }
+
     // ---- merge the four waves through LDS (reusing the staging ring), then write the partial.
     __builtin_amdgcn_s_waitcnt(0); // no DMA may land in the ring after this point
     __syncthreads();
     static_assert(kWaves * 32 * (D + 4 + 2) * 4 <= GE::kSmemBytes, "wave merge exceeds the LDS map");
-    write_partial<NT, D, CACHED>(s, smem, R, wave, c, g, out_o, out_ml);
+    write_partial<NT, D, CACHED>(s, smem, R, wave, c, g, out_o, out_ml, *kwide_word != 0);
 }
 
 // CACHED: the batch-1 partials go out with ordinary (cached) stores; an instance of its own, launched
@@ -1722,6 +1766,22 @@ struct MergeArgs {
     int32_t B;
     int32_t split_slots;
     int32_t rows_per_slot; // rows of one partial slot (32, or 80 for the 5-tile tree form)
+    // Exact recompute of a split (FP32-range decode; INT8 caches only): the partial kernel's inputs.
+    const uint16_t* q;
+    const int32_t* positions;
+    const int32_t* parents;
+    const int8_t* kc;
+    const int8_t* vc;
+    const uint16_t* ks;
+    const uint16_t* vs;
+    int64_t code_seq;
+    int64_t scale_seq;
+    int32_t P;
+    int32_t kps;          // B == 1: keys per split
+    int32_t max_keys;
+    int32_t split_budget; // B > 1: the device batch plan's budget
+    int32_t fused;        // the partial launch wrote the new rows itself (its split holding L took them)
+    float scale_log2;
 };
 
 constexpr int kMergeThreads = 256;
@@ -1729,6 +1789,178 @@ constexpr int kMergeDims = 32;                               // output dims per 
 constexpr int kMergeGroups = kMergeThreads / kMergeDims;     // split groups per block
 constexpr int kMergePre = 8;                                 // 64 splits loaded up front
 constexpr int kMergeMaxSplits = 2048;
+
+// ---- exact recompute of a split (FP32-range decode) -------------------------------------------
+//
+// A split whose partial the fast path could not hold (marked by the partial kernel for a K scale of
+// 512 or more, or non-finite: a V scale that large) is recomputed here for one query row and one
+// 32-dim slice, with the reference's decode FP32(code) * scale (include/ninfer/ops/gqa_attention.h:30)
+// and FP32 arithmetic, over exactly the keys the partial kernel gave that split: [k0, min(kend,
+// window)), below L when the launch wrote the new rows itself, plus the new rows [L, L + T) for the
+// split holding L. A key at or past L is visible to token t when bit (key - L) of t's mask is set
+// (causal or ancestor mask). Whole workgroup of 256 threads, one key per thread per block of 256.
+// m is the log2-domain maximum; l and o carry the partial kernel's 2^kPOffset factor.
+constexpr int kExactLds = 256 + 256 + 8 * 32 + 16; // + D floats of the query row
+
+template <int D>
+__device__ void exact_split(const MergeArgs& a, int b, int t, int qh, int k0, int kend, int d0, float* xs,
+                            float& m_out, float& l_out, float& o_out) {
+    constexpr int G = D / 64;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    float* xq = xs;                    // [D] query row * scale * log2(e)
+    float* xp = xs + D;                // [256] probabilities of the block's keys
+    float* xo = xs + D + 256;          // [8][32] slice sums per key part
+    float* xr = xs + D + 256 + 8 * 32; // [16] reductions
+    const int h = qh / a.G;
+    const int32_t* pos = a.positions + static_cast<int64_t>(b) * a.T;
+    const int pos_first = pos[0];
+    const int pos_last = pos[a.T - 1];
+    const int window = max(0, min(pos_last + 1, a.max_keys));
+    const int L = max(0, min(pos_first, window));
+    const int k1 = min(kend, window);
+    const int hend = a.fused ? min(k1, L) : k1;
+    const bool owner = a.fused && L >= k0 && L < kend && L < window;
+    const int n1 = max(0, hend - k0);
+    const int n2 = owner ? max(0, min(window, L + a.T) - L) : 0;
+    const uint32_t nmask = new_key_mask(a.parents ? a.parents + static_cast<int64_t>(b) * a.T : nullptr, t);
+    const int8_t* kbase = a.kc + static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
+    const int8_t* vbase = a.vc + static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
+    const uint16_t* ksb = a.ks + static_cast<int64_t>(b) * a.scale_seq + static_cast<int64_t>(h) * a.P * G;
+    const uint16_t* vsb = a.vs + static_cast<int64_t>(b) * a.scale_seq + static_cast<int64_t>(h) * a.P * G;
+    __syncthreads(); // the caller's use of xs is over
+    if (tid < D) { xq[tid] = bf16_to_f32(a.q[static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + tid]) * a.scale_log2; }
+    __syncthreads();
+    float M = -INFINITY; // uniform
+    float Ls = 0.0f;     // uniform
+    float Od = 0.0f;     // threads tid < 32: dim d0 + tid
+    const auto key_of = [&](int i) { return i < n1 ? k0 + i : L + (i - n1); };
+    for (int base = 0; base < n1 + n2; base += 256) {
+        const int i = base + tid;
+        float sk = -INFINITY;
+        if (i < n1 + n2) {
+            const int k = key_of(i);
+            const bool vis = k < L || (static_cast<unsigned>(k - L) < 32u && ((nmask >> (k - L)) & 1u) != 0u);
+            if (vis) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int gq = 0; gq < G; ++gq) {
+                    const float sc = f16_bits_to_f32(ksb[static_cast<int64_t>(k) * G + gq]);
+                    float part = 0.0f;
+                    for (int d = 0; d < 64; ++d) {
+                        part = fmaf(xq[64 * gq + d], static_cast<float>(kbase[static_cast<int64_t>(k) * D + 64 * gq + d]) * sc, part);
+                    }
+                    acc += part;
+                }
+                sk = acc;
+            }
+        }
+        float bm = wave_max(sk);
+        if (lane == 0) { xr[wave] = bm; }
+        __syncthreads();
+        bm = fmaxf(fmaxf(xr[0], xr[1]), fmaxf(xr[2], xr[3]));
+        const float Mn = fmaxf(M, bm);
+        const float alpha = (M == -INFINITY || Mn == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+        const float pk = (sk == -INFINITY || Mn == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sk - Mn + kPOffset);
+        xp[tid] = pk;
+        float bs = wave_sum(pk);
+        __syncthreads(); // xr read by every thread, xp written
+        if (lane == 0) { xr[4 + wave] = bs; }
+        // O slice: thread (dim tid % 32, key part tid / 32) sums its 32 keys of the block
+        const int dim = tid & 31;
+        const int part = tid >> 5;
+        const int dg = (d0 + dim) / 64;
+        float acc = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const int ii = base + 32 * part + j;
+            const float pj = xp[32 * part + j];
+            if (pj != 0.0f) {
+                const int k = key_of(ii);
+                const float v = static_cast<float>(vbase[static_cast<int64_t>(k) * D + d0 + dim]) * f16_bits_to_f32(vsb[static_cast<int64_t>(k) * G + dg]);
+                acc = fmaf(pj, v, acc);
+            }
+        }
+        xo[32 * part + dim] = acc;
+        __syncthreads();
+        bs = (xr[4] + xr[5]) + (xr[6] + xr[7]);
+        if (tid < 32) {
+            float s = 0.0f;
+#pragma unroll
+            for (int q8 = 0; q8 < 8; ++q8) { s += xo[32 * q8 + tid]; }
+            Od = fmaf(Od, alpha, s);
+        }
+        Ls = fmaf(Ls, alpha, bs);
+        M = Mn;
+        __syncthreads(); // xp, xo and xr are reused by the next block
+    }
+    m_out = M;
+    l_out = Ls;
+    o_out = Od;
+}
+
+// The merge of one output row's 32-dim slice over its splits in split order (running log-sum-exp),
+// recomputing each split the fast path could not hold. Whole workgroup; writes the output.
+template <int D, int RPS>
+__device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0, float* xs) {
+    const int tid = threadIdx.x;
+    const int h = qh / a.G;
+    const int gi = qh - h * a.G;
+    const int rc = t / a.tokens_per_chunk;
+    const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
+    const int rps = RPS > 0 ? RPS : a.rows_per_slot;
+    int first = 0;
+    int count = a.nsplit;
+    int kps = a.kps;
+    int* xi = reinterpret_cast<int*>(xs + D + 256 + 8 * 32);
+    if (a.B > 1) {
+        first = a.seq_table[2 * b];
+        count = a.seq_table[2 * b + 1];
+        __syncthreads();
+        if (tid < 64) {
+            const int kb = static_cast<int>(batch_kps(batch_windows(a.positions, a.T, a.B, a.max_keys), a.split_budget));
+            if (tid == 0) { xi[8] = kb; }
+        }
+        __syncthreads();
+        kps = xi[8];
+    }
+    const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots;
+    float M = -INFINITY;
+    float Ls = 0.0f;
+    float Od = 0.0f;
+    for (int j = 0; j < count; ++j) {
+        const int64_t slot = slot0 + first + j;
+        float ms = a.part_ml[slot * (2 * rps) + 2 * r];
+        float ls = a.part_ml[slot * (2 * rps) + 2 * r + 1];
+        float od = tid < 32 ? a.part_o[slot * (static_cast<int64_t>(rps) * D) + static_cast<int64_t>(r) * D + d0 + tid] : 0.0f;
+        const bool nonfin = tid < 32 && ls > 0.0f && !__builtin_isfinite(od);
+        __syncthreads();
+        if (tid < 64) {
+            const bool any = __any(nonfin);
+            if (tid == 0) { xi[9] = any ? 1 : 0; }
+        }
+        __syncthreads();
+        const bool redo = a.kc != nullptr && (ls < 0.0f || !__builtin_isfinite(ls) || xi[9] != 0);
+        if (redo) { exact_split<D>(a, b, t, qh, j * kps, j * kps + kps, d0, xs, ms, ls, od); }
+        if (ls > 0.0f) {
+            const float Mn = fmaxf(M, ms);
+            const float al = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
+            const float be = __builtin_amdgcn_exp2f(ms - Mn);
+            Od = fmaf(Od, al, od * be);
+            Ls = fmaf(Ls, al, ls * be);
+            M = Mn;
+        }
+    }
+    if (tid < 32) {
+        const float val = Ls > 0.0f ? Od / Ls : 0.0f;
+        const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d0 + tid;
+        if (a.out_f32) {
+            static_cast<float*>(a.out)[oi] = val;
+        } else {
+            static_cast<uint16_t*>(a.out)[oi] = f32_to_bf16_bits(val);
+        }
+    }
+}
 
 // Log-sum-exp merge over splits (reference src/ops/kernel/gqa_attention_decode.cuh:144-227,
 // including "every split empty => 0"). Block (row, dim slice): (b, t, qh) x 32 dims. Thread
@@ -1745,7 +1977,9 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     __shared__ float lw[kMergeMaxSplits];
     __shared__ float red[kMergeThreads / 64];
     __shared__ float part[kMergeGroups][kMergeDims];
+    __shared__ int redo_flag;
     const int row_id = blockIdx.x; // (b, t, qh)
+    if (threadIdx.x == 0) { redo_flag = 0; }
     const int qh = row_id % a.Hq;
     const int t = (row_id / a.Hq) % a.T;
     const int b = row_id / (a.Hq * a.T);
@@ -1771,9 +2005,11 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
         pre[k] = s < nsplit ? ld(po + static_cast<int64_t>(s) * rps * D + r * D + d) : 0.0f;
     }
     float M = -INFINITY;
+    bool redo = false; // a split the fast path could not hold (marked, or non-finite)
     for (int s = tid; s < nsplit; s += kMergeThreads) {
         const float ls = ld(ml + s * (2 * rps) + 2 * r + 1);
         const float ms = ld(ml + s * (2 * rps) + 2 * r);
+        redo |= ls < 0.0f || !__builtin_isfinite(ls);
         wts[s] = ls > 0.0f ? ms : -INFINITY;
         lw[s] = ls;
         M = fmaxf(M, wts[s]);
@@ -1801,16 +2037,27 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
 #pragma unroll
         for (int k = 0; k < kMergePre; ++k) {
             const int s = sg + kMergeGroups * k;
-            if (s < nsplit) { o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o; }
+            if (s < nsplit) {
+                redo |= wts[s] != 0.0f && !__builtin_isfinite(pre[k]);
+                o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o;
+            }
         }
 #pragma unroll 4
         for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
             const float v = ld(po + static_cast<int64_t>(s) * rps * D + r * D + d);
+            redo |= wts[s] != 0.0f && !__builtin_isfinite(v);
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
     }
     part[sg][tid - sg * kMergeDims] = o;
+    if (redo) { redo_flag = 1; }
     __syncthreads();
+    if (redo_flag != 0 && a.kc != nullptr) {
+        // the split weights are no longer needed: their LDS holds the exact path's scratch
+        static_assert(D + kExactLds <= kMergeMaxSplits, "exact-path scratch exceeds the weights' LDS");
+        merge_row_exact<D, RPS>(a, b, t, qh, blockIdx.y * kMergeDims, wts);
+        return;
+    }
     if (tid < kMergeDims) {
         float acc = 0.0f;
 #pragma unroll
@@ -1832,9 +2079,12 @@ constexpr int kMergeRowsPerBlock = kMergeThreads / kMergeDims;
 
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(MergeArgs a) {
+    __shared__ int redo_flag;
     const int tid = threadIdx.x;
-    const int row_id = blockIdx.x * kMergeRowsPerBlock + tid / kMergeDims; // (b, t, qh)
-    if (row_id >= a.B * a.T * a.Hq) { return; }
+    if (tid == 0) { redo_flag = 0; }
+    __syncthreads();
+    const int row_id = min(static_cast<int>(blockIdx.x * kMergeRowsPerBlock + tid / kMergeDims), a.B * a.T * a.Hq - 1); // (b, t, qh)
+    const bool row_live = static_cast<int>(blockIdx.x * kMergeRowsPerBlock + tid / kMergeDims) < a.B * a.T * a.Hq;
     const int qh = row_id % a.Hq;
     const int t = (row_id / a.Hq) % a.T;
     const int b = row_id / (a.Hq * a.T);
@@ -1852,6 +2102,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
     float M = -INFINITY;
     float lsum = 0.0f;
     float o = 0.0f;
+    bool redo = false; // a split the fast path could not hold (marked, or non-finite)
     constexpr int kBatch = 8;
 #pragma unroll 1
     for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
@@ -1865,6 +2116,8 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
+            redo |= s0 + k < nsplit && (mlv[k].y < 0.0f || !__builtin_isfinite(mlv[k].y) ||
+                                        (mlv[k].y > 0.0f && !__builtin_isfinite(ov[k])));
             // A split with no visible key never wrote its partial rows: skip it.
             if (!(mlv[k].y > 0.0f)) { continue; }
             const float mn = fmaxf(M, mlv[k].x);
@@ -1875,6 +2128,19 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
             M = mn;
         }
     }
+    if (redo && row_live) { redo_flag = 1; }
+    __syncthreads();
+    if (redo_flag != 0 && a.kc != nullptr) {
+        // the workgroup's rows one after another, exactly
+        __shared__ float xs[D + kExactLds];
+        for (int k = 0; k < kMergeRowsPerBlock; ++k) {
+            const int rid = static_cast<int>(blockIdx.x) * kMergeRowsPerBlock + k;
+            if (rid >= a.B * a.T * a.Hq) { break; }
+            merge_row_exact<D, 0>(a, rid / (a.Hq * a.T), (rid / a.Hq) % a.T, rid % a.Hq, blockIdx.y * kMergeDims, xs);
+        }
+        return;
+    }
+    if (!row_live) { return; }
     const float val = lsum > 0.0f ? o / lsum : 0.0f;
     const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
     if (a.out_f32) {
@@ -2175,6 +2441,21 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     mg.split_slots = plan.split_slots;
     mg.rows_per_slot = plan.rows_per_slot;
     mg.out_f32 = out_f32 ? 1 : 0;
+    mg.q = q;
+    mg.positions = positions;
+    mg.parents = parents;
+    mg.kc = c.kc;
+    mg.vc = c.vc;
+    mg.ks = c.ks;
+    mg.vs = c.vs;
+    mg.code_seq = c.code_seq;
+    mg.scale_seq = c.scale_seq;
+    mg.P = c.P;
+    mg.kps = plan.keys_per_split;
+    mg.max_keys = static_cast<int32_t>(max_keys);
+    mg.split_budget = plan.split_budget;
+    mg.fused = k_new != nullptr ? 1 : 0;
+    mg.scale_log2 = a.scale_log2;
     const dim3 rows_grid((c.B * T * Hq + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock, c.D / kMergeDims);
     if (c.B > 1 && c.D == 128) {
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<128>, rows_grid, dim3(kMergeThreads), 0, stream, mg);

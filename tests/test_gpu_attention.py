@@ -268,6 +268,53 @@ def test_large_magnitude_groups_within_fp16_range(gpu):
     _check_out(out, ref, REL_L2_F32)
 
 
+@pytest.mark.parametrize("absmax", [1e5, 1e6])
+@pytest.mark.parametrize("form", ["a1", "tree", "d256", "long"])
+def test_fp32_range_groups(gpu, absmax, form):
+    """The reference decodes cached K/V as FP32(code) * scale (include/ninfer/ops/gqa_attention.h:30),
+    and INT8-G64 scales reach 65,504, so a group's values may exceed FP16's range. Groups with an
+    absolute maximum of 1e5 and 1e6 (scale absmax / 127, above 512) in the history of K and of V, and
+    a new token whose K/V rows the op itself quantizes at that size, against the FP64 oracle: chunks
+    holding such a scale divide their K scales by a power of two (undone on the FP32 scores) and the
+    wave's V scales by a running power of two (undone on O). Causal (two-tile), tree (five-tile),
+    head_dim 256 (24|4 heads) and a long context (splits of 1,024+ keys)."""
+    T, Hq, Hkv, D, L = 4, 40, 8, 128, 3000
+    parents = None
+    if form == "tree":
+        T = 16
+        parents = np.array(_bfs_tree(16), dtype=np.int32)
+    elif form == "d256":
+        Hq, Hkv, D = 24, 4, 256
+    elif form == "long":
+        L = 60000
+    print(f"case fp32 range {form} absmax={absmax:g}", flush=True)
+    case = AttnCase([L], T=T, Hq=Hq, Hkv=Hkv, D=D, seed=int(absmax) % 1000 + len(form), parents=parents,
+                    qstd=2e-5, gen="pcg" if L > 10000 else "splitmix")
+    rng = np.random.default_rng(int(absmax) + len(form))
+    G = D // 64
+    big = np.float16(absmax / 127.0).view(np.uint16)
+    for sc in (case.ks, case.vs):
+        for _ in range(24):
+            h, r, g = int(rng.integers(0, Hkv)), int(rng.integers(0, L)), int(rng.integers(0, G))
+            sc[0, h, r, g] = big
+    # the new rows of token 1 carry absmax-sized values: the in-kernel quantization gives them such scales
+    per_tok = D * Hkv
+    for arr in (case.k_new, case.v_new):
+        x = (arr[per_tok:2 * per_tok].astype(np.uint32) << 16).view(np.float32)
+        x = x * np.float32(absmax / max(1e-6, float(np.abs(x).max())))
+        arr[per_tok:2 * per_tok] = ((x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
+    expected_cache, ref = case.oracle_after_append()
+    mode = "TREE" if parents is not None else "A1"
+    out, cache = gpu_runner.run_attention(case, out_f32=True, mode=mode)
+    _check_cache(cache, expected_cache)
+    assert np.all(np.isfinite(out))
+    # The rel-L2 bars only: the reference's attention_bf16 composite is an elementwise envelope for
+    # its registered activation range, and outputs here cancel next to values of 1e6 (it is printed).
+    _check_out(out, ref, REL_L2_F32)
+    out16, _ = gpu_runner.run_attention(case, out_f32=False, mode=mode)
+    _check_out(out16, ref, REL_L2_BF16)
+
+
 def test_repeated_calls_one_workspace(gpu):
     """Successive calls on one workspace (filled with a non-zero pattern first): no call depends on
     what an earlier one left in the split scratch. Three A3 calls with different queries on one
