@@ -185,6 +185,7 @@ _SIGNATURES = {
     "nmi_rt_memcpy_dtoh": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t]),
     "nmi_rt_memcpy_dtod": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, _STREAM]),
     "nmi_rt_fill_u8": (C.c_int, [C.c_void_p, C.c_uint8, C.c_size_t, _STREAM]),
+    "nmi_rt_next_row_i32": (C.c_int, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, _STREAM]),
     "nmi_rt_stream_create": (C.c_int, [P(C.c_void_p)]),
     "nmi_rt_stream_destroy": (C.c_int, [_STREAM]),
     "nmi_rt_stream_synchronize": (C.c_int, [_STREAM]),
@@ -197,6 +198,8 @@ _SIGNATURES = {
     "nmi_rt_capture_end": (C.c_int, [_STREAM, P(C.c_void_p)]),
     "nmi_rt_graph_launch": (C.c_int, [C.c_void_p, _STREAM]),
     "nmi_rt_graph_destroy": (C.c_int, [C.c_void_p]),
+    "nmi_rt_stream_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, _STREAM]),
+    "nmi_rt_read_ceiling": (C.c_int, [C.c_void_p, C.c_size_t, C.c_int32, C.c_void_p, _STREAM]),
 }
 
 _lib: C.CDLL | None = None

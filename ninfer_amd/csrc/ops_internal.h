@@ -59,10 +59,10 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
 size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T);
 
 // Size of the per-device static split scratch of nmi_gqa_attention_noalloc. 16 MiB holds every plan
-// of one sequence (T <= 32, any context, the registered geometries: at most 10.2 MiB, the 80-row
-// form at 40/8 heads and T = 16, 8 KV heads x 32 splits x 80 rows x 128 dims x 4 B plus the (m, l)
-// pairs) and of batches up to ~100 sequences at T <= 6 (64 sequences at T = 4: 8.1 MiB); larger
-// batches with several row chunks need more and are rejected.
+// of one sequence (T <= 32, any context, the registered geometries: at most 5.2 MiB, the 80-row
+// form at 40/8 heads and T = 16, 8 KV heads x 32 splits x 80 rows x 128 dims x 2 B of FP16 O / l
+// plus the FP32 (m, l) pairs) and of batches up to ~240 sequences at T <= 6 (64 sequences at T = 4:
+// 4.1 MiB); larger batches need more and are rejected.
 inline constexpr size_t kStaticScratchBytes = size_t{16} << 20;
 
 // The calling device's static scratch (resolved on first use per device); throws Unsupported when

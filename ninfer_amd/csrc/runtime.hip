@@ -16,6 +16,17 @@ __global__ void fill_u8_kernel(uint8_t* dst, uint8_t value, size_t bytes) {
     }
 }
 
+// Row (*counter mod rows) of a [rows, cols] table into dst, then *counter + 1. Every thread reads
+// the counter before thread 0 advances it (the barrier orders the read before the write).
+__global__ void next_row_i32_kernel(const int32_t* table, int32_t rows, int32_t cols, int32_t* counter,
+                                    int32_t* dst) {
+    const int32_t c = *counter;
+    const int32_t r = ((c % rows) + rows) % rows;
+    for (int i = threadIdx.x; i < cols; i += blockDim.x) { dst[i] = table[static_cast<int64_t>(r) * cols + i]; }
+    __syncthreads();
+    if (threadIdx.x == 0) { *counter = c + 1; }
+}
+
 } // namespace
 } // namespace nmi
 
@@ -75,6 +86,18 @@ int nmi_rt_fill_u8(void* dst, uint8_t value, size_t bytes, nmi_stream_t stream) 
         hipLaunchKernelGGL(nmi::fill_u8_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                            reinterpret_cast<hipStream_t>(stream), static_cast<uint8_t*>(dst), value, bytes);
         nmi::check_launch("fill_u8_kernel");
+    });
+}
+
+int nmi_rt_next_row_i32(const int32_t* table, int32_t rows, int32_t cols, int32_t* counter, int32_t* dst,
+                        nmi_stream_t stream) {
+    return guarded([&] {
+        if (table == nullptr || counter == nullptr || dst == nullptr || rows < 1 || cols < 1 || cols > 1024) {
+            throw nmi::InvalidArgument("next_row_i32: table, counter and dst must be non-null, rows >= 1, cols in [1, 1024]");
+        }
+        hipLaunchKernelGGL(nmi::next_row_i32_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream),
+                           table, rows, cols, counter, dst);
+        nmi::check_launch("next_row_i32_kernel");
     });
 }
 

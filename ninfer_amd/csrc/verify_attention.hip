@@ -93,6 +93,20 @@ __device__ __forceinline__ void wait_chunk(bool next_in_flight) {
 }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+// A partial O plane holds FP16 values: the merges load the 32-bit word holding element i and take
+// its half later (i & 1), so a batch of loads stays in flight (converting each value inside its
+// guarded load makes the compiler wait for that load before the next one).
+__device__ __forceinline__ uint32_t partial_o_word(const uint16_t* base, int64_t i) {
+    return reinterpret_cast<const uint32_t*>(base)[i >> 1];
+}
+__device__ __forceinline__ float partial_o_half(uint32_t w, int64_t i) {
+    return f16_bits_to_f32(static_cast<uint16_t>(w >> (16 * static_cast<uint32_t>(i & 1))));
+}
+__device__ __forceinline__ float partial_o_at(const uint16_t* base, int64_t i) {
+    return partial_o_half(partial_o_word(base, i), i);
+}
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
 struct AttnArgs {
@@ -107,8 +121,8 @@ struct AttnArgs {
     uint16_t* vs;
     uint16_t* kb; // BF16 cache planes (BF16 kernel only)
     uint16_t* vb;
-    float* part_o;  // [row chunk][KV head][split_slots][32][D]
-    float* part_ml; // [row chunk][KV head][split_slots][32][2]
+    uint16_t* part_o; // FP16 bits [row chunk][KV head][split_slots][rows][D], each row divided by its sum
+    float* part_ml;   // [row chunk][KV head][split_slots][rows][2]
     int32_t* seq_table; // B > 1: per sequence (first slot, split count), written by the partial launch
     int64_t code_seq;
     int64_t scale_seq;
@@ -856,13 +870,14 @@ __device__ __forceinline__ void append_row(const uint16_t* ksrc, const uint16_t*
 }
 
 // Merge the four waves' (m, l, O) through LDS (reusing the staging area) and write the
-// workgroup's partial: out_o [rows][D] (rows < R) and out_ml [rows][2] (log2-domain max, row sum).
+// workgroup's partial: out_o [rows][D] (rows < R), O / l in FP16 (a weighted mean of V' values, so
+// finite wherever V' is), and out_ml [rows][2] (log2-domain max, row sum l) in FP32.
 // Rows go through LDS 32 at a time (two 16-row tiles per batch). The combine is branch-free (a wave
 // that saw no visible key has m = -inf, weight 0 and zero accumulators) and every LDS read of a row
 // is issued before its first use. CACHED: ordinary stores instead of non-temporal ones.
 template <int NT, int D, bool CACHED, typename State>
 __device__ __forceinline__ void write_partial(const State& s, char* smem, int R, int wave, int c, int g,
-                                              float* out_o, float* out_ml, bool kmark = false) {
+                                              uint16_t* out_o, float* out_ml, bool kmark = false) {
     constexpr int kRowStride = D + 4;                       // floats; rows stay 16-byte aligned
     float* sm_o = reinterpret_cast<float*>(smem);           // [kWaves][32][kRowStride]
     float* sm_m = sm_o + kWaves * 32 * kRowStride;          // [32][kWaves]: one 16-byte read per row
@@ -930,17 +945,20 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
             }
             if (r >= rows) { continue; }
             const int row = rb + r;
+            const float inv = lsum > 0.0f ? __builtin_amdgcn_rcpf(lsum) : 0.0f;
+            const u2 oh = {static_cast<uint32_t>(f32_to_f16_bits(o[0] * inv)) | (static_cast<uint32_t>(f32_to_f16_bits(o[1] * inv)) << 16),
+                           static_cast<uint32_t>(f32_to_f16_bits(o[2] * inv)) | (static_cast<uint32_t>(f32_to_f16_bits(o[3] * inv)) << 16)};
             if (kmark) { lsum = -1.0f; } // a K scale of 512 or more: the merge recomputes this split
             // Read once, by the merge: non-temporal unless the plan routes long splits' partials
             // through the caches.
             if constexpr (CACHED) {
-                *reinterpret_cast<f4*>(out_o + row * D + d4) = o;
+                *reinterpret_cast<u2*>(out_o + row * D + d4) = oh;
                 if (d4 == 0) {
                     out_ml[2 * row] = M;
                     out_ml[2 * row + 1] = lsum;
                 }
             } else {
-                __builtin_nontemporal_store(o, reinterpret_cast<f4*>(out_o + row * D + d4));
+                __builtin_nontemporal_store(oh, reinterpret_cast<u2*>(out_o + row * D + d4));
                 if (d4 == 0) {
                     __builtin_nontemporal_store(M, out_ml + 2 * row);
                     __builtin_nontemporal_store(lsum, out_ml + 2 * row + 1);
@@ -1126,7 +1144,7 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     const int hend = fused ? min(k1, L) : k1;
     const bool owner = fused && L >= k0 && L < kend && L < window;
     const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot;
-    float* out_o = a.part_o + pidx * (RMAX * D);
+    uint16_t* out_o = a.part_o + pidx * (RMAX * D);
     float* out_ml = a.part_ml + pidx * (2 * RMAX);
 
 
@@ -1632,7 +1650,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int hend = fused ? min(k1, L) : k1;
     const bool owner = fused && L >= k0 && L < k0 + kps && L < window;
     const int64_t pidx = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + slot0 + split;
-    float* out_o = a.part_o + pidx * (32 * D);
+    uint16_t* out_o = a.part_o + pidx * (32 * D);
     float* out_ml = a.part_ml + pidx * 64;
     if (k0 >= hend && !owner) {
         __builtin_amdgcn_s_waitcnt(0);
@@ -1751,7 +1769,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 }
 
 struct MergeArgs {
-    const float* part_o;
+    const uint16_t* part_o; // FP16 O / l
+
     const float* part_ml;
     void* out;
     int32_t T;
@@ -1932,7 +1951,7 @@ __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0
         const int64_t slot = slot0 + first + j;
         float ms = a.part_ml[slot * (2 * rps) + 2 * r];
         float ls = a.part_ml[slot * (2 * rps) + 2 * r + 1];
-        float od = tid < 32 ? a.part_o[slot * (static_cast<int64_t>(rps) * D) + static_cast<int64_t>(r) * D + d0 + tid] : 0.0f;
+        float od = tid < 32 ? partial_o_at(a.part_o, slot * (static_cast<int64_t>(rps) * D) + static_cast<int64_t>(r) * D + d0 + tid) : 0.0f;
         const bool nonfin = tid < 32 && ls > 0.0f && !__builtin_isfinite(od);
         __syncthreads();
         if (tid < 64) {
@@ -1941,7 +1960,11 @@ __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0
         }
         __syncthreads();
         const bool redo = a.kc != nullptr && (ls < 0.0f || !__builtin_isfinite(ls) || xi[9] != 0);
-        if (redo) { exact_split<D>(a, b, t, qh, j * kps, j * kps + kps, d0, xs, ms, ls, od); }
+        if (redo) {
+            exact_split<D>(a, b, t, qh, j * kps, j * kps + kps, d0, xs, ms, ls, od);
+        } else {
+            od *= ls; // the stored O / l back to O
+        }
         if (ls > 0.0f) {
             const float Mn = fmaxf(M, ms);
             const float al = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
@@ -1991,18 +2014,18 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots;
     constexpr int rps = RPS; // rows per partial slot (the launch's plan.rows_per_slot)
     const float* ml = a.part_ml + slot0 * (2 * rps);
-    const float* po = a.part_o + slot0 * (rps * D);
+    const uint16_t* po = a.part_o + slot0 * (rps * D);
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int sg = tid / kMergeDims;
     const int d = blockIdx.y * kMergeDims + (tid - sg * kMergeDims);
 
-    float pre[kMergePre];
+    uint32_t pre[kMergePre]; // FP16 words, converted at use
 #pragma unroll
     for (int k = 0; k < kMergePre; ++k) {
         const int s = sg + kMergeGroups * k;
-        pre[k] = s < nsplit ? ld(po + static_cast<int64_t>(s) * rps * D + r * D + d) : 0.0f;
+        pre[k] = s < nsplit ? partial_o_word(po, static_cast<int64_t>(s) * rps * D + r * D + d) : 0u;
     }
     float M = -INFINITY;
     bool redo = false; // a split the fast path could not hold (marked, or non-finite)
@@ -2022,7 +2045,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     float lsum = 0.0f;
     for (int s = tid; s < nsplit; s += kMergeThreads) {
         const float w = (M != -INFINITY && wts[s] != -INFINITY) ? __builtin_amdgcn_exp2f(wts[s] - M) : 0.0f;
-        wts[s] = w;
+        wts[s] = w * lw[s]; // the weight of the split's O / l
         lsum = fmaf(lw[s], w, lsum);
     }
     lsum = wave_sum(lsum);
@@ -2038,13 +2061,14 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
         for (int k = 0; k < kMergePre; ++k) {
             const int s = sg + kMergeGroups * k;
             if (s < nsplit) {
-                redo |= wts[s] != 0.0f && !__builtin_isfinite(pre[k]);
-                o = wts[s] != 0.0f ? fmaf(pre[k], wts[s], o) : o;
+                const float v = partial_o_half(pre[k], d);
+                redo |= wts[s] != 0.0f && !__builtin_isfinite(v);
+                o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
             }
         }
 #pragma unroll 4
         for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
-            const float v = ld(po + static_cast<int64_t>(s) * rps * D + r * D + d);
+            const float v = partial_o_at(po, static_cast<int64_t>(s) * rps * D + r * D + d);
             redo |= wts[s] != 0.0f && !__builtin_isfinite(v);
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
@@ -2098,7 +2122,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
     const int64_t slot0 = (static_cast<int64_t>(rc) * a.Hkv + h) * a.split_slots + first;
     const int rps = a.rows_per_slot;
     const float* ml = a.part_ml + slot0 * (2 * rps) + 2 * r;
-    const float* po = a.part_o + slot0 * (rps * D) + r * D + d;
+    const uint16_t* po = a.part_o + slot0 * (rps * D) + r * D + (d & ~1); // whole words: d & 1 picks the half
     float M = -INFINITY;
     float lsum = 0.0f;
     float o = 0.0f;
@@ -2107,23 +2131,24 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_rows_kernel(M
 #pragma unroll 1
     for (int s0 = 0; s0 < nsplit; s0 += kBatch) {
         float2 mlv[kBatch];
-        float ov[kBatch];
+        uint32_t ow[kBatch]; // FP16 words, converted at use
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
             const int s = s0 + k;
             mlv[k] = s < nsplit ? *reinterpret_cast<const float2*>(ml + static_cast<int64_t>(s) * (2 * rps)) : float2{-INFINITY, 0.0f};
-            ov[k] = s < nsplit ? po[static_cast<int64_t>(s) * rps * D] : 0.0f;
+            ow[k] = s < nsplit ? partial_o_word(po, static_cast<int64_t>(s) * rps * D + (d & 1)) : 0u;
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
+            const float ov = partial_o_half(ow[k], d);
             redo |= s0 + k < nsplit && (mlv[k].y < 0.0f || !__builtin_isfinite(mlv[k].y) ||
-                                        (mlv[k].y > 0.0f && !__builtin_isfinite(ov[k])));
+                                        (mlv[k].y > 0.0f && !__builtin_isfinite(ov)));
             // A split with no visible key never wrote its partial rows: skip it.
             if (!(mlv[k].y > 0.0f)) { continue; }
             const float mn = fmaxf(M, mlv[k].x);
             const float alpha = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
             const float beta = __builtin_amdgcn_exp2f(mlv[k].x - mn);
-            o = fmaf(o, alpha, ov[k] * beta);
+            o = fmaf(o, alpha, ov * (mlv[k].y * beta));
             lsum = fmaf(lsum, alpha, mlv[k].y * beta);
             M = mn;
         }
@@ -2292,7 +2317,7 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
                         p.keys_per_split >= kAttnCachedPartialKeys;
     const size_t part_units = static_cast<size_t>(cols) * p.split_slots;
     p.part_o_offset = 0;
-    const size_t o_bytes = part_units * p.rows_per_slot * static_cast<size_t>(D) * sizeof(float);
+    const size_t o_bytes = part_units * p.rows_per_slot * static_cast<size_t>(D) * sizeof(uint16_t); // FP16 O / l
     p.part_ml_offset = (o_bytes + 255) & ~static_cast<size_t>(255);
     const size_t ml_bytes = part_units * 2 * p.rows_per_slot * sizeof(float);
     p.seq_table_offset = (p.part_ml_offset + ml_bytes + 255) & ~static_cast<size_t>(255);
@@ -2364,7 +2389,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     a.vb = c.vb;
     a.ks = c.ks;
     a.vs = c.vs;
-    a.part_o = reinterpret_cast<float*>(ws + plan.part_o_offset);
+    a.part_o = reinterpret_cast<uint16_t*>(ws + plan.part_o_offset);
     a.part_ml = reinterpret_cast<float*>(ws + plan.part_ml_offset);
     a.seq_table = reinterpret_cast<int32_t*>(ws + plan.seq_table_offset);
     a.code_seq = c.code_seq;

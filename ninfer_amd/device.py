@@ -189,6 +189,29 @@ def copy_array(dst: "DeviceArray", src: "DeviceArray", stream: Stream | None = N
                                    stream.handle if stream else None))
 
 
+def next_row_i32(table: "DeviceArray", counter: "DeviceArray", dst: "DeviceArray", stream: Stream | None = None) -> None:
+    """dst <- row (counter mod rows) of the int32 table (shape (cols, rows), rows contiguous), then
+    counter + 1 (on the device)."""
+    cols, rows = table.shape[0], table.shape[1]
+    check(lib().nmi_rt_next_row_i32(C.c_void_p(table.ptr), rows, cols, C.c_void_p(counter.ptr), C.c_void_p(dst.ptr),
+                                    stream.handle if stream else None))
+
+
+READ_VECTOR, READ_LDS_DMA = 0, 1
+
+
+def stream_copy(dst_ptr: int, src_ptr: int, nbytes: int, stream: Stream | None = None) -> None:
+    """Copy-ceiling control: one launch of 16-byte loads and stores over `nbytes`."""
+    check(lib().nmi_rt_stream_copy(C.c_void_p(dst_ptr), C.c_void_p(src_ptr), nbytes,
+                                   stream.handle if stream else None))
+
+
+def read_ceiling(src_ptr: int, nbytes: int, form: int, sink: DeviceBuffer, stream: Stream | None = None) -> None:
+    """Read-ceiling control: one launch that reads `nbytes` (READ_VECTOR or READ_LDS_DMA)."""
+    check(lib().nmi_rt_read_ceiling(C.c_void_p(src_ptr), nbytes, form, C.c_void_p(sink.ptr),
+                                    stream.handle if stream else None))
+
+
 def memcpy_dtod(dst: DeviceBuffer, src: DeviceBuffer, nbytes: int, stream: Stream | None = None) -> None:
     """Stream-ordered device-to-device copy of `nbytes` (hipMemcpyAsync)."""
     assert nbytes <= dst.nbytes and nbytes <= src.nbytes

@@ -11,7 +11,7 @@ import pytest
 
 import ninfer_amd as na
 from ninfer_amd import ops
-from ninfer_amd._capi import Tensor, lib
+from ninfer_amd._capi import INVALID_ARGUMENT, Tensor, lib
 
 ROOT = Path(__file__).resolve().parent.parent
 
@@ -413,10 +413,10 @@ def test_workspace_bound_covers_every_envelope(q_heads, kv_heads, head_dim):
 
 def test_static_scratch_holds_every_batch1_plan():
     """The allocation-free entry's 16 MiB static scratch holds the largest batch-1 plan of every
-    registered geometry and T <= 32 (10.2 MiB: the 80-row form at 40/8 heads, T = 16)."""
+    registered geometry and T <= 32 (5.2 MiB: the 80-row form at 40/8 heads, T = 16)."""
     worst = max(ops.gqa_attention_workspace_bound(qh, T) for qh in (40, 24, 16) for T in range(1, 33))
     assert worst == ops.gqa_attention_workspace_bound(40, 16)
-    assert 10 << 20 < worst <= 16 << 20
+    assert 5 << 20 < worst <= 16 << 20
 
 
 def test_workspace_bound_reference_call_shapes():
@@ -497,3 +497,16 @@ def test_compiled_cpp_layer_maps_statuses_to_reference_exceptions():
     r = subprocess.run([str(_driver()), "errors"], capture_output=True, text=True, timeout=60)
     print(r.stdout)
     assert r.returncode == 0 and "ERRORS PASS" in r.stdout, r.stdout + r.stderr
+
+
+def test_runtime_helper_validation():
+    L = lib()
+    fake = C.c_void_p(1 << 20)
+    # host checks reject before any launch
+    assert L.nmi_rt_stream_copy(fake, fake, 17, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_stream_copy(None, fake, 16, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_read_ceiling(fake, 24, 0, fake, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_read_ceiling(fake, 32, 7, fake, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_next_row_i32(None, 4, 3, fake, fake, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_next_row_i32(fake, 0, 3, fake, fake, None) == INVALID_ARGUMENT
+    assert L.nmi_rt_next_row_i32(fake, 4, 1025, fake, fake, None) == INVALID_ARGUMENT
