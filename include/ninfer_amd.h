@@ -160,13 +160,16 @@ size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int3
  * (include/ninfer/ops/gqa_attention.h:50; src/ops/wrapper/gqa_attention.cpp:229-245), as a status
  * plus the size: the geometry follows from q_heads (24 -> 4 KV heads and 16 -> 2 at head_dim 256,
  * the reference's registered ones; 40 -> 8 at head_dim 128), and the size covers every execution
- * envelope of one sequence. tokens <= 0 or above 32 give 0; other q_heads NMI_INVALID_ARGUMENT. */
+ * envelope of one sequence (above 32 tokens: the prompt route's launches of 32 and its last one).
+ * tokens <= 0 give 0; other q_heads NMI_INVALID_ARGUMENT. */
 int nmi_gqa_attention_workspace_bound(int32_t q_heads, int32_t tokens, size_t* bytes);
 
 /* A1, replaces gqa_attention (include/ninfer/ops/gqa_attention.h:71-73): quantize-append the T
  * new K/V columns at rows positions[t] and compute causal GQA over rows [0, positions[t]].
  * q/out BF16 [D, Hq, T(, B)]; k/v BF16 [D, Hkv, T(, B)]; positions I32 [T(, B)] sequential;
- * out may also be FP32 (EXTENSION). */
+ * out may also be FP32 (EXTENSION). T above 32 is the reference's prompt route
+ * (src/ops/wrapper/gqa_attention.cpp:202-213): one sequence (B = 1); the rows are appended first,
+ * then the tokens attend in launches of 32 through the same workspace. */
 int nmi_gqa_attention(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
                       const nmi_tensor* positions, float scale, const nmi_kv_layer_view* cache,
                       nmi_gqa_envelope envelope, void* workspace, size_t workspace_bytes,
@@ -196,7 +199,7 @@ int nmi_gqa_attention_cached(const nmi_tensor* q, const nmi_tensor* positions, f
  * -1, parents[u] < u. Node u occupies row positions[u]; query t sees history rows
  * [0, positions[0]) and the new rows of its ancestors-or-self. A parent outside [0, u) ends the
  * ancestor walk there (nmi_tree_accept_greedy treats it the same way). write_cache = 0 gives A3
- * (k and v may then be NULL). T above 32 returns NMI_UNSUPPORTED, as for A1 and A3. */
+ * (k and v may then be NULL). T above 32 returns NMI_UNSUPPORTED (the mask is 32 bits per row). */
 int nmi_gqa_attention_tree(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
                            const nmi_tensor* positions, const nmi_tensor* parents, float scale,
                            const nmi_kv_layer_view* cache, nmi_gqa_envelope envelope,

@@ -4,6 +4,7 @@
 #include "common.h"
 #include "ops_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <limits>
 #include <string>
@@ -137,11 +138,11 @@ AttnShape validate_attention(const nmi_tensor* q, const nmi_tensor* positions,
     s.Hkv = cache->num_kv_heads;
     s.out_f32 = out->dtype == NMI_FP32;
     require(s.T > 0, op, "T must be positive");
-    if (s.T > kAttnMaxTokens) {
-        // the reference serves larger T by its prompt route; this build serves verify rounds only
-        throw Unsupported(op + ": T above 32 query tokens (the prompt route) is not built");
-    }
     require(s.B > 0, op, "batch must be positive");
+    if (s.T > kAttnMaxTokens && s.B != 1) {
+        // the reference's prompt route (T beyond the verify extents) takes one sequence
+        throw Unsupported(op + ": T above 32 query tokens (the prompt route) serves one sequence");
+    }
     require(s.Hkv > 0 && s.Hq > 0 && s.Hq % s.Hkv == 0, op, "unsupported Q/KV head geometry");
     require(s.Hq / s.Hkv <= kAttnRowsPerTile, op, "unsupported Q/KV head geometry");
     require(s.D == cache->head_dim, op, "q head_dim does not match the cache");
@@ -178,6 +179,19 @@ void require_workspace(void* ws, size_t bytes, size_t need, const std::string& o
     require((reinterpret_cast<uintptr_t>(ws) & 255u) == 0, op, "workspace must be 256-byte aligned");
 }
 
+// The prompt route (reference src/ops/wrapper/gqa_attention.cpp:202-213,262-275: T beyond the verify
+// extents, one sequence, causal): the new rows are written first (A2), then the query tokens attend
+// over the cache in launches of at most kAttnMaxTokens consecutive tokens. Each launch is a verify
+// problem of its own: its first position is the history boundary, rows below it (earlier prompt
+// tokens included) are visible to all its tokens, and its own rows are masked causally. One
+// workspace serves the launches one after another (stream order).
+struct PromptChunks {
+    int32_t full = 0; // launches of kAttnMaxTokens tokens
+    int32_t tail = 0; // tokens of the last, shorter launch (0: none)
+};
+
+PromptChunks prompt_chunks(int32_t T) { return PromptChunks{T / kAttnMaxTokens, T % kAttnMaxTokens}; }
+
 // static_ws: the split partials go to the device's static scratch (the allocation-free entry
 // point); ws/ws_bytes are then ignored.
 int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v,
@@ -197,10 +211,40 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
         require_built(c, op);
         // The 80-row form (INT8, head_dim 128) unless the static scratch of the allocation-free entry
         // cannot hold its partials.
-        SplitPlan plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys, c.kb == nullptr);
-        if (static_ws && plan.bytes > kStaticScratchBytes && plan.rows_per_slot != kAttnRowsPerTile) {
-            plan = plan_attention(s.Hq, s.Hkv, s.D, s.T, s.B, env.max_visible_keys, false);
+        const auto make_plan = [&](int32_t T) {
+            SplitPlan p = plan_attention(s.Hq, s.Hkv, s.D, T, s.B, env.max_visible_keys, c.kb == nullptr);
+            if (static_ws && p.bytes > kStaticScratchBytes && p.rows_per_slot != kAttnRowsPerTile) {
+                p = plan_attention(s.Hq, s.Hkv, s.D, T, s.B, env.max_visible_keys, false);
+            }
+            return p;
+        };
+        if (s.T > kAttnMaxTokens) {
+            if (parents != nullptr) { throw Unsupported(op + ": ancestor masks serve at most 32 query tokens"); }
+            const PromptChunks pc = prompt_chunks(s.T);
+            const SplitPlan full = make_plan(kAttnMaxTokens);
+            const SplitPlan last = pc.tail > 0 ? make_plan(pc.tail) : full;
+            const size_t need = std::max(full.bytes, last.bytes);
+            if (static_ws) {
+                ws = static_scratch(need, op);
+                ws_bytes = need;
+            }
+            require_workspace(ws, ws_bytes, need, op);
+            if (write_cache) {
+                launch_kv_append(static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
+                                 static_cast<const int32_t*>(positions->data), nullptr, CommitBounds{}, s.T, c, stream);
+            }
+            const size_t out_elem = s.out_f32 ? 4 : 2;
+            for (int32_t t0 = 0; t0 < s.T; t0 += kAttnMaxTokens) {
+                const int32_t Tc = std::min(kAttnMaxTokens, s.T - t0);
+                const size_t off = static_cast<size_t>(t0) * s.Hq * s.D; // [D, Hq, T]: token-major
+                launch_verify_attention(static_cast<const uint16_t*>(q->data) + off, nullptr, nullptr,
+                                        static_cast<const int32_t*>(positions->data) + t0, nullptr, Tc, s.Hq, c,
+                                        scale, env.max_visible_keys, ws, Tc == kAttnMaxTokens ? full : last,
+                                        static_cast<char*>(out->data) + off * out_elem, s.out_f32, stream);
+            }
+            return;
         }
+        SplitPlan plan = make_plan(s.T);
         if (static_ws) {
             ws = static_scratch(plan.bytes, op);
             ws_bytes = plan.bytes;
@@ -285,14 +329,21 @@ const char* nmi_build_info(void) {
 size_t nmi_gqa_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                                          int32_t tokens, int32_t batch,
                                          uint32_t max_visible_keys) {
-    // 0 for invalid shapes and for T above 32 (no built route: the op itself reports NMI_UNSUPPORTED)
-    if (tokens <= 0 || tokens > kAttnMaxTokens || batch <= 0 || kv_heads <= 0 || q_heads <= 0 ||
-        q_heads % kv_heads != 0 || head_dim <= 0 || max_visible_keys == 0 || q_heads / kv_heads > kAttnRowsPerTile) {
+    // 0 for invalid shapes and for batches above 32 tokens (no built route: the op itself reports
+    // NMI_UNSUPPORTED)
+    if (tokens <= 0 || batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads != 0 || head_dim <= 0 ||
+        max_visible_keys == 0 || q_heads / kv_heads > kAttnRowsPerTile || (tokens > kAttnMaxTokens && batch != 1)) {
         return 0;
     }
-    // the cache type is not an argument: the larger of the two row forms
-    return std::max(plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys, true).bytes,
-                    plan_attention(q_heads, kv_heads, head_dim, tokens, batch, max_visible_keys, false).bytes);
+    // the cache type is not an argument: the larger of the two row forms; the prompt route reuses one
+    // workspace for its launches of 32 tokens and its shorter last launch
+    const auto bytes = [&](int32_t T) {
+        return std::max(plan_attention(q_heads, kv_heads, head_dim, T, batch, max_visible_keys, true).bytes,
+                        plan_attention(q_heads, kv_heads, head_dim, T, batch, max_visible_keys, false).bytes);
+    };
+    if (tokens <= kAttnMaxTokens) { return bytes(tokens); }
+    const PromptChunks pc = prompt_chunks(tokens);
+    return std::max(bytes(kAttnMaxTokens), pc.tail > 0 ? bytes(pc.tail) : size_t{0});
 }
 
 // reference gqa_attention_workspace_bytes(q_heads, tokens) (src/ops/wrapper/gqa_attention.cpp:229-245):
@@ -303,8 +354,8 @@ int nmi_gqa_attention_workspace_bound(int32_t q_heads, int32_t tokens, size_t* b
     return guarded([&] {
         require(bytes != nullptr, op, "bytes must be non-null");
         *bytes = 0;
-        // T <= 0 needs nothing (as in the reference); T above 32 runs no route of this build.
-        if (tokens <= 0 || tokens > kAttnMaxTokens) { return; }
+        // T <= 0 needs nothing (as in the reference)
+        if (tokens <= 0) { return; }
         int32_t kv_heads = 0, head_dim = 0;
         switch (q_heads) {
         case 24: kv_heads = 4; head_dim = 256; break;
@@ -312,7 +363,13 @@ int nmi_gqa_attention_workspace_bound(int32_t q_heads, int32_t tokens, size_t* b
         case 40: kv_heads = 8; head_dim = 128; break;
         default: throw InvalidArgument(op + ": unsupported Q/KV head geometry");
         }
-        *bytes = attention_workspace_bound(q_heads, kv_heads, head_dim, tokens);
+        if (tokens <= kAttnMaxTokens) {
+            *bytes = attention_workspace_bound(q_heads, kv_heads, head_dim, tokens);
+        } else { // the prompt route's launches of 32 tokens and its shorter last launch
+            const PromptChunks pc = prompt_chunks(tokens);
+            *bytes = std::max(attention_workspace_bound(q_heads, kv_heads, head_dim, kAttnMaxTokens),
+                              pc.tail > 0 ? attention_workspace_bound(q_heads, kv_heads, head_dim, pc.tail) : size_t{0});
+        }
     });
 }
 

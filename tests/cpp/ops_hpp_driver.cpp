@@ -63,7 +63,7 @@ int run_errors() {
     const std::size_t mtp = ops::gqa_attention_workspace_bytes(24, 1);
     const std::size_t prompt = ops::gqa_attention_workspace_bytes(24, 2048);
     std::printf("workspace 40x4=%zu 24x1=%zu 24x2048=%zu\n", verify, mtp, prompt);
-    if (verify == 0 || mtp == 0 || prompt != 0) { ++failures; }
+    if (verify == 0 || mtp == 0 || prompt != ops::gqa_attention_workspace_bytes(24, 32)) { ++failures; }
     expect_throw<std::invalid_argument>("workspace geometry", [] { (void)ops::gqa_attention_workspace_bytes(36, 4); });
 
     std::vector<unsigned char> arena_mem(verify + 4096);
@@ -81,9 +81,9 @@ int run_errors() {
     expect_throw<std::overflow_error>("padded_context above int32", [&] {
         ops::gqa_attention(q, k, k, pos, scale, fake_cache(0x80000000u, 0x7FFFFFFFu), {1, 4100}, arena, out, nullptr);
     });
-    Tensor q33(fake(0x10000), DType::BF16, {128, 40, 33}), k33(fake(0x10000), DType::BF16, {128, 8, 33});
-    Tensor pos33(fake(0x10000), DType::I32, {33}), out33(fake(0x10000), DType::BF16, {128, 40, 33});
-    expect_throw<std::runtime_error>("prompt route (T = 33) not built", [&] {
+    Tensor q33(fake(0x10000), DType::BF16, {128, 40, 33, 2}), k33(fake(0x10000), DType::BF16, {128, 8, 33, 2});
+    Tensor pos33(fake(0x10000), DType::I32, {33, 2}), out33(fake(0x10000), DType::BF16, {128, 40, 33, 2});
+    expect_throw<std::runtime_error>("prompt route (T = 33) for two sequences", [&] {
         ops::gqa_attention(q33, k33, k33, pos33, scale, fake_cache(4224, 4100), {1, 4100}, arena, out33, nullptr);
     });
     expect_throw<std::invalid_argument>("arena too small for the envelope", [&] {

@@ -92,14 +92,32 @@ def test_gqa_attention_validation(override, needle):
                           a["out"])
 
 
-def test_gqa_attention_prompt_route_is_unsupported():
-    """T above 32 is valid for the reference (its prompt route, gqa_attention.h:59-60) but not built
-    here: NMI_UNSUPPORTED (NotImplementedError), not an invalid argument."""
-    a, ws = _attention_args(q=_t(na.BF16, (128, 40, 33)), out=_t(na.BF16, (128, 40, 33)),
-                            k=_t(na.BF16, (128, 8, 33)), v=_t(na.BF16, (128, 8, 33)), positions=_t(na.I32, (33,)))
-    with pytest.raises(NotImplementedError, match="T above 32"):
+def test_gqa_attention_prompt_route_limits():
+    """T above 32 is the reference's prompt route (gqa_attention.h:59-60, one sequence, causal): a
+    batch of several sequences there is NMI_UNSUPPORTED (NotImplementedError), not an invalid
+    argument, and so is an ancestor mask above 32 tokens."""
+    a, ws = _attention_args(q=_t(na.BF16, (128, 40, 33, 2)), out=_t(na.BF16, (128, 40, 33, 2)),
+                            k=_t(na.BF16, (128, 8, 33, 2)), v=_t(na.BF16, (128, 8, 33, 2)),
+                            positions=_t(na.I32, (33, 2)))
+    with pytest.raises(NotImplementedError, match="prompt route"):
         ops.gqa_attention(a["q"], a["k"], a["v"], a["positions"], a["scale"], a["cache"], a["envelope"], ws,
                           a["out"])
+    a, ws = _attention_args(q=_t(na.BF16, (128, 40, 33)), out=_t(na.BF16, (128, 40, 33)),
+                            k=_t(na.BF16, (128, 8, 33)), v=_t(na.BF16, (128, 8, 33)), positions=_t(na.I32, (33,)))
+    with pytest.raises(NotImplementedError, match="ancestor masks"):
+        ops.gqa_attention_tree(a["q"], a["k"], a["v"], a["positions"], _t(na.I32, (33,), 0x40000), a["scale"],
+                               a["cache"], a["envelope"], True, ws, a["out"])
+
+
+def test_prompt_route_workspace_sizes():
+    """Above 32 tokens one workspace serves the launches of 32 tokens and the shorter last one."""
+    for T, tail in ((33, 1), (64, 0), (100, 4), (4096, 0)):
+        want = max(ops.gqa_attention_workspace_bytes(40, 8, 128, 32, 1, 8192),
+                   ops.gqa_attention_workspace_bytes(40, 8, 128, tail, 1, 8192) if tail else 0)
+        assert ops.gqa_attention_workspace_bytes(40, 8, 128, T, 1, 8192) == want > 0
+        bound = max(ops.gqa_attention_workspace_bound(24, 32), ops.gqa_attention_workspace_bound(24, tail) if tail else 0)
+        assert ops.gqa_attention_workspace_bound(24, T) == bound > 0
+    assert ops.gqa_attention_workspace_bytes(40, 8, 128, 33, 2, 8192) == 0
 
 
 def test_gqa_attention_cache_validation():
@@ -425,7 +443,7 @@ def test_workspace_bound_reference_call_shapes():
     assert ops.gqa_attention_workspace_bound(24, 1) > 0
     assert ops.gqa_attention_workspace_bound(16, 4) > 0
     assert ops.gqa_attention_workspace_bound(40, 0) == 0
-    assert ops.gqa_attention_workspace_bound(24, 4096) == 0  # no built route above 32 tokens
+    assert ops.gqa_attention_workspace_bound(24, 4096) == ops.gqa_attention_workspace_bound(24, 32)  # prompt route
     with pytest.raises(ValueError, match="unsupported Q/KV head geometry"):
         ops.gqa_attention_workspace_bound(36, 4)
 
@@ -492,7 +510,7 @@ def _driver():
 def test_compiled_cpp_layer_maps_statuses_to_reference_exceptions():
     """include/ninfer_amd/ops.hpp compiled by hipcc as a reference caller would compile it: the
     (q_heads, tokens) workspace query of layouts_impl.h:152, std::invalid_argument /
-    std::overflow_error from host validation, and std::runtime_error for the unbuilt prompt route."""
+    std::overflow_error from host validation, and std::runtime_error for a batch on the prompt route."""
     import subprocess
     r = subprocess.run([str(_driver()), "errors"], capture_output=True, text=True, timeout=60)
     print(r.stdout)

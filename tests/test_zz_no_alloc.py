@@ -120,7 +120,8 @@ def _run(case, noalloc):
     return out.numpy(), cache.download()
 
 
-@pytest.mark.parametrize("calls", [[([7680], 4, 1), ([1000], 3, 2), ([3000, 17, 900, 5000], 4, 3)]])
+@pytest.mark.parametrize("calls", [[([7680], 4, 1), ([1000], 3, 2), ([3000, 17, 900, 5000], 4, 3),
+                                    ([1200], 70, 4), ([300], 4, 5)]])
 def test_noalloc_matches_workspace_form(gpu, calls):
     for Ls, T, seed in calls:
         print(f"case noalloc Ls={Ls} T={T}", flush=True)
