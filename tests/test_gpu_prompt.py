@@ -10,7 +10,7 @@ import pytest
 import ninfer_amd as na
 from ninfer_amd import ops
 from ninfer_amd.device import DeviceArray, DeviceBuffer, synchronize
-from helpers import AttnCase, rel_l2
+from helpers import AttnCase, reference_composite_ok, rel_l2
 import gpu_runner
 
 pytestmark = pytest.mark.gpu
@@ -80,3 +80,58 @@ def test_prompt_rows_match_verify_launches(gpu):
     synchronize()
     out_tail, _ = gpu_runner.run_attention(tail, out_f32=True, mode="A3", cache=cache, envelope=(1, case.max_context))
     assert np.array_equal(out_all.reshape(T, -1)[32:], out_tail.reshape(32, -1))
+
+
+# The reference's prompt-route matrix at its registered geometries (tests/ops/test_gqa_attention.cpp:
+# 1543-1546 INT8 prefill cases, 1564-1569 BF16 prefill cases, 1575-1576 the T = 1024 split-API
+# case), with its input distribution: Q and K uniform in [-0.25, 0.25), V in [-1, 1) (:778-782).
+GEOMETRIES = [(24, 4), (16, 2)]
+
+
+@pytest.mark.parametrize("Hq,Hkv", GEOMETRIES)
+@pytest.mark.parametrize("T,base", [(65, 0), (192, 0), (65, 384)])
+def test_prompt_reference_int8_cases(gpu, Hq, Hkv, T, base):
+    print(f"case prompt int8 {Hq}|{Hkv} T={T} base={base}", flush=True)
+    case = AttnCase([base], T=T, Hq=Hq, Hkv=Hkv, D=256, dist="uniform", seed=904 + T + base + Hq)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=False)
+    kc, vc, ks, vs = cache.download()
+    for got, want, name in zip((kc, vc, ks, vs), expected_cache, ("K codes", "V codes", "K scales", "V scales")):
+        assert np.array_equal(got, want), f"{name} differ"
+    _check(case, out, ref, REL_L2_BF16)
+    ok, msg = reference_composite_ok(out, ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("Hq,Hkv", GEOMETRIES)
+@pytest.mark.parametrize("T,base", [(128, 0), (512, 0), (128, 128), (512, 128), (65, 384)])
+def test_prompt_reference_bf16_cases(gpu, Hq, Hkv, T, base):
+    print(f"case prompt bf16 {Hq}|{Hkv} T={T} base={base}", flush=True)
+    case = AttnCase([base], T=T, Hq=Hq, Hkv=Hkv, D=256, kv="bf16", dist="uniform", seed=113 + T + base + Hq)
+    _, ref = case.oracle_after_append()
+    out, _ = gpu_runner.run_attention(case, out_f32=False)
+    _check(case, out, ref, REL_L2_BF16)
+    ok, msg = reference_composite_ok(out, ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("kv", ["i8", "bf16"])
+def test_prompt_final_row_against_a3(gpu, kv):
+    """A1 over a 1,024-token prompt at history 17, then A3 of the final token alone over the cache
+    that A2 filled: both equal the oracle's final row (the reference's split-API case with
+    final_row_only, :975-1060)."""
+    T, base, Hq, Hkv, D = 1024, 17, 24, 4, 256
+    case = AttnCase([base], T=T, Hq=Hq, Hkv=Hkv, D=D, kv=kv, dist="uniform", seed=1405)
+    _, ref = case.oracle_after_append()
+    out, _ = gpu_runner.run_attention(case, out_f32=True)
+    _check(case, out, ref, REL_L2_F32)
+    cache = gpu_runner.upload_cache(case)
+    gpu_runner.append(case, cache)
+    synchronize()
+    last = AttnCase([base], T=1, Hq=Hq, Hkv=Hkv, D=D, kv=kv, dist="uniform", seed=1405)
+    last.q = case.q[(T - 1) * Hq * D:]
+    last.positions = case.positions[T - 1:]
+    out1, _ = gpu_runner.run_attention(last, out_f32=True, mode="A3", cache=cache, envelope=(1, case.max_context))
+    ref_last = ref.reshape(T, -1)[T - 1]
+    _check(case, out1.reshape(-1), ref_last, REL_L2_F32)
+    _check(case, out.reshape(T, -1)[T - 1], ref_last, REL_L2_F32)
