@@ -793,7 +793,12 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
                     k[e] = sort_key(v, row);
                 }
             }
-            wave_top_cap(k, k, kCandidateCap, wcand, wout);
+            // the lane maxima bound the threshold: the cap largest of them leave a few dozen
+            // candidates, where all KPL keys per lane as heads cost KPL ballots per bit
+            uint64_t head[1] = {k[0]};
+#pragma unroll
+            for (int e = 1; e < KPL; ++e) { head[0] = max_u64(head[0], k[e]); }
+            wave_top_cap(k, head, kCandidateCap, wcand, wout);
             if (lane < kCandidateCap) {
                 a.cand[(static_cast<int64_t>(t) * gridDim.x + blockIdx.x) * kCandidateCap + lane] = wout[lane];
             }
