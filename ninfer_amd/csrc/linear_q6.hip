@@ -481,24 +481,33 @@ __global__ __launch_bounds__(64 * W) void linear_q6_kernel(LinearArgs a) {
     }
 }
 
-// ---- wide form: more than 16 columns, 32 per pass over the weight --------------------------------
+// ---- wide form: more than 16 columns, 32 or 64 per pass over the weight ---------------------------
 //
 // The column passes above re-stream the whole weight once per 4, 8 or 16 columns (x of 16 columns
 // at K = 5120 already fills the LDS). Here K is the outer loop: x moves through the LDS in blocks of
-// 256 (4 groups) for all 16 * NCB columns, and each wave keeps FP32 totals for its kWideTiles tiles x
+// 256 (4 groups) for all 16 * NCB columns, and each wave keeps FP32 totals for its MAXT tiles x
 // 16 * NCB columns in registers while it streams those tiles' 4-group chunks of the block. A lane
 // decodes its 16 codes of a group once and feeds NCB pairs of MFMAs (one per 16-column block).
 // Each x block carries its own power-of-two column factors (its largest |x| lands in
 // [2^14, 2^15), so its BF16 values are exact in FP16); a block's per-group sums, weighted by their
-// scales, are rescaled by the factor's exact inverse into the totals. The epilogue writes BF16
-// logits, argmax keys, or per column the workgroup's kCandidateCap largest keys (top-cap form).
+// scales, are rescaled by the factor's exact inverse into the totals. A workgroup runs ROUNDS
+// rounds over K, each for MAXT further tiles per wave, so 64 columns (128 totals per 8 tiles, more
+// than a lane has at two waves per SIMD) take 4 tiles per wave and two rounds: each code is decoded
+// once for all 64 columns. The epilogue of a round writes BF16 logits, folds argmax keys, or per
+// column merges the round's rows into the workgroup's kCandidateCap largest keys (top-cap form).
 constexpr int kWideWaves = 8;
 constexpr int kWideCG = 4;          // groups per streamed chunk and per x block (256 elements of K)
-constexpr int kWideTiles = 8;       // 16-row tiles per wave
 constexpr int kWideStages = 2;      // chunk stages per wave: kWideStages chunks in flight while one computes
 constexpr int kXBlockCol = kWideCG * 128; // bytes of one column of an x block (FP16)
-constexpr int kWideXBuffers = 4;    // x blocks in LDS: the pair in use and the next pair
-constexpr int kWideColumns = 32;    // columns per pass (two 16-column MFMA blocks)
+constexpr int kWideXBuffers = 3;    // x blocks in LDS: the block in use, the next, the one being staged
+constexpr int kWideTilesPerWave = 8; // tiles per wave over all rounds (every form: the same grid)
+
+// The two forms: 32 columns, 8 tiles per wave in one round; 64 columns, 4 tiles per wave per round.
+template <int NCB>
+struct WideForm {
+    static constexpr int kTiles = NCB == 2 ? 8 : 4;
+    static constexpr int kRounds = kWideTilesPerWave / kTiles;
+};
 
 template <int NCB>
 constexpr size_t wide_x_bytes() { return static_cast<size_t>(kWideXBuffers) * 16 * NCB * (kXBlockCol + 4); } // x blocks + factors
@@ -506,8 +515,8 @@ constexpr size_t wide_x_bytes() { return static_cast<size_t>(kWideXBuffers) * 16
 template <int NCB>
 constexpr size_t wide_lds_bytes() {
     constexpr size_t main = wide_x_bytes<NCB>() + static_cast<size_t>(kWideWaves) * kWideStages * Chunk<kWideCG>::kStage;
-    // top-cap epilogue: the workgroup's BF16 logits of every column, then the selection scratch
-    constexpr size_t keys = static_cast<size_t>(16 * NCB) * kWideWaves * kWideTiles * kTileRows * 2 +
+    // top-cap epilogue: the workgroup's BF16 logits of every column for one round, then the selection scratch
+    constexpr size_t keys = static_cast<size_t>(16 * NCB) * kWideWaves * WideForm<NCB>::kTiles * kTileRows * 2 +
                             static_cast<size_t>(kWideWaves) * (64 + kCandidateCap) * 8;
     return main > keys ? main : keys;
 }
@@ -516,12 +525,14 @@ template <int NCB>
 __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearArgs a) {
     constexpr int W = kWideWaves;
     constexpr int CG = kWideCG;
-    constexpr int MAXT = kWideTiles;
+    constexpr int MAXT = WideForm<NCB>::kTiles;
+    constexpr int ROUNDS = WideForm<NCB>::kRounds;
     constexpr int NC = 16 * NCB;      // columns of the pass
     constexpr int TPC = 64 * W / NC;  // x staging threads per column (consecutive lanes of one wave)
     constexpr int EPT = CG * 64 / TPC; // x elements of a block per staging thread
     constexpr int NX = EPT / 8;       // 16-byte x loads per staging thread
-    static_assert(MAXT % 2 == 0 && MAXT >= 3 && TPC <= 64, "wide geometry");
+    constexpr int S = kWideStages;
+    static_assert(MAXT % S == 0 && MAXT > S && TPC <= 64, "wide geometry");
     using CH = Chunk<CG>;
     extern __shared__ __attribute__((aligned(16))) char dsmem[];
     NMI_AS3 char* smem = (NMI_AS3 char*)dsmem;
@@ -529,7 +540,6 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
     NMI_AS3 float* finv = (NMI_AS3 float*)(smem + XB * NC * kXBlockCol); // [XB][NC] 1 / column factor
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    constexpr int S = kWideStages;
     NMI_AS3 char* ring = smem + wide_x_bytes<NCB>() + wave * S * CH::kStage;
     const int G = a.G;
     const int nkb = (G + CG - 1) / CG;
@@ -545,7 +555,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
     // reads zero), so every lane issues exactly NX loads.
     const int scol = threadIdx.x / TPC;
     const int spart = threadIdx.x - scol * TPC;
-    // The pass's own columns only (at most 8192 x 32 BF16 values), so the out-of-range offset lies
+    // The pass's own columns only (at most 8192 x 64 BF16 values), so the out-of-range offset lies
     // far past the resource whatever T is.
     const __amdgpu_buffer_rsrc_t xr_src = raw_buffer(a.x + static_cast<int64_t>(a.K) * a.t0, static_cast<int64_t>(a.K) * a.tp * 2);
     i4 xr[NX];
@@ -590,220 +600,221 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
         if (spart == 0) { finv[buf * NC + scol] = 1.0f / f; } // a power of two: exact
     };
 
-    // Blocks go in pairs: item j of pair p streams chunk 2p + (j & 1) of tile gw + (j / 2) * nwaves,
-    // so a tile's two chunks of the pair are consecutive items and the 128-byte lines of its high
-    // plane (64 bytes per chunk) are used whole while they are in L2. x block kb lives in buffer
-    // kb % 4: pair p computes on blocks 2p and 2p + 1 while blocks 2p + 2 and 2p + 3 are staged.
-    // Slots past the last tile and blocks past the last one still issue their DMAs (they read zero
-    // or bytes that are never used), so every wait below is one fixed count.
-    constexpr int J = 2 * MAXT; // items per pair
-    auto issue = [&](NMI_AS3 char* st, int p, int j) {
-        issue_item<CG>(st, pl, dl, gw + (j >> 1) * nwaves, 2 * p + (j & 1), G);
-    };
-    const int npairs = (nkb + 1) / 2;
-    auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
-    xload(0);
-#pragma unroll
-    for (int j = 0; j < S; ++j) { issue(ring + j * CH::kStage, 0, j); }
-    __builtin_amdgcn_s_waitcnt(((S * CH::kDma) & 0xf) | (((S * CH::kDma) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
-    xstage(0);
-    xload(clamp_block(1));
-    __builtin_amdgcn_s_waitcnt(0); // once per launch: block 1 lands behind the first items
-    xstage(1);
-
     const uint32_t kMaskA = 0x003f003fu;
     const uint32_t kConstB = 0x64206420u;
-    float tot[MAXT][NCB][4];
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) { tot[i][cb][r] = 0.0f; }
-        }
-    }
     // waits for item j: the S - 1 younger items stay in flight, and the x loads while they are younger
     constexpr int kYoung = (S - 1) * CH::kDma;
     constexpr int kWaitItem = (kYoung & 0xf) | ((kYoung >> 4) << 14) | (0x7 << 4) | (0xf << 8);
     constexpr int kWaitItemX = ((kYoung + NX) & 0xf) | (((kYoung + NX) >> 4) << 14) | (0x7 << 4) | (0xf << 8);
-    static_assert(J > 2 * S, "both x blocks of the next pair land inside the pair");
+    constexpr int RPW = MAXT * kTileRows; // rows per wave, column and round
+    NMI_AS3 uint16_t* lg = (NMI_AS3 uint16_t*)smem;
+
 #pragma unroll 1
-    for (int p = 0; p < npairs; ++p) {
-        __syncthreads(); // blocks 2p, 2p + 1 are in LDS; every wave is done with blocks 2p - 2, 2p - 1
-        // x loads of block 2p + 2: issued after items 0 .. S - 1, staged at item S; those of block
-        // 2p + 3: issued at item S after items .. 2S - 1, staged at item 2S
-        xload(clamp_block(2 * p + 2));
-        float fi[2][NCB];
+    for (int round = 0; round < ROUNDS; ++round) {
+        // This round's tiles of the wave: gw + (round * MAXT + j) * nwaves, j < MAXT.
+        const int tile0 = gw + round * MAXT * nwaves;
+        // Blocks go one after another: item j of block kb streams chunk kb of tile tile0 + j * nwaves.
+        // x block kb lives in buffer kb % XB: block kb computes while block kb + 1 sits staged, and
+        // block kb + 2 is loaded at the block's start and staged at item S, once its loads have
+        // landed. Slots past the last tile and the block past the last one still issue their DMAs
+        // (they read zero or bytes that are never used), so every wait below is one fixed count.
+        auto issue = [&](NMI_AS3 char* st, int kb, int j) { issue_item<CG>(st, pl, dl, tile0 + j * nwaves, kb, G); };
+        auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
+        xload(0);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int j = 0; j < S; ++j) { issue(ring + j * CH::kStage, 0, j); }
+        __builtin_amdgcn_s_waitcnt(((S * CH::kDma) & 0xf) | (((S * CH::kDma) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+        xstage(0);
+        xload(clamp_block(1));
+        __builtin_amdgcn_s_waitcnt(0); // once per round: block 1 lands behind the first items
+        xstage(1);
+
+        float tot[MAXT][NCB][4];
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) { fi[h][cb] = finv[((2 * p + h) & (XB - 1)) * NC + c + 16 * cb]; }
-        }
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int i = j >> 1;
-            const int h = j & 1;
-            const int kb = 2 * p + h;
-            NMI_AS3 char* st = ring + (j % S) * CH::kStage;
-            if (j < S || (j > S && j < 2 * S)) {
-                __builtin_amdgcn_s_waitcnt(kWaitItemX);
-            } else {
-                __builtin_amdgcn_s_waitcnt(kWaitItem);
-            }
-            if (j == S) {
-                xstage((2 * p + 2) & (XB - 1));
-                xload(clamp_block(2 * p + 3));
-            }
-            if (j == 2 * S) { xstage((2 * p + 3) & (XB - 1)); }
-            const NMI_AS3 char* xk = smem + (kb & (XB - 1)) * NC * kXBlockCol;
-            const int ng = min(CG, G - kb * CG); // <= 0 for the block past the last
-            float bacc[NCB][4];
+        for (int i = 0; i < MAXT; ++i) {
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) { bacc[cb][r] = 0.0f; }
+                for (int r = 0; r < 4; ++r) { tot[i][cb][r] = 0.0f; }
             }
-            uint64_t nib[CG];
-            uint32_t hig[CG];
-            uint32_t sc[4][CG / 2];
+        }
+        int buf = 0;      // kb % XB
+        int buf_next = 2; // (kb + 2) % XB
+#pragma unroll 1
+        for (int kb = 0; kb < nkb; ++kb) {
+            __syncthreads(); // blocks kb and kb + 1 are in LDS; every wave is done with block kb - 1
+            xload(clamp_block(kb + 2));
+            float fi[NCB];
 #pragma unroll
-            for (int gl = 0; gl < CG; ++gl) {
-                nib[gl] = *(const NMI_AS3 uint64_t*)(st + c * CH::kNibRow + 16 * ((2 * gl + (b >> 1)) ^ swz<CH::kNibRow>(c)) +
-                                                     8 * (b & 1));
-                hig[gl] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + c * CH::kHighRow + 16 * (gl ^ swz<CH::kHighRow>(c)) + 4 * b);
-            }
+            for (int cb = 0; cb < NCB; ++cb) { fi[cb] = finv[buf * NC + c + 16 * cb]; }
+            const NMI_AS3 char* xk = smem + buf * NC * kXBlockCol;
+            const int ng = min(CG, G - kb * CG);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int j = 0; j < MAXT; ++j) {
+                NMI_AS3 char* st = ring + (j % S) * CH::kStage;
+                if (j < S) {
+                    __builtin_amdgcn_s_waitcnt(kWaitItemX);
+                } else {
+                    __builtin_amdgcn_s_waitcnt(kWaitItem);
+                }
+                if (j == S) { xstage(buf_next); }
+                float bacc[NCB][4];
 #pragma unroll
-                for (int q = 0; q < CG / 2; ++q) {
-                    sc[r][q] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + CH::kHigh + (4 * b + r) * CH::kScaleRow + 4 * q);
+                for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) { bacc[cb][r] = 0.0f; }
+                }
+                uint64_t nib[CG];
+                uint32_t hig[CG];
+                uint32_t sc[4][CG / 2];
+#pragma unroll
+                for (int gl = 0; gl < CG; ++gl) {
+                    nib[gl] = *(const NMI_AS3 uint64_t*)(st + c * CH::kNibRow + 16 * ((2 * gl + (b >> 1)) ^ swz<CH::kNibRow>(c)) +
+                                                         8 * (b & 1));
+                    hig[gl] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + c * CH::kHighRow + 16 * (gl ^ swz<CH::kHighRow>(c)) + 4 * b);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                    for (int q = 0; q < CG / 2; ++q) {
+                        sc[r][q] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + CH::kHigh + (4 * b + r) * CH::kScaleRow + 4 * q);
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
+                if (j + S < MAXT) {
+                    issue(st, kb, j + S);
+                } else {
+                    issue(st, kb + 1, j + S - MAXT);
+                }
+#pragma unroll
+                for (int gl = 0; gl < CG; ++gl) {
+                    if (gl < ng) {
+                        h8 a0, a1;
+                        decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
+                        const int q0 = 8 * gl + 2 * b;
+#pragma unroll
+                        for (int cb = 0; cb < NCB; ++cb) {
+                            const NMI_AS3 char* xc = xk + (c + 16 * cb) * kXBlockCol;
+                            const i4 x0 = *(const NMI_AS3 i4*)(xc + 16 * (q0 ^ c));
+                            const i4 x1 = *(const NMI_AS3 i4*)(xc + 16 * ((q0 + 1) ^ c));
+                            f4 acc = {0.f, 0.f, 0.f, 0.f};
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const uint32_t w = sc[r][gl >> 1];
+                                const float sv = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
+                                bacc[cb][r] = fmaf(sv, acc[r], bacc[cb][r]);
+                            }
+                        }
+                    }
+                }
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) { tot[j][cb][r] = fmaf(bacc[cb][r], fi[cb], tot[j][cb][r]); }
                 }
             }
-            __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
-            if (j + S < J) {
-                issue(st, p, j + S);
-            } else {
-                issue(st, p + 1, j + S - J);
-            }
+            buf = buf == XB - 1 ? 0 : buf + 1;
+            buf_next = buf_next == XB - 1 ? 0 : buf_next + 1;
+        }
+        __builtin_amdgcn_s_waitcnt(0); // the DMAs of the items past the last block
+        __syncthreads();               // LDS is free for the epilogue
+
+        // ---- epilogue of the round: lane holds rows 4b + r of tile tile0 + i * nwaves for columns
+        // c + 16 cb. The top-cap form first puts the round's BF16 logits in LDS ([column][wave][tile
+        // slot][16 rows]).
+        uint64_t best[NCB]; // argmax keys of the round
 #pragma unroll
-            for (int gl = 0; gl < CG; ++gl) {
-                if (gl < ng) {
-                    h8 a0, a1;
-                    decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
-                    const int q0 = 8 * gl + 2 * b;
+        for (int cb = 0; cb < NCB; ++cb) { best[cb] = 0; }
 #pragma unroll
-                    for (int cb = 0; cb < NCB; ++cb) {
-                        const NMI_AS3 char* xc = xk + (c + 16 * cb) * kXBlockCol;
-                        const i4 x0 = *(const NMI_AS3 i4*)(xc + 16 * (q0 ^ c));
-                        const i4 x1 = *(const NMI_AS3 i4*)(xc + 16 * ((q0 + 1) ^ c));
-                        f4 acc = {0.f, 0.f, 0.f, 0.f};
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+        for (int i = 0; i < MAXT; ++i) {
+            const int r0 = (tile0 + i * nwaves) * kTileRows + 4 * b;
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                const int col = c + 16 * cb;
+                uint16_t bf[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    bf[r] = f32_to_bf16_bits(tot[i][cb][r]);
+                    if (a.keys != nullptr && r0 + r < a.valid_rows) { best[cb] = max_u64(best[cb], logit_key(bf[r], r0 + r)); }
+                }
+                const uint2 packed{static_cast<uint32_t>(bf[0]) | (static_cast<uint32_t>(bf[1]) << 16),
+                                   static_cast<uint32_t>(bf[2]) | (static_cast<uint32_t>(bf[3]) << 16)};
+                if (a.cand != nullptr) {
+                    *(NMI_AS3 i2*)(lg + (col * W + wave) * RPW + i * kTileRows + 4 * b) =
+                        i2{static_cast<int>(packed.x), static_cast<int>(packed.y)};
+                }
+                if (a.out != nullptr && col < a.tp) {
+                    uint16_t* o = a.out + static_cast<int64_t>(a.N) * (a.t0 + col) + r0;
+                    if (r0 + 4 <= a.N && (a.N & 3) == 0) { // 8-byte aligned
+                        *reinterpret_cast<uint2*>(o) = packed;
+                    } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const uint32_t w = sc[r][gl >> 1];
-                            const float sv = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
-                            bacc[cb][r] = fmaf(sv, acc[r], bacc[cb][r]);
+                            if (r0 + r < a.N) { o[r] = bf[r]; }
                         }
                     }
                 }
             }
-            if (ng > 0) {
+        }
+        if (a.keys != nullptr) {
+            // the wave's key per column over the rounds so far: folded into its own slot (the
+            // earlier round's value is this lane's own store)
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) { tot[i][cb][r] = fmaf(bacc[cb][r], fi[h][cb], tot[i][cb][r]); }
+            for (int cb = 0; cb < NCB; ++cb) {
+                uint64_t v = max_u64(best[cb], shfl_xor_u64(best[cb], 16));
+                v = max_u64(v, shfl_xor_u64(v, 32));
+                if (lane < 16 && c + 16 * cb < a.tp) {
+                    uint64_t* kslot = a.keys + static_cast<int64_t>(a.t0 + c + 16 * cb) * nwaves + gw;
+                    *kslot = round > 0 ? max_u64(v, *kslot) : v;
                 }
             }
         }
-    }
-    __builtin_amdgcn_s_waitcnt(0); // the DMAs of the items past the last block
-    __syncthreads();               // LDS is free for the epilogue
-
-    // ---- epilogue: lane holds rows 4b + r of tile gw + i * nwaves for columns c + 16 cb. The
-    // top-cap form first puts the workgroup's BF16 logits in LDS ([column][wave][tile slot][16 rows]).
-    constexpr int RPW = MAXT * kTileRows; // rows per wave and column
-    NMI_AS3 uint16_t* lg = (NMI_AS3 uint16_t*)smem;
-    uint64_t best[NCB];
+        if (a.cand != nullptr) {
+            // Top-cap form: wave w takes columns w, w + W, ...: the round's W * RPW keys of the
+            // column (penalty-adjusted logits of rows below valid_rows), KPL per lane, plus the
+            // workgroup's list from the earlier rounds (one key per lane below kCandidateCap, read
+            // back from its own candidate slot), then the kCandidateCap largest.
+            constexpr int KPL = W * RPW / 64; // keys per lane
+            uint64_t* wcand = (uint64_t*)(smem + NC * W * RPW * 2 + wave * 64 * 8);
+            uint64_t* wout = (uint64_t*)(smem + NC * W * RPW * 2 + W * 64 * 8 + wave * kCandidateCap * 8);
+            __syncthreads();
+#pragma unroll 1
+            for (int lc = wave; lc < a.tp; lc += W) {
+                const int t = a.t0 + lc;
+                const int hseq = t / a.cols_per_seq;
+                const int hcol = t - hseq * a.cols_per_seq;
+                const nmi_sampling_config& cf = a.config[hseq];
+                const bool hpen = cf.temperature > 0.0f && (cf.presence_penalty != 0.0f || cf.frequency_penalty != 0.0f);
+                uint64_t* slot_out = a.cand + (static_cast<int64_t>(t) * gridDim.x + blockIdx.x) * kCandidateCap;
+                uint64_t k[KPL + 1];
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) { best[cb] = 0; }
-#pragma unroll
-    for (int i = 0; i < MAXT; ++i) {
-        const int r0 = (gw + i * nwaves) * kTileRows + 4 * b;
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            const int col = c + 16 * cb;
-            uint16_t bf[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                bf[r] = f32_to_bf16_bits(tot[i][cb][r]);
-                if (r0 + r < a.valid_rows) { best[cb] = max_u64(best[cb], logit_key(bf[r], r0 + r)); }
-            }
-            const uint2 packed{static_cast<uint32_t>(bf[0]) | (static_cast<uint32_t>(bf[1]) << 16),
-                               static_cast<uint32_t>(bf[2]) | (static_cast<uint32_t>(bf[3]) << 16)};
-            if (a.cand != nullptr) {
-                *(NMI_AS3 i2*)(lg + (col * W + wave) * RPW + i * kTileRows + 4 * b) =
-                    i2{static_cast<int>(packed.x), static_cast<int>(packed.y)};
-            }
-            if (a.out != nullptr && col < a.tp) {
-                uint16_t* o = a.out + static_cast<int64_t>(a.N) * (a.t0 + col) + r0;
-                if (r0 + 4 <= a.N && (a.N & 3) == 0) { // 8-byte aligned
-                    *reinterpret_cast<uint2*>(o) = packed;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (r0 + r < a.N) { o[r] = bf[r]; }
+                for (int e = 0; e < KPL; ++e) {
+                    const int slot = (e % (RPW / 64)) * 64 + lane; // row slot within the origin wave
+                    const int wv = e / (RPW / 64);                 // origin wave
+                    const int row = ((blockIdx.x * W + wv) + (round * MAXT + slot / kTileRows) * nwaves) * kTileRows +
+                                    slot % kTileRows;
+                    k[e] = 0;
+                    if (row < a.valid_rows) { // the penalty counts cover the token domain only
+                        float v = bf16_to_f32(lg[(lc * W + wv) * RPW + slot]);
+                        if (hpen) { v = adjusted_logit(v, row, cf, a.drafts + static_cast<int64_t>(hseq) * (a.cols_per_seq - 1), hcol); }
+                        k[e] = sort_key(v, row);
                     }
                 }
+                // this wave wrote the slot in the earlier round (same column, same lanes)
+                k[KPL] = round > 0 && lane < kCandidateCap ? slot_out[lane] : 0ull;
+                // the lane maxima bound the threshold: the cap largest of them leave a few dozen
+                // candidates, where all keys per lane as heads cost one ballot per key and bit
+                uint64_t head[1] = {k[0]};
+#pragma unroll
+                for (int e = 1; e <= KPL; ++e) { head[0] = max_u64(head[0], k[e]); }
+                wave_top_cap(k, head, kCandidateCap, wcand, wout);
+                if (lane < kCandidateCap) { slot_out[lane] = wout[lane]; }
+                wave_lds_sync();
             }
         }
-    }
-    if (a.keys != nullptr) {
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            uint64_t v = max_u64(best[cb], shfl_xor_u64(best[cb], 16));
-            v = max_u64(v, shfl_xor_u64(v, 32));
-            if (lane < 16 && c + 16 * cb < a.tp) { a.keys[static_cast<int64_t>(a.t0 + c + 16 * cb) * nwaves + gw] = v; }
-        }
-    }
-    if (a.cand != nullptr) {
-        // Top-cap form: wave w takes columns w, w + W, ...: the column's W * RPW keys (penalty-adjusted
-        // logits of rows below valid_rows), 16 per lane, then the kCandidateCap largest.
-        constexpr int KPL = W * RPW / 64; // keys per lane
-        uint64_t* wcand = (uint64_t*)(smem + NC * W * RPW * 2 + wave * 64 * 8);
-        uint64_t* wout = (uint64_t*)(smem + NC * W * RPW * 2 + W * 64 * 8 + wave * kCandidateCap * 8);
-        __syncthreads();
-#pragma unroll 1
-        for (int lc = wave; lc < a.tp; lc += W) {
-            const int t = a.t0 + lc;
-            const int hseq = t / a.cols_per_seq;
-            const int hcol = t - hseq * a.cols_per_seq;
-            const nmi_sampling_config& cf = a.config[hseq];
-            const bool hpen = cf.temperature > 0.0f && (cf.presence_penalty != 0.0f || cf.frequency_penalty != 0.0f);
-            uint64_t k[KPL];
-#pragma unroll
-            for (int e = 0; e < KPL; ++e) {
-                const int slot = (e % (RPW / 64)) * 64 + lane; // row slot within the origin wave
-                const int wv = e / (RPW / 64);                 // origin wave
-                const int row = ((blockIdx.x * W + wv) + (slot / kTileRows) * nwaves) * kTileRows + slot % kTileRows;
-                k[e] = 0;
-                if (row < a.valid_rows) { // the penalty counts cover the token domain only
-                    float v = bf16_to_f32(lg[(lc * W + wv) * RPW + slot]);
-                    if (hpen) { v = adjusted_logit(v, row, cf, a.drafts + static_cast<int64_t>(hseq) * (a.cols_per_seq - 1), hcol); }
-                    k[e] = sort_key(v, row);
-                }
-            }
-            // the lane maxima bound the threshold: the cap largest of them leave a few dozen
-            // candidates, where all KPL keys per lane as heads cost KPL ballots per bit
-            uint64_t head[1] = {k[0]};
-#pragma unroll
-            for (int e = 1; e < KPL; ++e) { head[0] = max_u64(head[0], k[e]); }
-            wave_top_cap(k, head, kCandidateCap, wcand, wout);
-            if (lane < kCandidateCap) {
-                a.cand[(static_cast<int64_t>(t) * gridDim.x + blockIdx.x) * kCandidateCap + lane] = wout[lane];
-            }
-            wave_lds_sync();
-        }
+        __syncthreads(); // the next round's x and chunk stages reuse the LDS
     }
 }
 
@@ -848,16 +859,15 @@ constexpr int kInstanceCount = sizeof(kInstances) / sizeof(kInstances[0]);
 LinearPlan plan_linear(int32_t N, int32_t Kp, int32_t T, bool top_cap, int32_t K) {
     const int32_t ntiles = (N + kTileRows - 1) / kTileRows;
     constexpr size_t kLds = 160 * 1024;
-    const int32_t wide_grid = (ntiles + kWideWaves * kWideTiles - 1) / (kWideWaves * kWideTiles);
+    const int32_t wide_grid = (ntiles + kWideWaves * kWideTilesPerWave - 1) / (kWideWaves * kWideTilesPerWave);
     if (T > 16 && K % 8 == 0 && wide_grid <= kLinearGrid) {
-        // one pass over the weight per 32 columns (64 columns per pass need 128 FP32 totals per lane
-        // beside the streaming registers: more than the 256 a lane has at two waves per SIMD)
+        // one pass over the weight per 32 columns (T <= 32) or per 64 columns in two rounds (above)
         LinearPlan p{};
         p.wide = true;
-        p.tp = kWideColumns;
+        p.tp = T > 32 ? 64 : 32;
         p.waves = kWideWaves;
         p.cg = kWideCG;
-        p.lds = wide_lds_bytes<kWideColumns / 16>();
+        p.lds = p.tp == 64 ? wide_lds_bytes<4>() : wide_lds_bytes<2>();
         p.passes = (T + p.tp - 1) / p.tp;
         p.grid = wide_grid;
         return p;
@@ -934,7 +944,11 @@ void launch_linear_q6(LinearArgs a, const LinearPlan& p, hipStream_t stream) {
         for (int32_t pass = 0; pass < p.passes; ++pass) {
             a.t0 = pass * p.tp;
             a.tp = std::min(p.tp, a.T - a.t0);
-            launch_wide<kWideColumns / 16>(a, p, stream);
+            if (p.tp == 64) {
+                launch_wide<4>(a, p, stream);
+            } else {
+                launch_wide<2>(a, p, stream);
+            }
         }
         return;
     }
