@@ -54,13 +54,15 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The cap-th largest high word among the wave's M values per lane (0 = no value): the largest t
-// with at least cap values whose high word is >= t. 0 when fewer than cap values exist.
+// A threshold on the high words of the wave's M values per lane (0 = no value): the largest t
+// whose low 16 bits are zero with at least cap values whose high word is >= t (the cap-th largest
+// high word with its low half cleared; the high words of BF16 logits have no low half). 0 when
+// fewer than cap values exist.
 template <int M>
 __device__ __forceinline__ uint32_t wave_cap_high(const uint32_t (&hi)[M], int cap) {
     uint32_t t = 0;
 #pragma unroll 1
-    for (int bit = 31; bit >= 0; --bit) {
+    for (int bit = 31; bit >= 16; --bit) {
         const uint32_t c = t | (1u << bit);
         int n = 0;
 #pragma unroll
@@ -107,7 +109,16 @@ __device__ __forceinline__ bool wave_rank_top(const uint64_t (&k)[N], uint64_t T
     if (lane < total) {
         const uint64_t key = cand[lane];
         int r = 0;
-        for (int j = 0; j < total; ++j) { r += cand[j] > key ? 1 : 0; }
+        // eight LDS reads in flight per step (the 64 slots are the wave's own; those at or past
+        // total are not counted)
+#pragma unroll 1
+        for (int j0 = 0; j0 < total; j0 += 8) {
+            uint64_t cj[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { cj[u] = cand[(j0 + u) & 63]; }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) { r += (j0 + u < total && cj[u] > key) ? 1 : 0; }
+        }
         if (r < cap) { out[r] = key; }
     } else if (lane < cap) {
         out[lane] = 0;
