@@ -499,18 +499,21 @@ constexpr int kWideWaves = 8;
 constexpr int kWideCG = 4;          // groups per streamed chunk and per x block (256 elements of K)
 constexpr int kWideStages = 2;      // chunk stages per wave: kWideStages chunks in flight while one computes
 constexpr int kXBlockCol = kWideCG * 128; // bytes of one column of an x block (FP16)
-constexpr int kWideXBuffers = 3;    // x blocks in LDS: the block in use, the next, the one being staged
 constexpr int kWideTilesPerWave = 8; // tiles per wave over all rounds (every form: the same grid)
 
-// The two forms: 32 columns, 8 tiles per wave in one round; 64 columns, 4 tiles per wave per round.
+// The two forms: 32 columns, 8 tiles per wave in one round, x blocks consumed in pairs (four
+// buffers: the pair in use and the next pair); 64 columns, 4 tiles per wave per round, x blocks one
+// after another (three buffers, the most that fit beside the chunk stages at 64 columns).
 template <int NCB>
 struct WideForm {
     static constexpr int kTiles = NCB == 2 ? 8 : 4;
     static constexpr int kRounds = kWideTilesPerWave / kTiles;
+    static constexpr bool kPairs = NCB == 2;
+    static constexpr int kXBuffers = kPairs ? 4 : 3;
 };
 
 template <int NCB>
-constexpr size_t wide_x_bytes() { return static_cast<size_t>(kWideXBuffers) * 16 * NCB * (kXBlockCol + 4); } // x blocks + factors
+constexpr size_t wide_x_bytes() { return static_cast<size_t>(WideForm<NCB>::kXBuffers) * 16 * NCB * (kXBlockCol + 4); } // x blocks + factors
 
 template <int NCB>
 constexpr size_t wide_lds_bytes() {
@@ -519,6 +522,39 @@ constexpr size_t wide_lds_bytes() {
     constexpr size_t keys = static_cast<size_t>(16 * NCB) * kWideWaves * WideForm<NCB>::kTiles * kTileRows * 2 +
                             static_cast<size_t>(kWideWaves) * (64 + kCandidateCap) * 8;
     return main > keys ? main : keys;
+}
+
+// One item's per-group sums, weighted by the group scales: a lane decodes its 16 codes of each
+// group once and feeds NCB pairs of MFMAs (one per 16-column block of the x block xk).
+template <int NCB>
+__device__ __forceinline__ void group_sums(const uint64_t (&nib)[kWideCG], const uint32_t (&hig)[kWideCG],
+                                           const uint32_t (&sc)[4][kWideCG / 2], int ng, const NMI_AS3 char* xk, int c,
+                                           int b, float (&bacc)[NCB][4]) {
+    const uint32_t kMaskA = 0x003f003fu;
+    const uint32_t kConstB = 0x64206420u;
+#pragma unroll
+    for (int gl = 0; gl < kWideCG; ++gl) {
+        if (gl < ng) {
+            h8 a0, a1;
+            decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
+            const int q0 = 8 * gl + 2 * b;
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                const NMI_AS3 char* xc = xk + (c + 16 * cb) * kXBlockCol;
+                const i4 x0 = *(const NMI_AS3 i4*)(xc + 16 * (q0 ^ c));
+                const i4 x1 = *(const NMI_AS3 i4*)(xc + 16 * ((q0 + 1) ^ c));
+                f4 acc = {0.f, 0.f, 0.f, 0.f};
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t w = sc[r][gl >> 1];
+                    const float sv = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
+                    bacc[cb][r] = fmaf(sv, acc[r], bacc[cb][r]);
+                }
+            }
+        }
+    }
 }
 
 template <int NCB>
@@ -536,7 +572,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
     using CH = Chunk<CG>;
     extern __shared__ __attribute__((aligned(16))) char dsmem[];
     NMI_AS3 char* smem = (NMI_AS3 char*)dsmem;
-    constexpr int XB = kWideXBuffers;
+    constexpr int XB = WideForm<NCB>::kXBuffers;
     NMI_AS3 float* finv = (NMI_AS3 float*)(smem + XB * NC * kXBlockCol); // [XB][NC] 1 / column factor
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -600,8 +636,6 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
         if (spart == 0) { finv[buf * NC + scol] = 1.0f / f; } // a power of two: exact
     };
 
-    const uint32_t kMaskA = 0x003f003fu;
-    const uint32_t kConstB = 0x64206420u;
     // waits for item j: the S - 1 younger items stay in flight, and the x loads while they are younger
     constexpr int kYoung = (S - 1) * CH::kDma;
     constexpr int kWaitItem = (kYoung & 0xf) | ((kYoung >> 4) << 14) | (0x7 << 4) | (0xf << 8);
@@ -613,6 +647,106 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
     for (int round = 0; round < ROUNDS; ++round) {
         // This round's tiles of the wave: gw + (round * MAXT + j) * nwaves, j < MAXT.
         const int tile0 = gw + round * MAXT * nwaves;
+        float tot[MAXT][NCB][4];
+#pragma unroll
+        for (int i = 0; i < MAXT; ++i) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) { tot[i][cb][r] = 0.0f; }
+            }
+        }
+        if constexpr (WideForm<NCB>::kPairs) {
+        // Blocks go in pairs: item j of pair p streams chunk 2p + (j & 1) of tile tile0 + (j / 2) *
+        // nwaves, so a tile's two chunks of the pair are consecutive items and the 128-byte lines of
+        // its high plane (64 bytes per chunk) are used whole while they are in L2. x block kb lives
+        // in buffer kb % 4: pair p computes on blocks 2p and 2p + 1 while blocks 2p + 2 and 2p + 3
+        // are staged. Slots past the last tile and blocks past the last one still issue their DMAs
+        // (they read zero or bytes that are never used), so every wait below is one fixed count.
+        constexpr int J = 2 * MAXT; // items per pair
+        static_assert(J > 2 * S, "both x blocks of the next pair land inside the pair");
+        auto issue = [&](NMI_AS3 char* st, int pp, int j) {
+            issue_item<CG>(st, pl, dl, tile0 + (j >> 1) * nwaves, 2 * pp + (j & 1), G);
+        };
+        const int npairs = (nkb + 1) / 2;
+        auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
+        xload(0);
+#pragma unroll
+        for (int j = 0; j < S; ++j) { issue(ring + j * CH::kStage, 0, j); }
+        __builtin_amdgcn_s_waitcnt(((S * CH::kDma) & 0xf) | (((S * CH::kDma) >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+        xstage(0);
+        xload(clamp_block(1));
+        __builtin_amdgcn_s_waitcnt(0); // once per round: block 1 lands behind the first items
+        xstage(1);
+#pragma unroll 1
+        for (int pp = 0; pp < npairs; ++pp) {
+            __syncthreads(); // blocks 2p, 2p + 1 are in LDS; every wave is done with blocks 2p - 2, 2p - 1
+            // x loads of block 2p + 2: issued after items 0 .. S - 1, staged at item S; those of block
+            // 2p + 3: issued at item S after items .. 2S - 1, staged at item 2S
+            xload(clamp_block(2 * pp + 2));
+            float fi[2][NCB];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) { fi[h][cb] = finv[((2 * pp + h) & (XB - 1)) * NC + c + 16 * cb]; }
+            }
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int i = j >> 1;
+                const int h = j & 1;
+                const int kb = 2 * pp + h;
+                NMI_AS3 char* st = ring + (j % S) * CH::kStage;
+                if (j < S || (j > S && j < 2 * S)) {
+                    __builtin_amdgcn_s_waitcnt(kWaitItemX);
+                } else {
+                    __builtin_amdgcn_s_waitcnt(kWaitItem);
+                }
+                if (j == S) {
+                    xstage((2 * pp + 2) & (XB - 1));
+                    xload(clamp_block(2 * pp + 3));
+                }
+                if (j == 2 * S) { xstage((2 * pp + 3) & (XB - 1)); }
+                const NMI_AS3 char* xk = smem + (kb & (XB - 1)) * NC * kXBlockCol;
+                const int ng = min(CG, G - kb * CG); // <= 0 for the block past the last
+                float bacc[NCB][4];
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) { bacc[cb][r] = 0.0f; }
+                }
+                uint64_t nib[CG];
+                uint32_t hig[CG];
+                uint32_t sc[4][CG / 2];
+#pragma unroll
+                for (int gl = 0; gl < CG; ++gl) {
+                    nib[gl] = *(const NMI_AS3 uint64_t*)(st + c * CH::kNibRow + 16 * ((2 * gl + (b >> 1)) ^ swz<CH::kNibRow>(c)) +
+                                                         8 * (b & 1));
+                    hig[gl] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + c * CH::kHighRow + 16 * (gl ^ swz<CH::kHighRow>(c)) + 4 * b);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                    for (int q = 0; q < CG / 2; ++q) {
+                        sc[r][q] = *(const NMI_AS3 uint32_t*)(st + CH::kNib + CH::kHigh + (4 * b + r) * CH::kScaleRow + 4 * q);
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0xc07f); // lgkmcnt(0): the stage is free
+                if (j + S < J) {
+                    issue(st, pp, j + S);
+                } else {
+                    issue(st, pp + 1, j + S - J);
+                }
+                group_sums<NCB>(nib, hig, sc, ng, xk, c, b, bacc);
+                if (ng > 0) {
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) { tot[i][cb][r] = fmaf(bacc[cb][r], fi[h][cb], tot[i][cb][r]); }
+                    }
+                }
+            }
+        }
+        } else {
         // Blocks go one after another: item j of block kb streams chunk kb of tile tile0 + j * nwaves.
         // x block kb lives in buffer kb % XB: block kb computes while block kb + 1 sits staged, and
         // block kb + 2 is loaded at the block's start and staged at item S, once its loads have
@@ -629,15 +763,6 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
         __builtin_amdgcn_s_waitcnt(0); // once per round: block 1 lands behind the first items
         xstage(1);
 
-        float tot[MAXT][NCB][4];
-#pragma unroll
-        for (int i = 0; i < MAXT; ++i) {
-#pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) { tot[i][cb][r] = 0.0f; }
-            }
-        }
         int buf = 0;      // kb % XB
         int buf_next = 2; // (kb + 2) % XB
 #pragma unroll 1
@@ -686,29 +811,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
                 } else {
                     issue(st, kb + 1, j + S - MAXT);
                 }
-#pragma unroll
-                for (int gl = 0; gl < CG; ++gl) {
-                    if (gl < ng) {
-                        h8 a0, a1;
-                        decode16(nib[gl], hig[gl], kMaskA, kConstB, a0, a1);
-                        const int q0 = 8 * gl + 2 * b;
-#pragma unroll
-                        for (int cb = 0; cb < NCB; ++cb) {
-                            const NMI_AS3 char* xc = xk + (c + 16 * cb) * kXBlockCol;
-                            const i4 x0 = *(const NMI_AS3 i4*)(xc + 16 * (q0 ^ c));
-                            const i4 x1 = *(const NMI_AS3 i4*)(xc + 16 * ((q0 + 1) ^ c));
-                            f4 acc = {0.f, 0.f, 0.f, 0.f};
-                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, __builtin_bit_cast(h8, x0), acc, 0, 0, 0);
-                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, __builtin_bit_cast(h8, x1), acc, 0, 0, 0);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const uint32_t w = sc[r][gl >> 1];
-                                const float sv = f16_bits_to_f32(static_cast<uint16_t>((gl & 1) ? (w >> 16) : (w & 0xffffu)));
-                                bacc[cb][r] = fmaf(sv, acc[r], bacc[cb][r]);
-                            }
-                        }
-                    }
-                }
+                group_sums<NCB>(nib, hig, sc, ng, xk, c, b, bacc);
 #pragma unroll
                 for (int cb = 0; cb < NCB; ++cb) {
 #pragma unroll
@@ -717,6 +820,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
             }
             buf = buf == XB - 1 ? 0 : buf + 1;
             buf_next = buf_next == XB - 1 ? 0 : buf_next + 1;
+        }
         }
         __builtin_amdgcn_s_waitcnt(0); // the DMAs of the items past the last block
         __syncthreads();               // LDS is free for the epilogue
