@@ -180,6 +180,27 @@ def time_graph(graph, stream, reps, warmup, prewarm_max=None, on_timed_start=Non
     return float(np.median(times)), float(np.percentile(times, 95)), times
 
 
+def time_calls(stream, fn, args) -> float:
+    """Milliseconds per call of fn: inside a captured graph of CALLS_PER_GRAPH calls, or with
+    --eager (for kernel traces) as plain launches, without a graph."""
+    if getattr(args, "eager", False):
+        from ninfer_amd.device import Event
+        for _ in range(args.warmup * CALLS_PER_GRAPH):
+            fn()
+        stream.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for _ in range(args.steps * CALLS_PER_GRAPH):
+            fn()
+        e1.record(stream)
+        stream.synchronize()
+        return e0.elapsed_ms(e1) / (args.steps * CALLS_PER_GRAPH)
+    g = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
+    ms = time_graph(g, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
+    del g
+    return ms
+
+
 def capture(stream, fn):
     from ninfer_amd.device import Graph
     g = Graph(stream)
@@ -566,10 +587,7 @@ def lm_head_bench(stream, args):
             ops.argmax(logits.tensor(), ids.tensor(), N, stream)
         out = {}
         for name, fn in (("fused", fused), ("unfused", unfused)):
-            g = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
-            ms = time_graph(g, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
-            out[f"{name}_us"] = ms * 1e3
-            del g
+            out[f"{name}_us"] = time_calls(stream, fn, args) * 1e3
         byts = lm_head_bytes(N, K, T)
         out["bytes"] = byts
         out["fused_gbs"] = byts / (out["fused_us"] * 1e-6) / 1e9
@@ -625,10 +643,7 @@ def mode_r_head_bench(stream, args, w, N: int, hidden: int) -> dict:
                                                  scal[0].tensor(), so.tensor(), scal[1].tensor(), scal[2].tensor(),
                                                  stats.tensor(), N, cfg_buf.ptr, ws_u, stream)
         for name, fn in (("fused", fused), ("unfused", unfused)):
-            g = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
-            ms = time_graph(g, stream, args.steps, args.warmup)[0] / CALLS_PER_GRAPH
-            out[f"b{B}_{name}_us"] = ms * 1e3
-            del g
+            out[f"b{B}_{name}_us"] = time_calls(stream, fn, args) * 1e3
     return out
 
 
@@ -845,7 +860,7 @@ def main():
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only c2: launch the step's kernels without a graph (for kernel traces)")
+                    help="with --only c2 or lm_head: launch the kernels without a graph (for kernel traces)")
     ap.add_argument("--only", choices=["c2", "round", "c3", "c3_bf16", "sampler", "c4", "c5", "gdn", "lm_head", "copy",
                                        "ceiling"],
                     default=None,

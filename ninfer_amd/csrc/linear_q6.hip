@@ -194,7 +194,11 @@ struct Planes {
 
 // The whole source offset rides in the range-checked voffset (soffset is not checked), so rows past
 // N and groups past G at the end of a plane read as zero instead of past the allocation.
-template <int CG>
+// KEEP_PARTIAL: the high and scale planes, of which a chunk reads part of each 128-byte line (64 and
+// 8 bytes per row at 4 groups), load with the default cache policy, so the later chunks of a row
+// find the rest of the line in L2 instead of fetching it again (the K-outer form reads a row's
+// chunks one block apart); the nibble rows are whole lines and stay non-temporal.
+template <int CG, bool KEEP_PARTIAL = false>
 __device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, const LinDma<CG>& d, int tile, int chunk,
                                            int G) {
     using C = Chunk<CG>;
@@ -204,9 +208,15 @@ __device__ __forceinline__ void issue_item(NMI_AS3 char* st, const Planes& pl, c
     const int o_s = r0 * (G * 2) + chunk * C::kScaleRow;
 #pragma unroll
     for (int q = 0; q < C::kNibDma; ++q) { dma16_nt(pl.n, st + q * 1024, d.n[q] + o_n, 0); }
+    if constexpr (KEEP_PARTIAL) {
 #pragma unroll
-    for (int q = 0; q < C::kHighDma; ++q) { dma16_nt(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
-    dma4s_nt(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
+        for (int q = 0; q < C::kHighDma; ++q) { dma16(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
+        dma4s(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
+    } else {
+#pragma unroll
+        for (int q = 0; q < C::kHighDma; ++q) { dma16_nt(pl.h, st + C::kNib + q * 1024, d.h[q] + o_h, 0); }
+        dma4s_nt(pl.s, st + C::kNib + C::kHigh, d.s + o_s, 0);
+    }
 }
 
 template <int TP, int W, int CG, bool HEAD>
@@ -666,7 +676,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
         constexpr int J = 2 * MAXT; // items per pair
         static_assert(J > 2 * S, "both x blocks of the next pair land inside the pair");
         auto issue = [&](NMI_AS3 char* st, int pp, int j) {
-            issue_item<CG>(st, pl, dl, tile0 + (j >> 1) * nwaves, 2 * pp + (j & 1), G);
+            issue_item<CG, true>(st, pl, dl, tile0 + (j >> 1) * nwaves, 2 * pp + (j & 1), G);
         };
         const int npairs = (nkb + 1) / 2;
         auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
@@ -752,7 +762,7 @@ __global__ __launch_bounds__(64 * kWideWaves) void linear_q6_wide_kernel(LinearA
         // block kb + 2 is loaded at the block's start and staged at item S, once its loads have
         // landed. Slots past the last tile and the block past the last one still issue their DMAs
         // (they read zero or bytes that are never used), so every wait below is one fixed count.
-        auto issue = [&](NMI_AS3 char* st, int kb, int j) { issue_item<CG>(st, pl, dl, tile0 + j * nwaves, kb, G); };
+        auto issue = [&](NMI_AS3 char* st, int kb, int j) { issue_item<CG, true>(st, pl, dl, tile0 + j * nwaves, kb, G); };
         auto clamp_block = [&](int kb) { return kb < nkb ? kb : nkb - 1; };
         xload(0);
 #pragma unroll
