@@ -972,10 +972,10 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
 // one workgroup (one wave per SIMD) per CU, which leaves 512 registers per lane for the doubled
 // accumulators and chunk registers. NT = 5 (D = 128): 80 query rows (a 16-node tree at group 5)
 // in one workgroup, so every key is streamed once; one wave per SIMD, the Q tile in LDS of its own.
-// One partial of the INT8 kernel: the keys [k0, kend) of sequence b (k0 a multiple of 128) for
-// this workgroup's KV head and row chunk, into partial slot `slot`.
+// One partial of the INT8 kernel: the keys [k0, kend) of sequence b (k0 a multiple of 128) for KV
+// head h and this workgroup's row chunk, into partial slot `slot`.
 template <int NT, int D, bool ONCE, bool CACHED>
-__device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, int b, int k0, int kend, int slot) {
+__device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, int b, int k0, int kend, int slot, int h) {
     constexpr int G = D / 64; // quant groups per row
     using GE = Geo<D>;
     constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
@@ -983,7 +983,6 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int h = blockIdx.y;
     const int rc = blockIdx.z;
 
     const int64_t head_code = static_cast<int64_t>(b) * a.code_seq + static_cast<int64_t>(h) * a.P * D;
@@ -1307,8 +1306,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
     // keeps one path: a second copy raises its register pressure into spills.
     if constexpr (NT <= 2) {
         if (a.B == 1) {
-            const int k0 = blockIdx.x * a.kps;
-            partial_segment<NT, D, ONCE, CACHED>(a, smem, 0, k0, k0 + a.kps, blockIdx.x);
+            // grid (KV head, split, row chunk): the dispatch order runs over the splits of every
+            // head together, so the splits past a device window shorter than the envelope plan (the
+            // last ones) are the workgroups that share a CU, not live splits of the last heads
+            const int split = blockIdx.y;
+            const int k0 = split * a.kps;
+            partial_segment<NT, D, ONCE, CACHED>(a, smem, 0, k0, k0 + a.kps, split, blockIdx.x);
             return;
         }
         // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
@@ -1317,7 +1320,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
                                                 recorder ? a.seq_table : nullptr);
         if (sr.b < 0) { return; } // a slot past the batch's last split: no partial
         const int k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
-        partial_segment<NT, D, ONCE, false>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x);
+        partial_segment<NT, D, ONCE, false>(a, smem, sr.b, k0, k0 + sr.kps, blockIdx.x, blockIdx.y);
     } else {
         int b = 0;
         int k0 = blockIdx.x * a.kps;
@@ -1331,7 +1334,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
             k0 = (static_cast<int>(blockIdx.x) - sr.first) * sr.kps;
             kend = k0 + sr.kps;
         }
-        partial_segment<NT, D, ONCE, false>(a, smem, b, k0, kend, blockIdx.x);
+        partial_segment<NT, D, ONCE, false>(a, smem, b, k0, kend, blockIdx.x, blockIdx.y);
     }
 }
 
@@ -2308,9 +2311,30 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     kps = ((kps + 127) / 128) * 128;
     kps = std::max<int64_t>(kps, kAttnMinKeysPerSplit);
     kps = off_power_of_two(kps);
+    int64_t nsplit = std::max<int64_t>(1, (static_cast<int64_t>(max_visible_keys) + kps - 1) / kps);
+    if (B == 1 && f.target == kAttnTargetWorkgroups) {
+        // Between one and 1.75 workgroups per CU, the CUs that hold two splits stream twice the
+        // keys of the others and set the layer's time. The fewest splits that fit one workgroup
+        // per CU are taken instead when their longest CU streams fewer keys (an envelope of 9,732
+        // keys at 8 KV heads: 39 splits of 256 keys = 312 workgroups become 26 of 384). Only the
+        // two-per-CU forms: their largest plan (wanted_splits() x 256 keys, at least 512
+        // workgroups) is never one of these, so attention_workspace_bound() stays exact.
+        const int64_t cus = kAttnTargetWorkgroups / 2;
+        const int64_t wgs = cols * nsplit;
+        const auto deepest = [&](int64_t n, int64_t k) { return (cols * n + cus - 1) / cus * k; };
+        if (wgs > cus && wgs * 4 < cus * 7 && cols <= cus) {
+            const int64_t per_col = cus / cols;
+            int64_t k1 = (static_cast<int64_t>(max_visible_keys) + per_col - 1) / per_col;
+            k1 = off_power_of_two(std::max<int64_t>(((k1 + 127) / 128) * 128, kAttnMinKeysPerSplit));
+            const int64_t n1 = std::max<int64_t>(1, (static_cast<int64_t>(max_visible_keys) + k1 - 1) / k1);
+            if (deepest(n1, k1) < deepest(nsplit, kps)) {
+                kps = k1;
+                nsplit = n1;
+            }
+        }
+    }
     p.keys_per_split = static_cast<int32_t>(kps);
-    p.nsplit = static_cast<int32_t>((static_cast<int64_t>(max_visible_keys) + kps - 1) / kps);
-    p.nsplit = std::max(p.nsplit, 1);
+    p.nsplit = static_cast<int32_t>(nsplit);
     p.split_slots = B == 1 ? p.nsplit : std::max(p.split_budget, B);
     // INT8 caches (the only ones offered the wide form) at head_dim 128 with one row chunk.
     p.cached_partials = B == 1 && wide_rows && D == 128 && !f.wide && p.row_chunks == 1 &&
@@ -2411,7 +2435,10 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     // One row chunk: every key is read by exactly one workgroup (non-temporal DMAs).
     const bool once = plan.row_chunks == 1;
     const int rows = plan.tokens_per_chunk * plan.G;
-    dim3 grid(plan.split_slots, c.Hkv, plan.row_chunks);
+    const dim3 grid_split_major(plan.split_slots, c.Hkv, plan.row_chunks);
+    // the INT8 batch-1 path of up to two row tiles takes (KV head, split, row chunk)
+    const dim3 grid_b1(c.Hkv, plan.split_slots, plan.row_chunks);
+    dim3 grid = grid_split_major;
 #define NMI_PARTIAL(KERNEL, NT, D)                                                                             \
     if (once) {                                                                                               \
         hipLaunchKernelGGL((KERNEL<NT, D, true>), grid, dim3(256), 0, stream, a);                            \
@@ -2431,6 +2458,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
             NMI_PARTIAL(verify_attn_partial_bf16_kernel, 2, 256)
         }
     } else if (c.D == 128) {
+        if (plan.rows_per_slot != kAttnWideRows && c.B == 1) { grid = grid_b1; }
         if (plan.rows_per_slot == kAttnWideRows) {
             NMI_PARTIAL(verify_attn_partial_kernel, 5, 128)
         } else if (plan.cached_partials && rows <= 16) {
@@ -2442,10 +2470,13 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
         } else {
             NMI_PARTIAL(verify_attn_partial_kernel, 2, 128)
         }
-    } else if (rows <= 16) {
-        NMI_PARTIAL(verify_attn_partial_kernel, 1, 256)
     } else {
-        NMI_PARTIAL(verify_attn_partial_kernel, 2, 256)
+        if (c.B == 1) { grid = grid_b1; }
+        if (rows <= 16) {
+            NMI_PARTIAL(verify_attn_partial_kernel, 1, 256)
+        } else {
+            NMI_PARTIAL(verify_attn_partial_kernel, 2, 256)
+        }
     }
 #undef NMI_PARTIAL
     check_launch("verify_attn_partial_kernel");

@@ -120,6 +120,27 @@ def test_prompt_route_workspace_sizes():
     assert ops.gqa_attention_workspace_bytes(40, 8, 128, 33, 2, 8192) == 0
 
 
+def _b1_workspace(kv_heads, head_dim, splits):
+    """Bytes of a batch-1 plan of one 32-row chunk per KV head: FP16 O [32 x head_dim] and FP32
+    (m, l) per row of every (KV head, split) slot, then the 8-byte sequence table, each 256-aligned."""
+    up = lambda n: (n + 255) // 256 * 256
+    units = kv_heads * splits
+    return up(up(up(units * 32 * head_dim * 2) + units * 2 * 32 * 4) + 8)
+
+
+def test_batch1_plan_avoids_partly_doubled_cus():
+    """Batch-1 splits of 256 keys over 40/8 heads: an envelope of 7,684 keys (C2) keeps 31 splits
+    (248 workgroups, one per CU); 9,732 keys (C2 plus the round's spare rows) would give 39 splits
+    = 312 workgroups, so that 56 CUs hold two, and is planned as 26 splits of 384 keys; 16,384
+    keys (64 splits, 512 workgroups, two per CU) and the C3 context (62 splits of 4,224 keys)
+    keep their plans."""
+    sizes = {env: ops.gqa_attention_workspace_bytes(40, 8, 128, 4, 1, env) for env in (7684, 9732, 16384, 260096)}
+    assert sizes[7684] == _b1_workspace(8, 128, 31)
+    assert sizes[9732] == _b1_workspace(8, 128, 26)
+    assert sizes[16384] == _b1_workspace(8, 128, 64)
+    assert sizes[260096] == _b1_workspace(8, 128, 62)
+
+
 def test_gqa_attention_cache_validation():
     c = _cache()
     c.quant_group = 32
