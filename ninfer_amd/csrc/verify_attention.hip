@@ -1561,10 +1561,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15;
     const int g = lane >> 4;
-    const int h = blockIdx.y;
+    // B = 1: grid (KV head, split, row chunk), as in the INT8 kernel; batches: (slot, KV head, row chunk)
+    const int h = a.B == 1 ? blockIdx.x : blockIdx.y;
     const int rc = blockIdx.z;
     int b = 0;
-    int split = blockIdx.x;
+    int split = a.B == 1 ? blockIdx.y : blockIdx.x;
     int kps = a.kps;
     int slot0 = 0;
     if (a.B > 1) {
@@ -2436,7 +2437,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     const bool once = plan.row_chunks == 1;
     const int rows = plan.tokens_per_chunk * plan.G;
     const dim3 grid_split_major(plan.split_slots, c.Hkv, plan.row_chunks);
-    // the INT8 batch-1 path of up to two row tiles takes (KV head, split, row chunk)
+    // the batch-1 paths (BF16, and INT8 of up to two row tiles) take (KV head, split, row chunk)
     const dim3 grid_b1(c.Hkv, plan.split_slots, plan.row_chunks);
     dim3 grid = grid_split_major;
 #define NMI_PARTIAL(KERNEL, NT, D)                                                                             \
@@ -2446,6 +2447,7 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
         hipLaunchKernelGGL((KERNEL<NT, D, false>), grid, dim3(256), 0, stream, a);                           \
     }
     if (c.kb != nullptr) {
+        if (c.B == 1) { grid = grid_b1; }
         if (c.D == 128) {
             if (rows <= 16) {
                 NMI_PARTIAL(verify_attn_partial_bf16_kernel, 1, 128)
