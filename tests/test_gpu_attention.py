@@ -111,6 +111,20 @@ def test_future_token_isolation(gpu):
     assert not np.array_equal(out_a[3 * per_q:], out_b[3 * per_q:])
 
 
+@pytest.mark.parametrize("L,env", [(7680, 9732), (8400, 9732), (3000, 12000), (12000, 12004)])
+def test_envelope_past_window(gpu, L, env):
+    """Batch-1 A1 under an envelope wider than the window, as in a replayed round: the plan's last
+    splits hold no keys and return (m, l) = (-inf, 0), and the head-fastest dispatch puts them last.
+    9,732 and 12,000 keys plan one workgroup per CU (26 and 32 splits of 384 keys; 256-key splits
+    would make 312 and 376 workgroups); 12,004 keys a 384-key plan over the whole window."""
+    print(f"case A1 L={L} envelope={env}", flush=True)
+    case = AttnCase([L], T=4, seed=2 * L + env, max_context=env)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, envelope=(1, env))
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
 def test_split_count_independence(gpu):
     """The same problem under two envelopes (different split plans) stays within tolerance of the
     oracle both ways; the two differ only by the FP16 rounding of probabilities, which is relative
