@@ -1034,10 +1034,13 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     // fall back to vmcnt(0) when the next chunk is unused). The first chunk's DMA starts right away;
     // the second waits until Q has landed, so Q is not queued behind every wave's two chunks at
     // launch (measured on MI355X: C2 14.60 -> 13.92 us per layer, C3, C4 and C5 unchanged).
+    // Chunks at or past the envelope hold no key any position can see, so they are not fetched (the
+    // last split of a plan usually ends past the envelope: at C2, keys 7,684-7,935).
     const int first = k0 + kChunk * wave;
-    if (first + kChunk <= a.P) { issue_chunk<D, ONCE>(ring, hb, dl, first, lane); }
+    const bool issued0 = first + kChunk <= a.P && first < a.max_keys;
+    if (issued0) { issue_chunk<D, ONCE>(ring, hb, dl, first, lane); }
     if (wave == 0) {
-        if (first + kChunk <= a.P) {
+        if (issued0) {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(GE::kDmaPerChunk));
         } else {
             __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -1046,7 +1049,9 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     // A bare barrier: the DMA'd Q and positions are in LDS once wave 0's wait returns, and a full
     // __syncthreads() would also wait for the chunk DMAs.
     __builtin_amdgcn_s_barrier();
-    if (first + kStride + kChunk <= a.P) { issue_chunk<D, ONCE>(ring + GE::kStageBytes, hb, dl, first + kStride, lane); }
+    if (first + kStride + kChunk <= a.P && first + kStride < a.max_keys) {
+        issue_chunk<D, ONCE>(ring + GE::kStageBytes, hb, dl, first + kStride, lane);
+    }
     i4 qraw[NT][G][2];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
