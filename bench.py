@@ -820,10 +820,21 @@ def round_bench(stream, args, layers, L2: int) -> dict:
     length = int(st["length"].numpy()[0])
     assert length == L2 + int(stats[1]) + int(stats[2]), "round length bookkeeping"
     assert length + T <= env[1], "rounds ran past the envelope"
-    del g, wbuf
+    # The round's parts, each timed alone as a graph: the 64 attention layers under the round's
+    # envelope at the last round's positions (replays rewrite the same 4 rows), and the fused head
+    # (replays advance the length, which nothing reads after this point).
+    g_attn = capture(stream, lambda: [ops.gqa_attention(ly.q.tensor(), ly.k.tensor(), ly.v.tensor(), st["pos"].tensor(), scale,
+                                                        ly.view, env, ws, ly.out.tensor(), stream) for ly in layers])
+    attn_ms = time_graph(g_attn, stream, args.steps, args.warmup)[0]
+    g_head = capture(stream, lambda: ops.speculative_accept_fused_head(
+        x3.tensor(), w, st["drafts"].tensor(), st["length"].tensor(), st["token"].tensor(), st["so"].tensor(),
+        st["ns"].tensor(), st["acc"].tensor(), st["stats"].tensor(), VOCAB, cfg.ptr, hws, stream))
+    head_ms = time_graph(g_head, stream, args.steps, args.warmup, prewarm_max=200)[0]
+    del g, g_attn, g_head, wbuf
     return dict(round_ms=ms, round_p95_ms=p95, rounds_counted=rounds, produced_per_round=produced,
                 tokens_per_s=produced / (ms * 1e-3), draft_agreement=0.8,
                 table_produced_per_round=drafts.table_produced, final_context=length,
+                attention_ms=attn_ms, attention_us_per_layer=attn_ms * 1e3 / len(layers), fused_head_ms=head_ms,
                 layers=len(layers), lm_head="Q6G64_F16S [248320, 5120] fused lm_head -> top-20 keys -> greedy accept")
 
 
@@ -1041,7 +1052,8 @@ def main():
             rres = round_bench(stream, args, layers, L2)
             result["round"] = rres
             log(f"round: {rres['round_ms']:.3f} ms, {rres['produced_per_round']:.2f} tokens/round, "
-                f"{rres['tokens_per_s']:.1f} tokens/s")
+                f"{rres['tokens_per_s']:.1f} tokens/s; alone: attention {rres['attention_us_per_layer']:.2f} us/layer, "
+                f"fused head {rres['fused_head_ms'] * 1e3:.1f} us")
         del layers
         if args.only == "round":
             return
