@@ -138,7 +138,9 @@ class Layer:
         self.pos = DeviceArray.from_numpy(na.I32, np.arange(L, L + T, dtype=np.int32), (T,))
         self.out = DeviceArray(na.BF16, (D, HQ, T))
         self.view = self.cache.view()
-        self.envelope = (1, max_context)
+        # every replay's window is L + T (fixed positions); the reference's launcher expects an exact
+        # window from eager calls and the replay interval from graphs (gqa_attention_decode.cu:16-19)
+        self.envelope = (L + T, max_context)
 
     def launch(self, ws, stream):
         from ninfer_amd import ops
@@ -788,7 +790,7 @@ def round_bench(stream, args, layers, L2: int) -> dict:
     cfg.upload(np.frombuffer(bytes(memoryview(na.SamplingConfig())), dtype=np.uint8))
     x3 = DeviceArray(na.BF16, (HID, T, 1), buf=x.buf)  # the verify columns of the one sequence
     hws = DeviceBuffer(ops.speculative_accept_fused_head_workspace_bytes(K, 1))
-    env = (1, L2 + T + ROUND_SPARE)
+    env = (L2 + T, L2 + T + ROUND_SPARE)  # the replays' windows: the first round's up to the spare rows
     ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(HQ, HKV, D, T, 1, env[1]))
     scale = float(np.float32(1.0 / np.sqrt(D)))
     drafts = DraftSource(tg, K, st["drafts"], agree=0.8, seed=77)

@@ -216,6 +216,7 @@ int attention_impl(const nmi_tensor* q, const nmi_tensor* k, const nmi_tensor* v
             if (static_ws && p.bytes > kStaticScratchBytes && p.rows_per_slot != kAttnRowsPerTile) {
                 p = plan_attention(s.Hq, s.Hkv, s.D, T, s.B, env.max_visible_keys, false);
             }
+            choose_b1_device_plan(p, s.B, env.min_visible_keys, c.kb == nullptr);
             return p;
         };
         if (s.T > kAttnMaxTokens) {

@@ -33,6 +33,7 @@ struct SplitPlan {
     int32_t split_budget = 0;     // B > 1: most splits per (row chunk, KV head) the device cuts the batch into
     int32_t rows_per_slot = 32;   // query rows of one partial slot: 32, or 80 (one row chunk of 5 MFMA tiles)
     bool cached_partials = false; // partials written and read through the caches (long B = 1 splits)
+    bool b1_device_plan = false;  // B = 1: the launched splits divide the device window (wide envelopes)
     size_t part_o_offset = 0;
     size_t part_ml_offset = 0;
     size_t seq_table_offset = 0; // B > 1: per sequence (first slot, split count)
@@ -54,6 +55,10 @@ inline constexpr int32_t kAttnCachedPartialKeys = 1024;
 // five 16-row tiles (one workgroup per CU) instead of several 32-row chunks that each stream every key.
 SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t B,
                          uint32_t max_visible_keys, bool wide_rows);
+
+// Marks a batch-1 plan whose splits are chosen on the device from the actual window, when the
+// envelope's shortest window would leave more than half of its splits empty (INT8, 32-row slots).
+void choose_b1_device_plan(SplitPlan& p, int32_t B, uint32_t min_visible_keys, bool int8_cache);
 
 // The largest plan_attention(Hq, Hkv, D, T, 1, keys, either form).bytes over every envelope (keys >= 1).
 size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T);

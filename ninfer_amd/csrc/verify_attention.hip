@@ -142,6 +142,29 @@ struct AttnArgs {
     float scale_log2; // softmax scale * log2(e)
 };
 
+// Keys per split of a batch-1 plan chosen on the device from the actual window, over the `launched`
+// splits of each of `cols` (row chunk, KV head) units the grid holds: the reference's device-side
+// active-split policy (src/ops/launcher/gqa_attention_decode.cu:16-20), with this build's host
+// rules (at least 256 keys, a multiple of 128, no power-of-two stride of 1,024 keys or more, and
+// one workgroup per CU where 1-1.75 would leave doubly loaded CUs). Used when the envelope is much
+// wider than the windows it admits, as for a graph replayed over many rounds: a plan sized for
+// the envelope's end would leave most splits empty and stream each window through a few.
+__device__ __forceinline__ int b1_device_kps(int window, int launched, int cols) {
+    constexpr int kCus = kAttnTargetWorkgroups / 2;
+    const auto up128 = [](int x) { return (x + 127) / 128 * 128; };
+    const auto off_pow2 = [](int k) { return (k >= 1024 && (k & (k - 1)) == 0) ? k + 128 : k; };
+    const int w = max(window, 1);
+    int kps = off_pow2(max(kAttnMinKeysPerSplit, up128((w + launched - 1) / launched)));
+    const int n = (w + kps - 1) / kps;
+    if (cols * n > kCus && cols * n * 4 < kCus * 7 && cols <= kCus) {
+        const int per_col = kCus / cols;
+        const int k1 = off_pow2(max(kAttnMinKeysPerSplit, up128((w + per_col - 1) / per_col)));
+        const int n1 = (w + k1 - 1) / k1;
+        if (n1 <= launched && (cols * n1 + kCus - 1) / kCus * k1 < (cols * n + kCus - 1) / kCus * kps) { kps = k1; }
+    }
+    return kps;
+}
+
 // ---- split plan of a batch -----------------------------------------------------------------------
 // B == 1 keeps the host plan, so the first chunk DMAs need not wait for the positions. For B > 1 the
 // sequences' windows W_i (keys visible to their last token, from the device positions) are cut into
@@ -974,7 +997,7 @@ __device__ __forceinline__ void write_partial(const State& s, char* smem, int R,
 // in one workgroup, so every key is streamed once; one wave per SIMD, the Q tile in LDS of its own.
 // One partial of the INT8 kernel: the keys [k0, kend) of sequence b (k0 a multiple of 128) for KV
 // head h and this workgroup's row chunk, into partial slot `slot`.
-template <int NT, int D, bool ONCE, bool CACHED>
+template <int NT, int D, bool ONCE, bool CACHED, bool DEV = false>
 __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, int b, int k0, int kend, int slot, int h) {
     constexpr int G = D / 64; // quant groups per row
     using GE = Geo<D>;
@@ -1035,9 +1058,12 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     // the second waits until Q has landed, so Q is not queued behind every wave's two chunks at
     // launch (measured on MI355X: C2 14.60 -> 13.92 us per layer, C3, C4 and C5 unchanged).
     // Chunks at or past the envelope hold no key any position can see, so they are not fetched (the
-    // last split of a plan usually ends past the envelope: at C2, keys 7,684-7,935).
-    const int first = k0 + kChunk * wave;
-    const bool issued0 = first + kChunk <= a.P && first < a.max_keys;
+    // last split of a plan usually ends past the envelope: at C2, keys 7,684-7,935). A batch-1 plan
+    // split on the device (the DEV instance) learns its range from the positions, so it fetches
+    // nothing before them.
+    constexpr bool dev = DEV;
+    int first = k0 + kChunk * wave;
+    const bool issued0 = !dev && first + kChunk <= a.P && first < a.max_keys;
     if (issued0) { issue_chunk<D, ONCE>(ring, hb, dl, first, lane); }
     if (wave == 0) {
         if (issued0) {
@@ -1049,6 +1075,15 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
     // A bare barrier: the DMA'd Q and positions are in LDS once wave 0's wait returns, and a full
     // __syncthreads() would also wait for the chunk DMAs.
     __builtin_amdgcn_s_barrier();
+    if constexpr (dev) {
+        // this split's keys of the device window: `slot` of the a.nsplit launched splits
+        const int win = min(max(__builtin_amdgcn_readfirstlane(pos_lds[a.T - 1]) + 1, 0), a.max_keys);
+        const int kpsd = b1_device_kps(win, a.nsplit, a.Hkv * a.row_chunks);
+        k0 = slot * kpsd;
+        kend = k0 + kpsd;
+        first = k0 + kChunk * wave;
+        if (first + kChunk <= a.P && first < a.max_keys) { issue_chunk<D, ONCE>(ring, hb, dl, first, lane); }
+    }
     if (first + kStride + kChunk <= a.P && first + kStride < a.max_keys) {
         issue_chunk<D, ONCE>(ring + GE::kStageBytes, hb, dl, first + kStride, lane);
     }
@@ -1300,7 +1335,8 @@ __device__ __forceinline__ void partial_segment(const AttnArgs& a, char* smem, i
 
 // CACHED: the batch-1 partials go out with ordinary (cached) stores; an instance of its own, launched
 // only for the plans that ask for it (kAttnCachedPartialKeys).
-template <int NT, int D, bool ONCE, bool CACHED = false>
+// DEV: a batch-1 plan split on the device (b1_device_kps of the window; up to two row tiles).
+template <int NT, int D, bool ONCE, bool CACHED = false, bool DEV = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && NT <= 2 ? 2 : 1, D == 128 && NT <= 2 ? 2 : 1))) void verify_attn_partial_kernel(AttnArgs a) {
     using GE = Geo<D>;
     constexpr int RMAX = NT == 5 ? kAttnWideRows : kAttnRowsPerTile; // rows per partial slot
@@ -1316,7 +1352,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
             // last ones) are the workgroups that share a CU, not live splits of the last heads
             const int split = blockIdx.y;
             const int k0 = split * a.kps;
-            partial_segment<NT, D, ONCE, CACHED>(a, smem, 0, k0, k0 + a.kps, split, blockIdx.x);
+            partial_segment<NT, D, ONCE, CACHED, DEV>(a, smem, 0, k0, k0 + a.kps, split, blockIdx.x);
             return;
         }
         // Slot 0 of row chunk 0, KV head 0 also records the sequences' ranges for the merge.
@@ -1929,7 +1965,8 @@ __device__ void exact_split(const MergeArgs& a, int b, int t, int qh, int k0, in
 
 // The merge of one output row's 32-dim slice over its splits in split order (running log-sum-exp),
 // recomputing each split the fast path could not hold. Whole workgroup; writes the output.
-template <int D, int RPS>
+// DEV: the partial launch split the batch-1 window on the device (b1_device_kps).
+template <int D, int RPS, bool DEV = false>
 __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0, float* xs) {
     const int tid = threadIdx.x;
     const int h = qh / a.G;
@@ -1941,6 +1978,10 @@ __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0
     int count = a.nsplit;
     int kps = a.kps;
     int* xi = reinterpret_cast<int*>(xs + D + 256 + 8 * 32);
+    if constexpr (DEV) {
+        const int win = min(max(a.positions[a.T - 1] + 1, 0), a.max_keys);
+        kps = b1_device_kps(win, a.nsplit, a.Hkv * a.row_chunks);
+    }
     if (a.B > 1) {
         first = a.seq_table[2 * b];
         count = a.seq_table[2 * b + 1];
@@ -2000,7 +2041,7 @@ __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0
 // split's (m, l) are requested before any reduction, so the block waits for memory about once.
 // The partials are written and read with non-temporal hints (each is read exactly once): 15.08 ->
 // 14.87 us per C2 layer on MI355X.
-template <int D, int RPS>
+template <int D, int RPS, bool DEV = false>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
     // Ordinary loads of the partials, whichever way they were written (measured on MI355X against
     // non-temporal loads: C3 with cached partials 98.6 -> 98.2 us, C2 13.39 -> 13.37 us per layer).
@@ -2088,7 +2129,7 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     if (redo_flag != 0 && a.kc != nullptr) {
         // the split weights are no longer needed: their LDS holds the exact path's scratch
         static_assert(D + kExactLds <= kMergeMaxSplits, "exact-path scratch exceeds the weights' LDS");
-        merge_row_exact<D, RPS>(a, b, t, qh, blockIdx.y * kMergeDims, wts);
+        merge_row_exact<D, RPS, DEV>(a, b, t, qh, blockIdx.y * kMergeDims, wts);
         return;
     }
     if (tid < kMergeDims) {
@@ -2356,6 +2397,15 @@ SplitPlan plan_attention(int32_t Hq, int32_t Hkv, int32_t D, int32_t T, int32_t 
     return p;
 }
 
+void choose_b1_device_plan(SplitPlan& p, int32_t B, uint32_t min_visible_keys, bool int8_cache) {
+    // An envelope whose shortest window would leave more than half of the plan's splits empty
+    // (a graph replayed from a short context up to a long envelope) splits each window on the
+    // device instead. The INT8 batch-1 kernel of one or two row tiles serves it; its speculative
+    // first chunks then wait for the positions.
+    const int64_t live_at_min = (std::max<int64_t>(min_visible_keys, 1) + p.keys_per_split - 1) / p.keys_per_split;
+    p.b1_device_plan = B == 1 && int8_cache && p.rows_per_slot == kAttnRowsPerTile && live_at_min * 2 < p.nsplit;
+}
+
 size_t attention_workspace_bound(int32_t Hq, int32_t Hkv, int32_t D, int32_t T) {
     // A batch-1 plan never has more than wanted_splits() splits (at least that many keys per split
     // cover any context), and it reaches that count once every split holds the minimum 256 keys.
@@ -2451,6 +2501,20 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     } else {                                                                                                  \
         hipLaunchKernelGGL((KERNEL<NT, D, false>), grid, dim3(256), 0, stream, a);                           \
     }
+    // INT8 cache, up to two row tiles: the host plan, or the batch-1 plan split on the device
+#define NMI_PARTIAL_I8(NT, D, ONCE, CACHED)                                                                   \
+    if (dev) {                                                                                                \
+        hipLaunchKernelGGL((verify_attn_partial_kernel<NT, D, ONCE, CACHED, true>), grid, dim3(256), 0, stream, a); \
+    } else {                                                                                                  \
+        hipLaunchKernelGGL((verify_attn_partial_kernel<NT, D, ONCE, CACHED>), grid, dim3(256), 0, stream, a); \
+    }
+#define NMI_PARTIAL_I8_ONCE(NT, D)                                                                            \
+    if (once) {                                                                                               \
+        NMI_PARTIAL_I8(NT, D, true, false)                                                                    \
+    } else {                                                                                                  \
+        NMI_PARTIAL_I8(NT, D, false, false)                                                                   \
+    }
+    const bool dev = plan.b1_device_plan;
     if (c.kb != nullptr) {
         if (c.B == 1) { grid = grid_b1; }
         if (c.D == 128) {
@@ -2469,22 +2533,24 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
         if (plan.rows_per_slot == kAttnWideRows) {
             NMI_PARTIAL(verify_attn_partial_kernel, 5, 128)
         } else if (plan.cached_partials && rows <= 16) {
-            hipLaunchKernelGGL((verify_attn_partial_kernel<1, 128, true, true>), grid, dim3(256), 0, stream, a);
+            NMI_PARTIAL_I8(1, 128, true, true)
         } else if (plan.cached_partials) {
-            hipLaunchKernelGGL((verify_attn_partial_kernel<2, 128, true, true>), grid, dim3(256), 0, stream, a);
+            NMI_PARTIAL_I8(2, 128, true, true)
         } else if (rows <= 16) {
-            NMI_PARTIAL(verify_attn_partial_kernel, 1, 128)
+            NMI_PARTIAL_I8_ONCE(1, 128)
         } else {
-            NMI_PARTIAL(verify_attn_partial_kernel, 2, 128)
+            NMI_PARTIAL_I8_ONCE(2, 128)
         }
     } else {
         if (c.B == 1) { grid = grid_b1; }
         if (rows <= 16) {
-            NMI_PARTIAL(verify_attn_partial_kernel, 1, 256)
+            NMI_PARTIAL_I8_ONCE(1, 256)
         } else {
-            NMI_PARTIAL(verify_attn_partial_kernel, 2, 256)
+            NMI_PARTIAL_I8_ONCE(2, 256)
         }
     }
+#undef NMI_PARTIAL_I8_ONCE
+#undef NMI_PARTIAL_I8
 #undef NMI_PARTIAL
     check_launch("verify_attn_partial_kernel");
 
@@ -2526,8 +2592,12 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<256>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128 && plan.rows_per_slot == kAttnWideRows) {
         hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    } else if (c.D == 128 && dev) {
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128) {
         hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+    } else if (dev) {
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     } else {
         hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
     }

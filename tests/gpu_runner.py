@@ -25,7 +25,9 @@ def run_attention(case, out_f32=False, mode="A1", cache=None, stream=None, envel
     v = DeviceArray.from_numpy(na.BF16, case.v_new, (D, Hkv, T, B))
     pos = DeviceArray.from_numpy(na.I32, case.positions, (T, B))
     out = DeviceArray(na.FP32 if out_f32 else na.BF16, (D, Hq, T, B))
-    env = envelope or (1, case.max_context)
+    # default: from the shortest window the case holds up to its capacity (an exact envelope when
+    # max_context is the window, as for the reference's eager calls)
+    env = envelope or (min(case.Ls) + T, case.max_context)
     ws = DeviceBuffer(ops.gqa_attention_workspace_bytes(Hq, Hkv, D, T, B, env[1]))
     ws.fill(0xFF)  # NaN bit patterns: the op may not depend on what scratch held before
     view = cache.view()

@@ -111,14 +111,33 @@ def test_future_token_isolation(gpu):
     assert not np.array_equal(out_a[3 * per_q:], out_b[3 * per_q:])
 
 
-@pytest.mark.parametrize("L,env", [(7680, 9732), (8400, 9732), (3000, 12000), (12000, 12004)])
+@pytest.mark.parametrize("L,env", [(7680, 9732), (8400, 9732), (7000, 12000), (12000, 12004)])
 def test_envelope_past_window(gpu, L, env):
-    """Batch-1 A1 under an envelope wider than the window, as in a replayed round: the plan's last
-    splits hold no keys and return (m, l) = (-inf, 0), and the head-fastest dispatch puts them last.
-    9,732 and 12,000 keys plan one workgroup per CU (26 and 32 splits of 384 keys; 256-key splits
-    would make 312 and 376 workgroups); 12,004 keys a 384-key plan over the whole window."""
-    print(f"case A1 L={L} envelope={env}", flush=True)
+    """Batch-1 A1 under an envelope wider than the window, as in a replayed round (from this window
+    up): the host plan's last splits hold no keys and return (m, l) = (-inf, 0), and the
+    head-fastest dispatch puts them last. 9,732 and 12,000 keys plan one workgroup per CU (26 and
+    32 splits of 384 keys; 256-key splits would make 312 and 376 workgroups); 12,004 keys a 384-key
+    plan over the whole window."""
+    print(f"case A1 L={L} envelope={(L + 4, env)}", flush=True)
     case = AttnCase([L], T=4, seed=2 * L + env, max_context=env)
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, envelope=(L + 4, env))
+    _check_cache(cache, expected_cache)
+    _check_out(out, ref, REL_L2_F32)
+
+
+@pytest.mark.parametrize("L,T", [(0, 4), (200, 3), (3000, 1), (7680, 4), (9000, 4), (40000, 3), (131000, 4)])
+def test_device_split_plan(gpu, L, T):
+    """Batch-1 A1 under an envelope far wider than the window (1 .. 131,076 keys), as in a graph
+    replayed from a short context up to a long one: the launched splits (61 of 2,176 keys for the
+    envelope's end) divide the window read from the device positions instead, at least 256 keys
+    each. Windows shorter than one split, 7,684 keys (31 splits of 256), 9,004 and 40,003 keys (one
+    workgroup per CU: 24 splits of 384 rather than 36 of 256, 32 of 1,280 rather than 53 of 768), a
+    window at the envelope's end (61 of 2,176), and one and two row tiles (T = 1 and 3: 5 and 15
+    rows; T = 4: 20 rows)."""
+    env = 131076
+    print(f"case A1 device plan L={L} T={T} envelope=(1, {env})", flush=True)
+    case = AttnCase([L], T=T, seed=7 * L + T, max_context=env, gen="pcg")
     expected_cache, ref = case.oracle_after_append()
     out, cache = gpu_runner.run_attention(case, out_f32=True, envelope=(1, env))
     _check_cache(cache, expected_cache)
@@ -283,7 +302,7 @@ def test_large_magnitude_groups_within_fp16_range(gpu):
 
 
 @pytest.mark.parametrize("absmax", [1e5, 1e6])
-@pytest.mark.parametrize("form", ["a1", "tree", "d256", "long"])
+@pytest.mark.parametrize("form", ["a1", "tree", "d256", "long", "wide_envelope"])
 def test_fp32_range_groups(gpu, absmax, form):
     """The reference decodes cached K/V as FP32(code) * scale (include/ninfer/ops/gqa_attention.h:30),
     and INT8-G64 scales reach 65,504, so a group's values may exceed FP16's range. Groups with an
@@ -291,9 +310,11 @@ def test_fp32_range_groups(gpu, absmax, form):
     a new token whose K/V rows the op itself quantizes at that size, against the FP64 oracle: chunks
     holding such a scale divide their K scales by a power of two (undone on the FP32 scores) and the
     wave's V scales by a running power of two (undone on O). Causal (two-tile), tree (five-tile),
-    head_dim 256 (24|4 heads) and a long context (splits of 1,024+ keys)."""
+    head_dim 256 (24|4 heads), a long context (splits of 1,024+ keys), and a window of 9,004 keys
+    under the envelope (1, 131,076), whose splits the device plans (24 of 384 keys)."""
     T, Hq, Hkv, D, L = 4, 40, 8, 128, 3000
     parents = None
+    env = None
     if form == "tree":
         T = 16
         parents = np.array(_bfs_tree(16), dtype=np.int32)
@@ -301,9 +322,11 @@ def test_fp32_range_groups(gpu, absmax, form):
         Hq, Hkv, D = 24, 4, 256
     elif form == "long":
         L = 60000
+    elif form == "wide_envelope":
+        L, env = 9000, 131076
     print(f"case fp32 range {form} absmax={absmax:g}", flush=True)
     case = AttnCase([L], T=T, Hq=Hq, Hkv=Hkv, D=D, seed=int(absmax) % 1000 + len(form), parents=parents,
-                    qstd=2e-5, gen="pcg" if L > 10000 else "splitmix")
+                    qstd=2e-5, gen="pcg" if (env or L) > 10000 else "splitmix", max_context=env)
     rng = np.random.default_rng(int(absmax) + len(form))
     G = D // 64
     big = np.float16(absmax / 127.0).view(np.uint16)
@@ -319,13 +342,14 @@ def test_fp32_range_groups(gpu, absmax, form):
         arr[per_tok:2 * per_tok] = ((x.view(np.uint32) + 0x7FFF + ((x.view(np.uint32) >> 16) & 1)) >> 16).astype(np.uint16)
     expected_cache, ref = case.oracle_after_append()
     mode = "TREE" if parents is not None else "A1"
-    out, cache = gpu_runner.run_attention(case, out_f32=True, mode=mode)
+    envelope = (1, env) if env else None
+    out, cache = gpu_runner.run_attention(case, out_f32=True, mode=mode, envelope=envelope)
     _check_cache(cache, expected_cache)
     assert np.all(np.isfinite(out))
     # The rel-L2 bars only: the reference's attention_bf16 composite is an elementwise envelope for
     # its registered activation range, and outputs here cancel next to values of 1e6 (it is printed).
     _check_out(out, ref, REL_L2_F32)
-    out16, _ = gpu_runner.run_attention(case, out_f32=False, mode=mode)
+    out16, _ = gpu_runner.run_attention(case, out_f32=False, mode=mode, envelope=envelope)
     _check_out(out16, ref, REL_L2_BF16)
 
 

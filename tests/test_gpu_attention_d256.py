@@ -87,6 +87,20 @@ def test_d256_batch_ragged(gpu):
     _check(out, ref, 1e-3)
 
 
+@pytest.mark.parametrize("L", [5000, 60000])
+def test_d256_device_split_plan(gpu, L):
+    """Batch-1 (16|2, T = 4: 32 rows) under the envelope (1, 65,540): the host plan's 103 splits of
+    640 keys divide the window read from the device positions instead (5,004 keys: 20 splits of
+    256; 60,004: 94 of 640)."""
+    env = 65540
+    print(f"case D=256 device plan L={L} envelope=(1, {env})", flush=True)
+    case = AttnCase([L], T=4, Hq=16, Hkv=2, D=256, seed=77 + L, max_context=env, gen="pcg")
+    expected_cache, ref = case.oracle_after_append()
+    out, cache = gpu_runner.run_attention(case, out_f32=True, envelope=(1, env))
+    _check_cache(cache, expected_cache)
+    _check(out, ref, 1e-3)
+
+
 def test_d256_tree(gpu):
     T = 16
     parents = np.array([-1] + [(u - 1) // 2 for u in range(1, T)], dtype=np.int32)
