@@ -113,9 +113,21 @@ __device__ __forceinline__ uint32_t fixed_u24(float u) {
     return static_cast<uint32_t>(s);
 }
 
+// W = rint(det_expf(y) * 2^40), y = fma(x, 1/T, -xmax/T). Inside det_expf's range the two scaling
+// steps and the 2^40 collapse into one exact ldexp: p * 2^k is exact when normal, and times 2^40 it
+// stays exact or overflows to inf in both forms; when p * 2^k is subnormal, both forms give a value
+// below 2^-85, which rounds to 0. Outside the range (NaN, overflow, underflow) det_expf itself runs.
 __device__ __forceinline__ uint64_t gen_weight(float x, float inv_temp, float m) {
-    const float w = det_expf(__builtin_fmaf(x, inv_temp, -m));
-    return static_cast<uint64_t>(__builtin_rintf(w * 1099511627776.0f)); // 2^40
+    const float y = __builtin_fmaf(x, inv_temp, -m);
+    float w;
+    if (det_exp_in_range(y)) {
+        int k;
+        const float p = det_exp_poly(y, &k);
+        w = __builtin_ldexpf(p, k + 40);
+    } else {
+        w = det_expf(y) * 1099511627776.0f; // 2^40
+    }
+    return static_cast<uint64_t>(__builtin_rintf(w));
 }
 
 // 16-bit ordered value of a BF16 token (the high half of the ordered-float key).
@@ -235,12 +247,16 @@ __device__ void column_scale(const GenArgs& a, int64_t cb, float* red, float* m,
 // ---- 2: coarse histogram of counts and masses ----------------------------------------------------
 // Lanes of a wave mostly fall into a few bins, so lane l adds into replica l % kCoarseReplicas; the
 // replica stride of kGenBins + 1 words puts the replicas of one bin in different LDS banks.
+// A replica word packs a bin's count (bits 52 and up) over its mass (bits 0-51), so each token costs
+// one LDS atomic: a replica sees at most kGenTile / kCoarseReplicas = 256 tokens of a tile, whose
+// weights (each at most 2^40 plus the rounding of fma(xmax, 1/T, -xmax/T)) sum below 2^49.
 constexpr int kCoarseReplicas = 16;
 constexpr int kReplicaStride = kGenBins + 1;
+constexpr int kCountShift = 52;
+static_assert(kGenTile / kCoarseReplicas <= 256, "packed replica words: count and mass fields");
 
 __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
-    __shared__ uint32_t cnt[kCoarseReplicas * kReplicaStride];
-    __shared__ uint64_t mass[kCoarseReplicas * kReplicaStride];
+    __shared__ uint64_t cm[kCoarseReplicas * kReplicaStride];
     __shared__ float red[kThreads / 64];
     const int t = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int64_t cb = static_cast<int64_t>(b) * a.ncols + c;
@@ -252,10 +268,7 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
         const uint32_t xq = in_domain ? column_ptr(a, b, a.K + 1 + i)[d] : 0u;
         a.dtab[static_cast<int64_t>(b) * a.K + i] = DraftEntry{xp | (xq << 16), in_domain ? d : -1};
     }
-    for (int i = threadIdx.x; i < kCoarseReplicas * kReplicaStride; i += kThreads) {
-        cnt[i] = 0;
-        mass[i] = 0;
-    }
+    for (int i = threadIdx.x; i < kCoarseReplicas * kReplicaStride; i += kThreads) { cm[i] = 0; }
     // The tile's tokens load while the column maximum is reduced.
     const int v0 = t * kGenTile + kPerThread * static_cast<int>(threadIdx.x);
     float x[16];
@@ -266,8 +279,8 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
     for (int e = 0; e < 16; ++e) {
         if (v0 + e < a.V) {
             const uint32_t slot = (threadIdx.x % kCoarseReplicas) * kReplicaStride + (ordered16(x[e]) >> 8);
-            atomicAdd(&cnt[slot], 1u);
-            atomicAdd(reinterpret_cast<unsigned long long*>(&mass[slot]), static_cast<unsigned long long>(gen_weight(x[e], inv_temp, m)));
+            const uint64_t add = (1ull << kCountShift) + gen_weight(x[e], inv_temp, m);
+            atomicAdd(reinterpret_cast<unsigned long long*>(&cm[slot]), static_cast<unsigned long long>(add));
         }
     }
     __syncthreads();
@@ -275,8 +288,9 @@ __global__ __launch_bounds__(kThreads) void gen_coarse_kernel(GenArgs a) {
     uint64_t ms = 0;
 #pragma unroll
     for (int r = 0; r < kCoarseReplicas; ++r) {
-        ct += cnt[r * kReplicaStride + threadIdx.x];
-        ms += mass[r * kReplicaStride + threadIdx.x];
+        const uint64_t w = cm[r * kReplicaStride + threadIdx.x];
+        ct += static_cast<uint32_t>(w >> kCountShift);
+        ms += w & ((1ull << kCountShift) - 1);
     }
     if (ct != 0) {
         atomicAdd(&a.ccount[cb * kGenBins + threadIdx.x], ct);

@@ -18,10 +18,9 @@ namespace nmi {
 // Deterministic exp: Cody-Waite reduction with ln2 split into 0x3f317200 + 0x35bfbe8e, degree-7
 // Taylor polynomial on |r| <= ln2/2 (Horner, explicit fma), 2^k applied in two normal-range steps.
 // The same algorithm runs in the CPU oracle, so results are bit-identical.
-__device__ __forceinline__ float det_expf(float x) {
-    if (!(x == x)) { return x; }
-    if (x > 88.72283935546875f) { return __builtin_inff(); }
-    if (x < -103.97208404541015625f) { return 0.0f; }
+//
+// det_exp_poly is its reduction and polynomial for x in [-103.972..., 88.722...]: e^x ~ p * 2^k.
+__device__ __forceinline__ float det_exp_poly(float x, int* k_out) {
     const float k = __builtin_rintf(x * 1.44269502162933349609375f);
     float r = __builtin_fmaf(k, -0.693145751953125f, x);
     r = __builtin_fmaf(k, -1.428606765330187045e-06f, r);
@@ -33,7 +32,20 @@ __device__ __forceinline__ float det_expf(float x) {
     p = __builtin_fmaf(p, r, 5.0000000000e-01f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const int ki = static_cast<int>(k);
+    *k_out = static_cast<int>(k);
+    return p;
+}
+
+__device__ __forceinline__ bool det_exp_in_range(float x) {
+    return x >= -103.97208404541015625f && x <= 88.72283935546875f;
+}
+
+__device__ __forceinline__ float det_expf(float x) {
+    if (!(x == x)) { return x; }
+    if (x > 88.72283935546875f) { return __builtin_inff(); }
+    if (x < -103.97208404541015625f) { return 0.0f; }
+    int ki;
+    const float p = det_exp_poly(x, &ki);
     const int k1 = ki / 2;
     const int k2 = ki - k1;
     const float s1 = __uint_as_float(static_cast<uint32_t>(k1 + 127) << 23);
