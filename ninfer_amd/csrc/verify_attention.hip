@@ -2051,13 +2051,16 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     __shared__ float red[kMergeThreads / 64];
     __shared__ float part[kMergeGroups][kMergeDims];
     __shared__ int redo_flag;
-    const int row_id = blockIdx.x; // (b, t, qh)
     if (threadIdx.x == 0) { redo_flag = 0; }
-    const int qh = row_id % a.Hq;
-    const int t = (row_id / a.Hq) % a.T;
-    const int b = row_id / (a.Hq * a.T);
-    const int h = qh / a.G;
-    const int gi = qh - h * a.G;
+    // Block x serves KV head x % Hkv (B == 1: batches use verify_attn_merge_rows_kernel). Blocks are
+    // dealt to the XCDs round-robin, and the batch-1 partial grid runs KV head fastest, so at 8 KV
+    // heads a head's partials and the blocks that merge them share an XCD and its L2.
+    const int h = static_cast<int>(blockIdx.x) % a.Hkv;
+    const int hrow = static_cast<int>(blockIdx.x) / a.Hkv; // t * G + gi
+    const int gi = hrow % a.G;
+    const int t = hrow / a.G;
+    const int b = 0;
+    const int qh = h * a.G + gi;
     const int rc = t / a.tokens_per_chunk;
     const int r = (t - rc * a.tokens_per_chunk) * a.G + gi;
     const int nsplit = a.nsplit; // B == 1 (batches use verify_attn_merge_rows_kernel)
