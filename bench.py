@@ -888,7 +888,7 @@ def main():
     ap.add_argument("--skip-long", action="store_true", help="skip the 260K-context layer")
     ap.add_argument("--skip-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only c2 or lm_head: launch the kernels without a graph (for kernel traces)")
+                    help="with --only c2, lm_head or sampler: launch the kernels without a graph (for kernel traces)")
     ap.add_argument("--only", choices=["c2", "round", "c3", "c3_bf16", "sampler", "c4", "c5", "gdn", "lm_head", "copy",
                                        "ceiling"],
                     default=None,
@@ -1069,7 +1069,12 @@ def main():
         sres = {}
         def per_call(fn):
             # Per call inside a graph of CALLS_PER_GRAPH calls (as in a captured verify step), and
-            # a one-call graph whose time includes the host's submission of the graph.
+            # a one-call graph whose time includes the host's submission of the graph. With --eager
+            # (kernel traces: rocprofv3's kernel trace of graph replays can crash the profiled
+            # process) plain launches, reported in every field.
+            if args.eager:
+                ms = time_calls(stream, fn, args)
+                return ms, ms, ms, ms
             g1 = capture(stream, fn)
             g_r = capture(stream, lambda: [fn() for _ in range(CALLS_PER_GRAPH)])
             iso, iso_p95, _ = time_graph(g1, stream, args.steps, args.warmup)
