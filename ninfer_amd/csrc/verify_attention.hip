@@ -1852,6 +1852,7 @@ constexpr int kMergeThreads = 256;
 constexpr int kMergeDims = 32;                               // output dims per block
 constexpr int kMergeGroups = kMergeThreads / kMergeDims;     // split groups per block
 constexpr int kMergePre = 8;                                 // 64 splits loaded up front
+constexpr int kMergeB1Dims = 32; // output dims per batch-1 merge block (64: C2 12.08 -> 12.35 us per layer on MI355X)
 constexpr int kMergeMaxSplits = 2048;
 
 // ---- exact recompute of a split (FP32-range decode) -------------------------------------------
@@ -2041,15 +2042,17 @@ __device__ void merge_row_exact(const MergeArgs& a, int b, int t, int qh, int d0
 // split's (m, l) are requested before any reduction, so the block waits for memory about once.
 // The partials are written and read with non-temporal hints (each is read exactly once): 15.08 ->
 // 14.87 us per C2 layer on MI355X.
-template <int D, int RPS, bool DEV = false>
+template <int D, int RPS, bool DEV = false, int DIMS = kMergeB1Dims>
 __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeArgs a) {
+    constexpr int kGroups = kMergeThreads / DIMS; // split groups per block
+    constexpr int kPre = 64 / kGroups;             // the first 64 splits' values loaded up front
     // Ordinary loads of the partials, whichever way they were written (measured on MI355X against
     // non-temporal loads: C3 with cached partials 98.6 -> 98.2 us, C2 13.39 -> 13.37 us per layer).
     const auto ld = [](const float* p) { return *p; };
     __shared__ float wts[kMergeMaxSplits];
     __shared__ float lw[kMergeMaxSplits];
     __shared__ float red[kMergeThreads / 64];
-    __shared__ float part[kMergeGroups][kMergeDims];
+    __shared__ float part[kGroups][DIMS];
     __shared__ int redo_flag;
     if (threadIdx.x == 0) { redo_flag = 0; }
     // Block x serves KV head x % Hkv (B == 1: batches use verify_attn_merge_rows_kernel). Blocks are
@@ -2071,13 +2074,13 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int sg = tid / kMergeDims;
-    const int d = blockIdx.y * kMergeDims + (tid - sg * kMergeDims);
+    const int sg = tid / DIMS;
+    const int d = blockIdx.y * DIMS + (tid - sg * DIMS);
 
-    uint32_t pre[kMergePre]; // FP16 words, converted at use
+    uint32_t pre[kPre]; // FP16 words, converted at use
 #pragma unroll
-    for (int k = 0; k < kMergePre; ++k) {
-        const int s = sg + kMergeGroups * k;
+    for (int k = 0; k < kPre; ++k) {
+        const int s = sg + kGroups * k;
         pre[k] = s < nsplit ? partial_o_word(po, static_cast<int64_t>(s) * rps * D + r * D + d) : 0u;
     }
     float M = -INFINITY;
@@ -2111,8 +2114,8 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
     float o = 0.0f;
     if (lsum > 0.0f) {
 #pragma unroll
-        for (int k = 0; k < kMergePre; ++k) {
-            const int s = sg + kMergeGroups * k;
+        for (int k = 0; k < kPre; ++k) {
+            const int s = sg + kGroups * k;
             if (s < nsplit) {
                 const float v = partial_o_half(pre[k], d);
                 redo |= wts[s] != 0.0f && !__builtin_isfinite(v);
@@ -2120,25 +2123,27 @@ __global__ __launch_bounds__(kMergeThreads) void verify_attn_merge_kernel(MergeA
             }
         }
 #pragma unroll 4
-        for (int s = sg + kMergeGroups * kMergePre; s < nsplit; s += kMergeGroups) {
+        for (int s = sg + kGroups * kPre; s < nsplit; s += kGroups) {
             const float v = partial_o_at(po, static_cast<int64_t>(s) * rps * D + r * D + d);
             redo |= wts[s] != 0.0f && !__builtin_isfinite(v);
             o = wts[s] != 0.0f ? fmaf(v, wts[s], o) : o;
         }
     }
-    part[sg][tid - sg * kMergeDims] = o;
+    part[sg][tid - sg * DIMS] = o;
     if (redo) { redo_flag = 1; }
     __syncthreads();
     if (redo_flag != 0 && a.kc != nullptr) {
         // the split weights are no longer needed: their LDS holds the exact path's scratch
         static_assert(D + kExactLds <= kMergeMaxSplits, "exact-path scratch exceeds the weights' LDS");
-        merge_row_exact<D, RPS, DEV>(a, b, t, qh, blockIdx.y * kMergeDims, wts);
+        // the exact path serves 32 dims per call
+#pragma unroll 1
+        for (int h32 = 0; h32 < DIMS / 32; ++h32) { merge_row_exact<D, RPS, DEV>(a, b, t, qh, blockIdx.y * DIMS + 32 * h32, wts); }
         return;
     }
-    if (tid < kMergeDims) {
+    if (tid < DIMS) {
         float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kMergeGroups; ++k) { acc += part[k][tid]; }
+        for (int k = 0; k < kGroups; ++k) { acc += part[k][tid]; }
         const float val = lsum > 0.0f ? acc / lsum : 0.0f;
         const int64_t oi = static_cast<int64_t>(D) * (qh + static_cast<int64_t>(a.Hq) * (t + static_cast<int64_t>(a.T) * b)) + d;
         if (a.out_f32) {
@@ -2594,15 +2599,15 @@ void launch_verify_attention(const uint16_t* q, const uint16_t* k_new, const uin
     } else if (c.B > 1) {
         hipLaunchKernelGGL(verify_attn_merge_rows_kernel<256>, rows_grid, dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128 && plan.rows_per_slot == kAttnWideRows) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnWideRows>), dim3(c.B * T * Hq, 128 / kMergeB1Dims), dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128 && dev) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 128 / kMergeB1Dims), dim3(kMergeThreads), 0, stream, mg);
     } else if (c.D == 128) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile>), dim3(c.B * T * Hq, 128 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<128, kAttnRowsPerTile>), dim3(c.B * T * Hq, 128 / kMergeB1Dims), dim3(kMergeThreads), 0, stream, mg);
     } else if (dev) {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile, true>), dim3(c.B * T * Hq, 256 / kMergeB1Dims), dim3(kMergeThreads), 0, stream, mg);
     } else {
-        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile>), dim3(c.B * T * Hq, 256 / kMergeDims), dim3(kMergeThreads), 0, stream, mg);
+        hipLaunchKernelGGL((verify_attn_merge_kernel<256, kAttnRowsPerTile>), dim3(c.B * T * Hq, 256 / kMergeB1Dims), dim3(kMergeThreads), 0, stream, mg);
     }
     check_launch("verify_attn_merge_kernel");
 }
