@@ -1852,7 +1852,7 @@ constexpr int kMergeThreads = 256;
 constexpr int kMergeDims = 32;                               // output dims per block
 constexpr int kMergeGroups = kMergeThreads / kMergeDims;     // split groups per block
 constexpr int kMergePre = 8;                                 // 64 splits loaded up front
-constexpr int kMergeB1Dims = 32; // output dims per batch-1 merge block (64: C2 12.08 -> 12.35 us per layer on MI355X)
+constexpr int kMergeB1Dims = 32; // output dims per batch-1 merge block (C2 on MI355X: 12.1 us per layer; 64: 12.35, 16: 12.47)
 constexpr int kMergeMaxSplits = 2048;
 
 // ---- exact recompute of a split (FP32-range decode) -------------------------------------------
