@@ -686,10 +686,10 @@ def gdn_bench(stream, args):
     from ninfer_amd.device import DeviceArray
     S, Hqk, Hv, C, T = GDN_S, GDN_HQK, GDN_HV, GDN_CONV, 4
     rng = np.random.default_rng(11)
+    # raw q/k, normalized by the op as in the reference's verify call
+    # (src/targets/qwen3_6/impl/runtime/text_context_impl.h:733-735, normalize_qk = true)
     q = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
-    q /= np.linalg.norm(q, axis=-1, keepdims=True)
     k = rng.uniform(-1, 1, (T, Hqk, S)).astype(np.float32)
-    k /= np.linalg.norm(k, axis=-1, keepdims=True)
     dq = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(q), (S, Hqk, T))
     dk = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(k), (S, Hqk, T))
     dv = DeviceArray.from_numpy(na.BF16, syn.f32_to_bf16_bits(rng.uniform(-1, 1, S * Hv * T)), (S, Hv, T))
@@ -711,7 +711,7 @@ def gdn_bench(stream, args):
         for ly in layers:
             ops.causal_conv1d_silu_snapshot(dx.tensor(), dw.tensor(), ly["conv"].tensor(), slot.tensor(),
                                             ly["xo"].tensor(), stream)
-            ops.gated_delta_rule_snapshot(dq.tensor(), dk.tensor(), dv.tensor(), dg.tensor(), db.tensor(), scale, False,
+            ops.gated_delta_rule_snapshot(dq.tensor(), dk.tensor(), dv.tensor(), dg.tensor(), db.tensor(), scale, True,
                                           ly["states"].tensor(), slot.tensor(), ly["out"].tensor(), stream)
     g = capture(stream, step)
     ms, p95, _ = time_graph(g, stream, args.steps, args.warmup)

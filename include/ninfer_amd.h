@@ -239,7 +239,8 @@ int nmi_speculative_accept_greedy_drafts(const nmi_tensor* target_tokens, const 
  * on the first rejection sample max(0, p_i - q_i) normalized with u_residual; if all K are
  * accepted sample column K with u_accept[K]. uniforms: u_accept FP32 [K+1(, B)],
  * u_residual FP32 [1(, B)]. Probabilities are 64-bit fixed point (bit-exact, order-free).
- * `config` is a DEVICE pointer. */
+ * Logits inside the token domain must be finite: a NaN or infinite logit leaves the column's
+ * weights, and so the decisions, unspecified. `config` is a DEVICE pointer. */
 size_t nmi_general_accept_workspace_bytes(int32_t token_domain, int32_t K, int32_t batch);
 int nmi_speculative_accept_general(const nmi_tensor* logits, const nmi_tensor* draft_logits,
                                    const nmi_tensor* drafts, const nmi_tensor* u_accept,
