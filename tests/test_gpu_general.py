@@ -99,3 +99,29 @@ def test_general_c4_shape(gpu, oracle):
     B, K, rows = 16, 3, 248320
     t, d, dr, ua, ur = _case(40, B, K, rows)
     _check(oracle, t, d, dr, ua, ur, np.arange(B, dtype=np.int32) * 1000 + 1024, rows, 0.7, 0.95)
+
+
+@pytest.mark.parametrize("top_p", [0.95, 1.0])
+def test_general_saturated_histogram(gpu, oracle, top_p):
+    """Columns whose tokens sit at the column maximum: in every tile, each replica word of the
+    coarse histogram then counts 256 tokens of the largest weight (2^40, or slightly more when
+    fma(x, 1/T, -x/T) rounds above zero at T = 0.7), the load its packed count and mass fields are
+    sized for; with top-p below 1 the nucleus cut falls inside a run of equal values. Sequence 0:
+    every token equal; sequence 1: the even ids at the maximum, the odd ids below it."""
+    B, K, rows = 2, 3, 248320
+    rng = np.random.default_rng(21)
+    t = np.empty((B, K + 1, rows), np.uint16)
+    d = np.empty((B, K, rows), np.uint16)
+    t[0] = syn.f32_to_bf16_bits(np.full(rows, 3.0, np.float32))
+    d[0] = syn.f32_to_bf16_bits(np.full(rows, 2.5, np.float32))
+    for c in range(K + 1):
+        col = np.full(rows, -1.75, np.float32)
+        col[1::2] = -1.75 - np.abs(rng.normal(0.0, 3.0, rows // 2)).astype(np.float32) - 0.125
+        t[1, c] = syn.f32_to_bf16_bits(col)
+    for c in range(K):
+        col = np.full(rows, 0.625, np.float32)
+        col[1::2] = 0.5 - np.abs(rng.normal(0.0, 2.0, rows // 2)).astype(np.float32)
+        d[1, c] = syn.f32_to_bf16_bits(col)
+    dr = rng.integers(0, rows, (B, K)).astype(np.int32)
+    u = syn.uniforms(22, B * (K + 2)).reshape(B, K + 2).astype(np.float32)
+    _check(oracle, t, d, dr, u[:, :K + 1], u[:, K + 1], np.array([5, 6], np.int32), rows, 0.7, top_p)
