@@ -1108,6 +1108,18 @@ def main():
             sres[f"mode_f_b{B}_us_per_seq"] = ms * 1e3 / B
             sres[f"mode_f_b{B}_isolated_us"] = iso * 1e3
             sres[f"mode_f_b{B}_isolated_p95_us"] = iso_p95 * 1e3
+        if not args.eager:
+            # the submission floor inside every "isolated" figure: a one-call graph of one one-thread
+            # kernel (increment of a device scalar), timed like the one-call graphs above
+            from ninfer_amd import ops as _ops
+            from ninfer_amd.device import DeviceArray as _DA
+            import ninfer_amd as _na
+            ctr = _DA.from_numpy(_na.I32, np.zeros(1, np.int32), (1,))
+            g0 = capture(stream, lambda: _ops.increment_i32_scalar(ctr.tensor(), stream))
+            floor, floor_p95, _ = time_graph(g0, stream, args.steps, args.warmup)
+            sres["graph_submit_floor_us"] = floor * 1e3
+            sres["graph_submit_floor_p95_us"] = floor_p95 * 1e3
+            del g0
         if args.only:
             log(f"sampler {sres}")
             return
