@@ -565,50 +565,82 @@ __global__ void select_hidden_kernel(const uint16_t* hidden, const int32_t* acce
 // ---- greedy tree acceptance ------------------------------------------------------------------------
 // Node u > 0 is accepted iff its parent is accepted and node_tokens[u] == target_tokens[parent];
 // the deepest accepted node wins (lowest index on ties).
-__global__ void tree_accept_kernel(const int32_t* parents, const int32_t* node_tokens,
-                                   const int32_t* target_tokens, int32_t N, int32_t* path,
-                                   int32_t* path_len, int32_t* length, int32_t* token,
-                                   int32_t* sampled_out, int32_t* num_sampled, int32_t* accepted,
-                                   int64_t* stats, int32_t stats_stride) {
+// One wave per tree: the lanes load the tree (parents, node tokens, targets), the length and the
+// statistics in one round trip; lane 0 walks the depths over LDS (node u needs its parent's depth,
+// so the walk stays sequential); the lanes then write the path, the sampled tokens and the
+// statistics.
+__global__ __launch_bounds__(64) void tree_accept_kernel(const int32_t* parents, const int32_t* node_tokens,
+                                                         const int32_t* target_tokens, int32_t N, int32_t* path,
+                                                         int32_t* path_len, int32_t* length, int32_t* token,
+                                                         int32_t* sampled_out, int32_t* num_sampled, int32_t* accepted,
+                                                         int64_t* stats, int32_t stats_stride) {
+    __shared__ int32_t spar[kMaxTreeNodes];
+    __shared__ int32_t stok[kMaxTreeNodes];
+    __shared__ int32_t stgt[kMaxTreeNodes];
+    __shared__ int32_t spath[kMaxTreeNodes];
+    __shared__ int32_t sdepth[kMaxTreeNodes];
+    __shared__ int32_t sres[2]; // best node, path length
+    static_assert(kMaxTreeNodes <= 64 && kStatsPerPositionOffset + kMaxTreeNodes <= 64, "one wave per tree");
     const int b = blockIdx.x;
-    if (threadIdx.x != 0) { return; }
+    const int lane = static_cast<int>(threadIdx.x);
     const int32_t* par = parents + static_cast<int64_t>(b) * N;
     const int32_t* tok = node_tokens + static_cast<int64_t>(b) * N;
     const int32_t* tgt = target_tokens + static_cast<int64_t>(b) * N;
     int32_t* pth = path + static_cast<int64_t>(b) * N;
     int32_t* so = sampled_out + static_cast<int64_t>(b) * N;
     int64_t* st = stats + static_cast<int64_t>(b) * stats_stride;
-    int depth[kMaxTreeNodes];
-    depth[0] = 0;
-    int best = 0;
-    for (int u = 1; u < N; ++u) {
-        depth[u] = -1;
-        const int p = par[u];
-        if (p < 0 || p >= u || depth[p] < 0) { continue; }
-        if (tok[u] != tgt[p]) { continue; }
-        depth[u] = depth[p] + 1;
-        if (depth[u] > depth[best]) { best = u; }
+    if (lane < N) {
+        spar[lane] = par[lane];
+        stok[lane] = tok[lane];
+        stgt[lane] = tgt[lane];
     }
-    const int len = depth[best] + 1;
-    int u = best;
-    for (int j = len - 1; j >= 0; --j) {
-        pth[j] = u;
-        u = par[u];
+    const int64_t st_old = lane < stats_stride ? st[lane] : 0;
+    const int32_t len_old = length[b];
+    __syncthreads();
+    if (lane == 0) {
+        int32_t* depth = sdepth;
+        depth[0] = 0;
+        int best = 0;
+        int best_depth = 0;
+        for (int u = 1; u < N; ++u) {
+            depth[u] = -1;
+            const int p = spar[u];
+            if (p < 0 || p >= u || depth[p] < 0) { continue; }
+            if (stok[u] != stgt[p]) { continue; }
+            depth[u] = depth[p] + 1;
+            if (depth[u] > best_depth) {
+                best = u;
+                best_depth = depth[u];
+            }
+        }
+        const int len = best_depth + 1;
+        int u = best;
+        for (int j = len - 1; j >= 0; --j) {
+            spath[j] = u;
+            u = spar[u];
+        }
+        sres[0] = best;
+        sres[1] = len;
     }
-    for (int j = len; j < N; ++j) { pth[j] = 0; }
+    __syncthreads();
+    const int best = sres[0];
+    const int len = sres[1];
     const int acc = len - 1;
-    for (int j = 0; j < N; ++j) { so[j] = 0; }
-    for (int j = 0; j < acc; ++j) { so[j] = tok[pth[j + 1]]; }
-    so[acc] = tgt[best];
-    path_len[b] = len;
-    num_sampled[b] = acc + 1;
-    accepted[b] = acc;
-    token[b] = tgt[best];
-    length[b] = length[b] + acc + 1;
-    st[0] += N - 1;
-    st[1] += acc;
-    st[2] += 1;
-    for (int j = 0; j < acc && kStatsPerPositionOffset + j < stats_stride; ++j) { st[kStatsPerPositionOffset + j] += 1; }
+    if (lane < N) {
+        pth[lane] = lane < len ? spath[lane] : 0;
+        so[lane] = lane < acc ? stok[spath[lane + 1]] : (lane == acc ? stgt[best] : 0);
+    }
+    if (lane == 0) {
+        path_len[b] = len;
+        num_sampled[b] = acc + 1;
+        accepted[b] = acc;
+        token[b] = stgt[best];
+        length[b] = len_old + acc + 1;
+    }
+    // stats: [0] += N - 1 drafted nodes, [1] += accepted, [2] += rounds, [4 + j] += 1 for j < acc
+    const int64_t add = lane == 0 ? N - 1 : lane == 1 ? acc : lane == 2 ? 1
+                        : (lane >= kStatsPerPositionOffset && lane - kStatsPerPositionOffset < acc) ? 1 : 0;
+    if (lane < stats_stride && add != 0) { st[lane] = st_old + add; }
 }
 
 } // namespace

@@ -357,3 +357,49 @@ def test_tree_accept_matches_oracle(gpu, oracle):
         assert list(S[b][: len(produced)]) == produced
         assert ns.numpy()[b] == len(exp) and acc.numpy()[b] == len(exp) - 1
         assert length.numpy()[b] == 1000 + len(exp)
+
+
+@pytest.mark.parametrize("N", [1, 5, 16, 32])
+def test_tree_accept_full_outputs(gpu, oracle, N):
+    """Every output of the greedy tree acceptance against the oracle's longest accepted path: the
+    path and the sampled tokens zero-padded to N, token, counts, length, and the statistics row
+    ([0] += N - 1 drafted nodes, [1] += accepted, [2] += 1 round, [4 + j] += 1 for j < accepted,
+    other entries unchanged) with a stride wider than 4 + N and nonzero starting values. Random
+    parents include malformed ones (negative, or not below the node), which the contract treats as
+    rejected."""
+    B, stride = 4, 4 + N + 3
+    rng = np.random.default_rng(100 + N)
+    parents = np.full((B, N), -1, np.int32)
+    for b in range(B):
+        for u in range(1, N):
+            r = rng.random()
+            parents[b, u] = rng.integers(0, u) if r < 0.8 else (u + rng.integers(0, 3) if r < 0.9 else -2)
+    node_tokens = rng.integers(0, 3, size=(B, N)).astype(np.int32)
+    target_tokens = rng.integers(0, 3, size=(B, N)).astype(np.int32)
+    stats0 = rng.integers(0, 50, size=(B, stride)).astype(np.int64)
+    dev = {n: DeviceArray.from_numpy(na.I32, a, (N, B)) for n, a in
+           [("p", parents), ("nt", node_tokens), ("tt", target_tokens)]}
+    path = DeviceArray.from_numpy(na.I32, np.full((B, N), 77, np.int32), (N, B))
+    so = DeviceArray.from_numpy(na.I32, np.full((B, N), 77, np.int32), (N, B))
+    plen, token, ns, acc = (DeviceArray(na.I32, (B,)) for _ in range(4))
+    length = DeviceArray.from_numpy(na.I32, np.arange(B, dtype=np.int32) * 10 + 500, (B,))
+    stats = DeviceArray.from_numpy(na.I64, stats0, (stride, B))
+    ops.tree_accept_greedy(dev["p"].tensor(), dev["nt"].tensor(), dev["tt"].tensor(), path.tensor(), plen.tensor(),
+                           length.tensor(), token.tensor(), so.tensor(), ns.tensor(), acc.tensor(), stats.tensor())
+    synchronize()
+    P, S, ST = path.numpy().reshape(B, N), so.numpy().reshape(B, N), stats.numpy().reshape(B, stride)
+    for b in range(B):
+        exp = list(oracle.tree_longest_path(parents[b], node_tokens[b], target_tokens[b]))
+        a = len(exp) - 1
+        assert list(P[b]) == exp + [0] * (N - len(exp)), b
+        produced = [int(node_tokens[b][u]) for u in exp[1:]] + [int(target_tokens[b][exp[-1]])]
+        assert list(S[b]) == produced + [0] * (N - len(produced)), b
+        assert plen.numpy()[b] == len(exp) and ns.numpy()[b] == a + 1 and acc.numpy()[b] == a
+        assert token.numpy()[b] == target_tokens[b][exp[-1]]
+        assert length.numpy()[b] == 500 + 10 * b + a + 1
+        want = stats0[b].copy()
+        want[0] += N - 1
+        want[1] += a
+        want[2] += 1
+        want[4:4 + a] += 1
+        assert list(ST[b]) == list(want), b
