@@ -451,11 +451,28 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
             __syncthreads();
             target = g_target;
         }
-        if (threadIdx.x == 0) {
-            int acc = 0;
-            while (acc < K && target[acc] == drafts[acc]) { ++acc; }
-            commit_round(drafts, K, acc, target[acc], *length, length, token, sampled_out,
-                         num_sampled, accepted, stats);
+        // One wave: every input is loaded at once, the accepted prefix is the first mismatch
+        // (ballot), and the commit (commit_round's stores, from the values read here) is written by
+        // the lanes in parallel.
+        if (wave == 0) {
+            static_assert(kMaxColumns <= 64 && kStatsPerPositionOffset + kMaxColumns <= 64, "one wave per sequence");
+            const int32_t tg = lane <= K ? target[lane] : 0;
+            const int32_t dr = lane < K ? drafts[lane] : 0;
+            const int64_t st = lane < a.stats_stride ? stats[lane] : 0;
+            const int32_t len0 = *length;
+            const uint64_t mism = __ballot(lane < K && tg != dr);
+            const int acc = mism != 0ull ? __ffsll(static_cast<long long>(mism)) - 1 : K;
+            const int32_t tstar = __shfl(tg, acc, 64);
+            if (lane <= K) { sampled_out[lane] = lane < acc ? dr : (lane == acc ? tstar : 0); }
+            if (lane == 0) {
+                *num_sampled = acc + 1;
+                *accepted = acc;
+                *token = tstar;
+                *length = len0 + acc + 1;
+            }
+            const int64_t add = lane == 0 ? K : lane == 1 ? acc : lane == 2 ? 1
+                                : (lane >= kStatsPerPositionOffset && lane - kStatsPerPositionOffset < acc) ? 1 : 0;
+            if (lane < a.stats_stride && add != 0) { stats[lane] = st + add; }
         }
         return;
     }
