@@ -452,8 +452,9 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
             target = g_target;
         }
         // One wave: every input is loaded at once, the accepted prefix is the first mismatch
-        // (ballot), and the commit (commit_round's stores, from the values read here) is written by
-        // the lanes in parallel.
+        // (ballot), and the lanes write the round's commit (src/ops/kernel/speculative_round.cuh:
+        // 145-166: drafts [0, a) then the target token, zero padded; length advances by a + 1;
+        // statistics) in parallel, from the values read here.
         if (wave == 0) {
             static_assert(kMaxColumns <= 64 && kStatsPerPositionOffset + kMaxColumns <= 64, "one wave per sequence");
             const int32_t tg = lane <= K ? target[lane] : 0;
@@ -478,6 +479,14 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
     }
 
     const int cap = candidate_cap(cfg, a.token_domain);
+    // The commit's inputs, loaded while the candidate lists merge.
+    __shared__ int32_t s_dr[kMaxColumns];
+    __shared__ int64_t s_st[64];
+    __shared__ int32_t s_len;
+    __shared__ int32_t s_res[2]; // accepted drafts, sampled token
+    if (static_cast<int>(threadIdx.x) < K) { s_dr[threadIdx.x] = drafts[threadIdx.x]; }
+    if (static_cast<int>(threadIdx.x) < 64 && static_cast<int>(threadIdx.x) < a.stats_stride) { s_st[threadIdx.x] = stats[threadIdx.x]; }
+    if (threadIdx.x == 0) { s_len = *length; }
     __shared__ uint64_t cand[4][64];
     __shared__ uint64_t top[4][kCandidateCap];
     __shared__ float e_sh[4][kCandidateCap];
@@ -522,9 +531,10 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
         wave_lds_sync();
     }
     __syncthreads();
-    if (threadIdx.x != 0) { return; }
+    if (wave != 0) { return; }
+    const int L = s_len;
+    if (lane == 0) {
     // Sequential accept: src/ops/kernel/speculative_round.cuh:337-366.
-    const int L = *length;
     int acc = 0;
     int tstar = 0;
     for (int i = 0; i <= K; ++i) {
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
         const int32_t* cidx = d_idx[i];
         const float* cprob = d_prob[i];
         if (i < K) {
-            const int dtok = drafts[i];
+            const int dtok = s_dr[i];
             float pd = 0.0f;
             for (int j = 0; j < n; ++j) {
                 if (cidx[j] == dtok) {
@@ -552,10 +562,26 @@ __global__ __launch_bounds__(256) void spec_merge_accept_kernel(SpecArgs a) {
         const float u = sampling_uniform(cfg.seed, L + K + 1, kPurposeBonus, 0u);
         tstar = pick_from_support(cidx, cprob, n, -1, u);
     }
-    commit_round(drafts, K, acc, tstar, L, length, token, sampled_out, num_sampled, accepted, stats);
-    if (cfg.token_counts != nullptr) {
-        for (int i = 0; i <= acc; ++i) { atomicAdd(&cfg.token_counts[sampled_out[i]], 1); }
+    s_res[0] = acc;
+    s_res[1] = tstar;
     }
+    wave_lds_sync();
+    // The round's commit (src/ops/kernel/speculative_round.cuh:145-166) by the lanes, from the
+    // values read at entry.
+    const int acc = s_res[0];
+    const int32_t tstar = s_res[1];
+    const int32_t out = lane < acc ? s_dr[lane] : (lane == acc ? tstar : 0);
+    if (lane <= K) { sampled_out[lane] = out; }
+    if (lane == 0) {
+        *num_sampled = acc + 1;
+        *accepted = acc;
+        *token = tstar;
+        *length = L + acc + 1;
+    }
+    const int64_t add = lane == 0 ? K : lane == 1 ? acc : lane == 2 ? 1
+                        : (lane >= kStatsPerPositionOffset && lane - kStatsPerPositionOffset < acc) ? 1 : 0;
+    if (lane < a.stats_stride && add != 0) { stats[lane] = s_st[lane] + add; }
+    if (cfg.token_counts != nullptr && lane <= acc) { atomicAdd(&cfg.token_counts[out], 1); }
 }
 
 // ---- MTP alignment ids (include/ninfer/ops/mtp_round.h:10-20) ------------------------------------

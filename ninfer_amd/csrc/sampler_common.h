@@ -123,24 +123,4 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-
-// Round commit epilogue shared by every acceptance mode (src/ops/kernel/speculative_round.cuh:
-// 145-166): drafts [0, a) then the correction/bonus token, zero padded; length advances by a + 1.
-__device__ inline void commit_round(const int32_t* drafts, int K, int a, int tstar, int L, int32_t* length,
-                                    int32_t* token, int32_t* sampled_out, int32_t* num_sampled,
-                                    int32_t* accepted, int64_t* stats) {
-    for (int i = 0; i <= K; ++i) { sampled_out[i] = 0; }
-    for (int i = 0; i < a; ++i) { sampled_out[i] = drafts[i]; }
-    sampled_out[a] = tstar;
-    const int produced = a + 1;
-    *num_sampled = produced;
-    *accepted = a;
-    *token = tstar;
-    *length = L + produced;
-    stats[0] += K;
-    stats[1] += a;
-    stats[2] += 1;
-    for (int i = 0; i < a; ++i) { stats[kStatsPerPositionOffset + i] += 1; }
-}
-
 } // namespace nmi
