@@ -567,15 +567,12 @@ __global__ __launch_bounds__(kThreads) void gen_pick_kernel(GenArgs a) {
     const int col_p = rejected >= 0 ? rejected : a.K;
     const ColDesc p = sd[col_p];
     const ColDesc q = rejected >= 0 ? sd[a.K + 1 + rejected] : p;
-    // Totals of the chosen weights (residual, or p when there is no residual mass).
+    // Totals of the chosen weights (residual, or p when there is no residual mass). The residual
+    // masses are non-negative, so their total is nonzero iff some tile's is (a block-wide OR).
     u128 rsum = 0;
 #pragma unroll
     for (int j = 0; j < kMaxDrawTilesPerThread; ++j) { rsum += rt[j]; }
-    const u128 rincl = block_scan<u128>(rejected >= 0 ? rsum : u128(0), sh);
-    __shared__ u128 rall;
-    if (tid == kThreads - 1) { rall = rincl; }
-    __syncthreads();
-    const bool use_res = rejected >= 0 && rall != 0;
+    const bool use_res = __syncthreads_or(rejected >= 0 && rsum != 0) != 0;
     u128 tt[kMaxDrawTilesPerThread];
     u128 tsum = 0;
 #pragma unroll
