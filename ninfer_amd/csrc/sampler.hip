@@ -185,6 +185,18 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
     const int col = blockIdx.y;
     const uint16_t* x = logits + static_cast<int64_t>(col) * column_stride;
     const int base = blockIdx.x * kArgmaxTile + threadIdx.x * 8;
+    int32_t* slot = out + col;
+    // The column's current holder and its key, read by thread 0 while the tile's loads are in
+    // flight. out only ever moves to a strictly larger key, so a holder read early that already
+    // beats the tile still does; a stale one makes the compare-and-swap below fail and retry.
+    int cur = -1;
+    uint64_t ck = 0;
+    const auto read_holder = [&] {
+        if (threadIdx.x == 0) {
+            cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ck = (cur >= 0 && cur < valid_rows) ? sort_key(bf16_to_f32(x[cur]), cur) : 0ull;
+        }
+    };
     uint64_t best = 0;
     if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0) {
         i4 raw[kArgmaxLoads];
@@ -193,6 +205,7 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
             const int r0 = base + u * 256 * 8;
             raw[u] = r0 + 8 <= valid_rows ? *reinterpret_cast<const i4*>(x + r0) : i4{0, 0, 0, 0};
         }
+        read_holder();
 #pragma unroll
         for (int u = 0; u < kArgmaxLoads; ++u) {
             const int r0 = base + u * 256 * 8;
@@ -210,6 +223,7 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
             }
         }
     } else {
+        read_holder();
         for (int u = 0; u < kArgmaxLoads; ++u) {
             for (int e = 0; e < 8; ++e) {
                 const int v = base + u * 256 * 8 + e;
@@ -229,15 +243,13 @@ __global__ __launch_bounds__(256) void argmax_tile_kernel(const uint16_t* logits
 #pragma unroll
     for (int w = 1; w < 4; ++w) { best = wbest[w] > best ? wbest[w] : best; }
     if (best == 0) { return; } // no row of this tile is below valid_rows
-    int32_t* slot = out + col;
-    int cur = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int mine = key_index(best);
     while (true) {
-        const uint64_t ck = (cur >= 0 && cur < valid_rows) ? sort_key(bf16_to_f32(x[cur]), cur) : 0ull;
         if (ck >= best) { break; } // keys are unique per row: the holder is at least as good
         const int seen = atomicCAS(slot, cur, mine);
         if (seen == cur) { break; }
         cur = seen;
+        ck = (cur >= 0 && cur < valid_rows) ? sort_key(bf16_to_f32(x[cur]), cur) : 0ull;
     }
 }
 
